@@ -1,0 +1,206 @@
+/*
+ * xvram_oracle.c — CPU oracle for the out-of-core FP32 SGEMM path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py load this library, and only as the checker.
+ * The product path (libxvram.so) never links, loads or calls it.
+ *
+ * Contents, each restating a reference algorithm:
+ *   - oracle_sgemm_f64 / oracle_sgemm_f64_columns: the reference's only CPU
+ *     GEMM, examples/preview-gemm/main.cpp:107-119 (FP32 inputs, FP64
+ *     accumulation, naive column/row/inner loop), generalised to the GEMM
+ *     descriptor's strided N/T operands, alpha and beta
+ *     (include/xvram/xvram.h:336-358, src/gemm/executor.cpp:166-243: alpha and
+ *     beta are rounded to FP32 first). It also accumulates
+ *     |alpha|*sum_k |a_ik|*|b_kj| + |beta*c0_ij|, the scale of the
+ *     per-element error bound.
+ *   - oracle_check_bound: counts elements violating
+ *     |C - C_ref| <= 4*K*2^-24 * (|alpha|(|A||B|)_ij + |beta*C0_ij|),
+ *     the BASELINE acceptance bound extended by the beta term; also the
+ *     reference example's own criterion 1e-4 + 2e-5*|ref| (main.cpp:116).
+ *   - oracle_pattern_*: the analytic integer pattern of the reference GEMM
+ *     bench, src/gemm_bench/pattern.cpp:207-237 (values, closed-form sums,
+ *     expected C).
+ *   - oracle_fill_uniform / oracle_fill_normal: the counter-based input
+ *     generator used for every seeded config (U[-1,1] = 2*(x>>40)*2^-24 - 1
+ *     with x = splitmix64 of the element counter; N(0, s^2) by Box-Muller in
+ *     FP64 rounded to FP32). The reference has no RNG on this path; this is
+ *     the build's own definition of "seeded inputs".
+ *
+ * Pinning (tests/test_oracle.py): pattern values/sums/expected against the
+ * reference KATs (tests/unit/gemm_pattern_tests.cpp:103-153); the SGEMM
+ * against brute-force Python loops on tiny shapes, against numpy float64
+ * matmul on medium shapes, against the analytic pattern (exact) for all four
+ * N/T combinations, and against the reference example's closed inputs
+ * (main.cpp:53-58); planted mistakes (dropped term, swapped operand, wrong
+ * beta) are shown to fail.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* A matrix in "operand" coordinates: element (r, c) lives at
+ * base[r * rs + c * cs] (elements). Column-major storage with ld and op N is
+ * rs = 1, cs = ld; op T is rs = ld, cs = 1; row-major swaps the two. */
+
+static inline double rnd_f32(double v) { return (double)(float)v; }
+
+/*
+ * C_ref(i,j) = alpha32 * sum_p a(i,p) * b(p,j) + beta32 * c0(i,j), FP64
+ * accumulation in the order p = 0..K-1 (main.cpp:111-113), for columns
+ * [j_begin, j_end). c0 may be NULL when beta == 0 (C is never read then,
+ * matching the library semantics). absab receives the bound scale.
+ */
+void oracle_sgemm_f64_columns(int64_t m, int64_t n, int64_t k, double alpha, const float* a,
+                              int64_t a_rs, int64_t a_cs, const float* b, int64_t b_rs,
+                              int64_t b_cs, double beta, const float* c0, int64_t c_rs,
+                              int64_t c_cs, double* ref, double* absab, int64_t ref_ld,
+                              int64_t j_begin, int64_t j_end, int threads) {
+  const double al = rnd_f32(alpha);
+  const double be = rnd_f32(beta);
+  (void)n;
+#ifdef _OPENMP
+  if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
+#else
+  (void)threads;
+#endif
+  for (int64_t column = j_begin; column < j_end; ++column) {
+    for (int64_t row = 0; row < m; ++row) {
+      double reference = 0.0;
+      double magnitude = 0.0;
+      for (int64_t inner = 0; inner < k; ++inner) {
+        const double x = (double)a[row * a_rs + inner * a_cs];
+        const double y = (double)b[inner * b_rs + column * b_cs];
+        reference += x * y;
+        magnitude += fabs(x) * fabs(y);
+      }
+      double value = al * reference;
+      double scale = fabs(al) * magnitude;
+      if (be != 0.0) {
+        const double old = (double)c0[row * c_rs + column * c_cs];
+        value += be * old;
+        scale += fabs(be * old);
+      }
+      const int64_t out = row + (column - j_begin) * ref_ld;
+      ref[out] = value;
+      if (absab) absab[out] = scale;
+    }
+  }
+}
+
+void oracle_sgemm_f64(int64_t m, int64_t n, int64_t k, double alpha, const float* a, int64_t a_rs,
+                      int64_t a_cs, const float* b, int64_t b_rs, int64_t b_cs, double beta,
+                      const float* c0, int64_t c_rs, int64_t c_cs, double* ref, double* absab,
+                      int threads) {
+  oracle_sgemm_f64_columns(m, n, k, alpha, a, a_rs, a_cs, b, b_rs, b_cs, beta, c0, c_rs, c_cs, ref,
+                           absab, m, 0, n, threads);
+}
+
+/*
+ * Compares an FP32 result (element (i,j) at c[i*c_rs + j*c_cs]) with the
+ * oracle. Returns the number of elements outside
+ * 4*K*2^-24*absab(i,j) (non-finite values always fail). max_err and
+ * max_ratio (error / bound) are reported through the out pointers.
+ */
+int64_t oracle_check_bound(int64_t m, int64_t n, int64_t k, const float* c, int64_t c_rs,
+                           int64_t c_cs, const double* ref, const double* absab, int64_t ref_ld,
+                           double* max_err, double* max_ratio) {
+  const double factor = 4.0 * (double)k * ldexp(1.0, -24);
+  int64_t bad = 0;
+  double worst = 0.0, worst_ratio = 0.0;
+  for (int64_t j = 0; j < n; ++j) {
+    for (int64_t i = 0; i < m; ++i) {
+      const double got = (double)c[i * c_rs + j * c_cs];
+      const double want = ref[i + j * ref_ld];
+      const double bound = factor * absab[i + j * ref_ld];
+      const double err = fabs(got - want);
+      if (!isfinite(got) || !(err <= bound)) ++bad;
+      if (isfinite(err) && err > worst) worst = err;
+      if (bound > 0.0 && isfinite(err) && err / bound > worst_ratio) worst_ratio = err / bound;
+    }
+  }
+  if (max_err) *max_err = worst;
+  if (max_ratio) *max_ratio = worst_ratio;
+  return bad;
+}
+
+/* The reference example's acceptance test: finite and
+ * |c - ref| <= 1e-4 + 2e-5*|ref| (examples/preview-gemm/main.cpp:116). */
+int64_t oracle_check_example_tolerance(int64_t m, int64_t n, const float* c, int64_t c_rs,
+                                       int64_t c_cs, const double* ref, int64_t ref_ld) {
+  int64_t bad = 0;
+  for (int64_t j = 0; j < n; ++j)
+    for (int64_t i = 0; i < m; ++i) {
+      const double got = (double)c[i * c_rs + j * c_cs];
+      const double want = ref[i + j * ref_ld];
+      if (!isfinite(got) || !(fabs(got - want) <= 1e-4 + 2e-5 * fabs(want))) ++bad;
+    }
+  return bad;
+}
+
+/* ---- analytic integer pattern (src/gemm_bench/pattern.cpp:207-237) ------ */
+
+uint64_t oracle_pattern_a(uint64_t row, uint64_t k_index) { return 1u + row % 3u + k_index % 2u; }
+
+uint64_t oracle_pattern_b(uint64_t k_index, uint64_t column) {
+  return 1u + column % 5u + k_index % 3u;
+}
+
+/* sum_p = sum (t%2), sum_q = sum (t%3), sum_pq = sum (t%2)(t%3) over t < k. */
+void oracle_pattern_sums(uint64_t k, uint64_t* sum_p, uint64_t* sum_q, uint64_t* sum_pq) {
+  static const uint64_t q_tail[3] = {0, 0, 1};
+  static const uint64_t pq_tail[6] = {0, 0, 1, 1, 1, 1};
+  *sum_p = k / 2u;
+  *sum_q = 3u * (k / 3u) + q_tail[k % 3u];
+  *sum_pq = 3u * (k / 6u) + pq_tail[k % 6u];
+}
+
+/* sum_t (a0 + t%2)(b0 + t%3) = k a0 b0 + a0 sum_q + b0 sum_p + sum_pq. */
+uint64_t oracle_pattern_expected(uint64_t row, uint64_t column, uint64_t k) {
+  const uint64_t a0 = 1u + row % 3u;
+  const uint64_t b0 = 1u + column % 5u;
+  uint64_t sp, sq, spq;
+  oracle_pattern_sums(k, &sp, &sq, &spq);
+  return k * a0 * b0 + a0 * sq + b0 * sp + spq;
+}
+
+/* ---- counter-based generator -------------------------------------------- */
+
+static inline uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+static inline uint64_t counter_bits(uint64_t seed, uint64_t index) {
+  return splitmix64(splitmix64(seed) ^ index);
+}
+
+/* out[i] = U[-1,1) for element counters first .. first+count-1. */
+void oracle_fill_uniform(float* out, uint64_t count, uint64_t seed, uint64_t first) {
+  for (uint64_t i = 0; i < count; ++i) {
+    const uint64_t x = counter_bits(seed, first + i);
+    out[i] = (float)(2.0 * (double)(x >> 40) * ldexp(1.0, -24) - 1.0);
+  }
+}
+
+/* N(0, sigma^2): Box-Muller on two counter draws (2i, 2i+1) in FP64. */
+void oracle_fill_normal(float* out, uint64_t count, uint64_t seed, uint64_t first, double sigma) {
+  const double two_pi = 6.283185307179586476925286766559;
+  for (uint64_t i = 0; i < count; ++i) {
+    const uint64_t e = first + i;
+    const uint64_t x1 = counter_bits(seed, 2u * e);
+    const uint64_t x2 = counter_bits(seed, 2u * e + 1u);
+    const double u1 = ((double)(x1 >> 11) + 1.0) * ldexp(1.0, -53); /* (0, 1] */
+    const double u2 = (double)(x2 >> 11) * ldexp(1.0, -53);         /* [0, 1) */
+    out[i] = (float)(sigma * sqrt(-2.0 * log(u1)) * cos(two_pi * u2));
+  }
+}
+
+int oracle_version(void) { return 1; }

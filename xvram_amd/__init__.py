@@ -1,0 +1,250 @@
+"""xvram_amd — MI355X-native out-of-core FP32 SGEMM behind the xVRAM v1 C ABI.
+
+The product is the native library ``lib/libxvram.so`` (C++20 host runtime +
+gfx950 FP32-MFMA kernel) whose only export is ``xvram_get_api``. This module is
+a thin Python client of that C ABI (ctypes), used by the tests and the bench the
+same way a C caller uses the function table. There is no Python or CPU
+fallback: if the native library is missing, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import numpy as np
+
+from . import abi
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(HERE, "lib")
+PRODUCT_LIB = os.path.join(LIB_DIR, "libxvram.so")
+HOSTSIM_LIB = os.path.join(LIB_DIR, "libxvram_hostsim.so")
+
+__all__ = ["Library", "Session", "Allocation", "GemmPlan", "Operation", "XvramError", "abi",
+           "load", "PRODUCT_LIB", "HOSTSIM_LIB"]
+
+
+class XvramError(RuntimeError):
+    def __init__(self, status: int, where: str, info: Optional[abi.ErrorInfo] = None):
+        self.status = status
+        self.status_name = abi.STATUS.get(status, "unknown")
+        self.where = where
+        self.info = info
+        detail = ""
+        if info is not None:
+            detail = (f" [{info.stage.decode()}/{info.operation.decode()}"
+                      f" native={info.native_name.decode()}:{info.native_code}]"
+                      f" {info.message.decode()}")
+        super().__init__(f"{where}: {self.status_name} ({status}){detail}")
+
+
+class Library:
+    """The xvram_get_api function table of one native library."""
+
+    def __init__(self, path: str = PRODUCT_LIB):
+        if not os.path.exists(path):
+            raise FileNotFoundError(
+                f"{path} is not built; run `python -m xvram_amd.build` (no fallback exists)")
+        self.path = path
+        self.dll = ctypes.CDLL(path)
+        get_api = self.dll.xvram_get_api
+        get_api.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
+        get_api.restype = ctypes.c_uint32
+        self.get_api = get_api
+        self.api = abi.ApiV1()
+        status = get_api(abi.ABI_VERSION_1, ctypes.sizeof(self.api), ctypes.byref(self.api))
+        if status != abi.SUCCESS:
+            raise XvramError(status, "xvram_get_api")
+
+    def status_name(self, status: int) -> str:
+        return self.api.status_name(status).decode()
+
+
+_loaded = {}
+
+
+def load(hostsim: bool = False) -> Library:
+    path = HOSTSIM_LIB if hostsim else PRODUCT_LIB
+    if path not in _loaded:
+        _loaded[path] = Library(path)
+    return _loaded[path]
+
+
+class Session:
+    def __init__(self, lib: Library, **config):
+        self.lib = lib
+        self.api = lib.api
+        cfg = abi.session_config_init()
+        for key, value in config.items():
+            setattr(cfg, key, value)
+        handle = ctypes.c_void_p()
+        status = self.api.session_create(ctypes.byref(cfg), ctypes.byref(handle))
+        if status != abi.SUCCESS:
+            raise XvramError(status, "session_create")
+        self.handle = handle
+        self.config = cfg
+
+    def error(self) -> abi.ErrorInfo:
+        info = abi.error_info_init()
+        self.api.session_get_error(self.handle, ctypes.byref(info))
+        return info
+
+    def check(self, status: int, where: str) -> None:
+        if status != abi.SUCCESS:
+            raise XvramError(status, where, self.error())
+
+    def telemetry(self) -> abi.SessionTelemetry:
+        t = abi.telemetry_init()
+        self.check(self.api.session_get_telemetry(self.handle, ctypes.byref(t)), "telemetry")
+        return t
+
+    def allocation(self, size: int, alignment: int = 0, flags: int = 0) -> "Allocation":
+        return Allocation(self, size, alignment, flags)
+
+    def drain(self, timeout_ms: int = abi.TIMEOUT_INFINITE) -> None:
+        self.check(self.api.session_drain(self.handle, timeout_ms), "session_drain")
+
+    def close(self, timeout_ms: int = abi.TIMEOUT_INFINITE) -> None:
+        if self.handle:
+            self.check(self.api.session_close(self.handle, timeout_ms), "session_close")
+
+    def release(self) -> None:
+        if self.handle:
+            self.api.session_release(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        try:
+            self.close()
+        finally:
+            self.release()
+
+
+class Allocation:
+    def __init__(self, session: Session, size: int, alignment: int = 0, flags: int = 0):
+        self.session = session
+        desc = abi.allocation_desc_init(size)
+        desc.alignment_bytes = alignment
+        desc.flags = flags
+        handle = ctypes.c_void_p()
+        session.check(session.api.allocation_create(session.handle, ctypes.byref(desc),
+                                                    ctypes.byref(handle)), "allocation_create")
+        self.handle = handle
+        self.size = size
+
+    def info(self) -> abi.AllocationInfo:
+        out = abi.AllocationInfo()
+        out.struct_size = ctypes.sizeof(out)
+        self.session.check(self.session.api.allocation_get_info(self.handle, ctypes.byref(out)),
+                           "allocation_get_info")
+        return out
+
+    def write(self, data, offset: int = 0) -> None:
+        arr = np.ascontiguousarray(data)
+        self.session.check(self.session.api.allocation_write(
+            self.handle, offset, arr.ctypes.data_as(ctypes.c_void_p), arr.nbytes),
+            "allocation_write")
+
+    def read_into(self, out: np.ndarray, offset: int = 0) -> np.ndarray:
+        assert out.flags.c_contiguous
+        self.session.check(self.session.api.allocation_read(
+            self.handle, offset, out.ctypes.data_as(ctypes.c_void_p), out.nbytes),
+            "allocation_read")
+        return out
+
+    def read(self, nbytes: Optional[int] = None, offset: int = 0, dtype=np.uint8) -> np.ndarray:
+        nbytes = self.size - offset if nbytes is None else nbytes
+        out = np.empty(nbytes // np.dtype(dtype).itemsize, dtype=dtype)
+        return self.read_into(out, offset)
+
+    def release(self) -> None:
+        if self.handle:
+            self.session.check(self.session.api.allocation_release(self.handle),
+                               "allocation_release")
+            self.handle = None
+
+
+def matrix(allocation: Allocation, rows: int, columns: int, ld: int,
+           layout: int = abi.COLUMN_MAJOR, offset: int = 0,
+           data_type: int = abi.DATA_FP32) -> abi.Matrix:
+    m = abi.matrix_init()
+    m.allocation = allocation.handle.value if allocation is not None else None
+    m.rows, m.columns, m.leading_dimension = rows, columns, ld
+    m.layout = layout
+    m.offset_bytes = offset
+    m.data_type = data_type
+    return m
+
+
+class Operation:
+    def __init__(self, session: Session, handle: ctypes.c_void_p):
+        self.session = session
+        self.handle = handle
+
+    def poll(self) -> abi.OperationInfo:
+        info = abi.operation_info_init()
+        self.session.check(self.session.api.operation_poll(self.handle, ctypes.byref(info)),
+                           "operation_poll")
+        return info
+
+    def wait(self, timeout_ms: int = abi.TIMEOUT_INFINITE):
+        info = abi.operation_info_init()
+        status = self.session.api.operation_wait(self.handle, timeout_ms, ctypes.byref(info))
+        return status, info
+
+    def cancel(self) -> int:
+        return self.session.api.operation_cancel(self.handle)
+
+    def error(self) -> abi.ErrorInfo:
+        info = abi.error_info_init()
+        self.session.api.operation_get_error(self.handle, ctypes.byref(info))
+        return info
+
+    def release(self) -> None:
+        if self.handle:
+            self.session.api.operation_release(self.handle)
+            self.handle = None
+
+
+class GemmPlan:
+    def __init__(self, session: Session, a: abi.Matrix, b: abi.Matrix, c: abi.Matrix,
+                 op_a: int = abi.OP_N, op_b: int = abi.OP_N, alpha: float = 1.0,
+                 beta: float = 0.0, compute_mode: int = abi.COMPUTE_AUTO,
+                 tile_hints=(0, 0, 0), deadline_ms: int = 0):
+        self.session = session
+        desc = abi.gemm_desc_init()
+        desc.a, desc.b, desc.c = a, b, c
+        desc.operation_a, desc.operation_b = op_a, op_b
+        desc.alpha, desc.beta = alpha, beta
+        desc.compute_mode = compute_mode
+        desc.tile_m_hint, desc.tile_n_hint, desc.tile_k_hint = tile_hints
+        desc.deadline_ms = deadline_ms
+        self.desc = desc
+        handle = ctypes.c_void_p()
+        session.check(session.api.gemm_plan_create(session.handle, ctypes.byref(desc),
+                                                   ctypes.byref(handle)), "gemm_plan_create")
+        self.handle = handle
+
+    def info(self) -> abi.GemmPlanInfo:
+        out = abi.plan_info_init()
+        self.session.check(self.session.api.gemm_plan_get_info(self.handle, ctypes.byref(out)),
+                           "gemm_plan_get_info")
+        return out
+
+    def execute(self, timeout_ms: int = abi.TIMEOUT_INFINITE) -> None:
+        self.session.check(self.session.api.gemm_execute(self.handle, timeout_ms), "gemm_execute")
+
+    def submit(self) -> Operation:
+        handle = ctypes.c_void_p()
+        self.session.check(self.session.api.gemm_submit(self.handle, ctypes.byref(handle)),
+                           "gemm_submit")
+        return Operation(self.session, handle)
+
+    def release(self) -> None:
+        if self.handle:
+            self.session.api.gemm_plan_release(self.handle)
+            self.handle = None

@@ -1,0 +1,93 @@
+"""Builds the native libraries in-tree.
+
+  lib/libxvram.so          the product: C++20 host runtime + gfx950 HIP kernel,
+                           exporting only ``xvram_get_api@@XVRAM_0.1``;
+  lib/libxvram_hostsim.so  the same host runtime over a host-memory device
+                           simulation, for CPU-only tests (never used on the
+                           product path).
+
+Run ``python -m xvram_amd.build`` (or ``__graft_entry__.build()``).
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+OBJ = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "lib")
+INCLUDE = os.path.join(ROOT, "include")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+ARCH = "gfx950"
+
+HOST_SOURCES = ["api.cpp", "session.cpp", "runtime.cpp", "gemm.cpp"]
+COMMON_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-fvisibility=hidden", "-DXVRAM_BUILDING_LIBRARY",
+                f"-I{INCLUDE}", f"-I{CSRC}", "-Wall", "-Wextra", "-Wno-unused-parameter"]
+# Packed-FP32 instructions are disabled for every HIP compile.
+HIP_FLAGS = ["-std=c++20", "-O3", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature",
+             "-Xclang", "-packed-fp32-ops", f"-I{CSRC}", f"-I{INCLUDE}"]
+
+
+def _run(cmd):
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(" ".join(cmd) + "\n" + proc.stdout)
+        raise RuntimeError(f"build step failed: {cmd[0]} {cmd[-1]}")
+    return proc.stdout
+
+
+def _compile_host(src, obj, extra):
+    _run(["g++", *COMMON_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
+    return obj
+
+
+def build(hostsim: bool = True, product: bool = True, verbose: bool = True) -> None:
+    os.makedirs(OBJ, exist_ok=True)
+    os.makedirs(LIB, exist_ok=True)
+    jobs = []
+    with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as pool:
+        if product:
+            hip_flags = [f"-I{ROCM}/include", "-D__HIP_PLATFORM_AMD__"]
+            for src in HOST_SOURCES + ["device_hip.cpp"]:
+                jobs.append(pool.submit(_compile_host, src,
+                                        os.path.join(OBJ, "hip_" + src.replace(".cpp", ".o")),
+                                        hip_flags))
+            jobs.append(pool.submit(_run, [HIPCC, *HIP_FLAGS, "-c",
+                                           os.path.join(CSRC, "sgemm_mfma.hip"), "-o",
+                                           os.path.join(OBJ, "sgemm_mfma.o")]))
+        if hostsim:
+            for src in HOST_SOURCES + ["device_hostsim.cpp"]:
+                jobs.append(pool.submit(_compile_host, src,
+                                        os.path.join(OBJ, "sim_" + src.replace(".cpp", ".o")),
+                                        ["-DXVRAM_HOSTSIM"]))
+        for j in jobs:
+            j.result()
+    if product:
+        objs = [os.path.join(OBJ, "hip_" + s.replace(".cpp", ".o"))
+                for s in HOST_SOURCES + ["device_hip.cpp"]] + [os.path.join(OBJ, "sgemm_mfma.o")]
+        out = os.path.join(LIB, "libxvram.so")
+        _run([HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", out + ".tmp", *objs,
+              f"-Wl,--version-script={os.path.join(CSRC, 'exports.map')}", "-Wl,--no-undefined",
+              f"-L{ROCM}/lib", "-lamdhip64", "-lpthread"])
+        os.replace(out + ".tmp", out)
+        if verbose:
+            print(f"built {out}")
+    if hostsim:
+        objs = [os.path.join(OBJ, "sim_" + s.replace(".cpp", ".o"))
+                for s in HOST_SOURCES + ["device_hostsim.cpp"]]
+        out = os.path.join(LIB, "libxvram_hostsim.so")
+        _run(["g++", "-shared", "-o", out + ".tmp", *objs,
+              f"-Wl,--version-script={os.path.join(CSRC, 'exports_hostsim.map')}",
+              "-Wl,--no-undefined", "-lpthread"])
+        os.replace(out + ".tmp", out)
+        if verbose:
+            print(f"built {out}")
+
+
+if __name__ == "__main__":
+    build()

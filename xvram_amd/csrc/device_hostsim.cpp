@@ -1,0 +1,322 @@
+// device_hostsim.cpp — host-memory simulation of the device layer.
+//
+// TEST FIXTURE: linked only into libxvram_hostsim.so, which tests/ load to
+// exercise the ABI boundary, session worker, panel cache, schedule and
+// accounting on machines without a GPU (the reference does the same with its
+// FakeCuda driver, tests/unit/residency_executor_fake_tests.cpp:128-1165).
+// The product library libxvram.so never contains this file.
+//
+// Simulation rules: every call completes synchronously; a reserved VA range is
+// backed by host memory so mapped frames are ordinary pointers; accesses to
+// unmapped frames are detected and fail the call; the tile "kernel" is a
+// plain loop with the SgemmLaunch semantics (beta == 0 never reads C).
+// Faults can be injected per call site (xvram_hostsim_inject), and the
+// reported device memory can be set (xvram_hostsim_set_memory).
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "device.hpp"
+
+namespace xvram {
+namespace {
+
+enum Site {
+  kInit, kMemInfo, kVaReserve, kVaFree, kMemCreate, kMemRelease, kMemMap, kMemUnmap, kSetAccess,
+  kHostAlloc, kStreamCreate, kEventCreate, kEventRecord, kEventQuery, kEventSync, kCopyH2D,
+  kCopyD2H, kLaunch, kSiteCount
+};
+
+constexpr int kSimFault = 9001;      // injected failure
+constexpr int kSimBadAccess = 9002;  // access to an unmapped or unknown address
+constexpr int kSimOutOfMemory = 2;   // same value as hipErrorOutOfMemory
+
+struct Injection {
+  long skip = -1; // calls to let through before failing; -1 = disabled
+  bool persistent = false;
+};
+
+struct SimState {
+  std::mutex mutex;
+  Injection sites[kSiteCount];
+  uint64_t free_bytes = 16ull << 30;
+  uint64_t total_bytes = 16ull << 30;
+  uint64_t kernel_launches = 0;
+} g_sim;
+
+int fault(Site site) {
+  std::lock_guard<std::mutex> lock(g_sim.mutex);
+  Injection& inj = g_sim.sites[site];
+  if (inj.skip < 0) return 0;
+  if (inj.skip > 0) {
+    --inj.skip;
+    return 0;
+  }
+  if (!inj.persistent) inj.skip = -1;
+  return kSimFault;
+}
+
+class HostSimDevice final : public Device {
+public:
+  ~HostSimDevice() override {
+    for (auto& r : reservations_) std::free(reinterpret_cast<void*>(r.first));
+  }
+
+  int init(int ordinal) override {
+    if (int f = fault(kInit)) return f;
+    return ordinal == 0 ? 0 : 101; // hipErrorInvalidDevice
+  }
+  int driver_version(int* version) override {
+    *version = 0;
+    return 0;
+  }
+  int mem_info(uint64_t* free_bytes, uint64_t* total_bytes) override {
+    if (int f = fault(kMemInfo)) return f;
+    std::lock_guard<std::mutex> lock(g_sim.mutex);
+    *free_bytes = g_sim.free_bytes;
+    *total_bytes = g_sim.total_bytes;
+    return 0;
+  }
+  int granularity(uint64_t* minimum, uint64_t* recommended) override {
+    *minimum = 4096;
+    *recommended = 4096;
+    return 0;
+  }
+
+  int va_reserve(uint64_t bytes, uint64_t alignment, uint64_t* address) override {
+    if (int f = fault(kVaReserve)) return f;
+    const uint64_t align = alignment < 4096 ? 4096 : alignment;
+    void* p = std::aligned_alloc(align, (bytes + align - 1) / align * align);
+    if (p == nullptr) return kSimOutOfMemory;
+    reservations_[reinterpret_cast<uint64_t>(p)] = bytes;
+    *address = reinterpret_cast<uint64_t>(p);
+    return 0;
+  }
+  int va_free(uint64_t address, uint64_t bytes) override {
+    if (int f = fault(kVaFree)) return f;
+    auto it = reservations_.find(address);
+    if (it == reservations_.end() || it->second != bytes) return kSimBadAccess;
+    for (auto& m : mappings_)
+      if (m.first >= address && m.first < address + bytes) return kSimBadAccess; // still mapped
+    std::free(reinterpret_cast<void*>(address));
+    reservations_.erase(it);
+    return 0;
+  }
+  int mem_create(uint64_t bytes, uint64_t* handle) override {
+    if (int f = fault(kMemCreate)) return f;
+    std::lock_guard<std::mutex> lock(g_sim.mutex);
+    if (bytes > g_sim.free_bytes) return kSimOutOfMemory;
+    g_sim.free_bytes -= bytes;
+    *handle = ++next_handle_;
+    handles_[*handle] = bytes;
+    return 0;
+  }
+  int mem_release(uint64_t handle) override {
+    if (int f = fault(kMemRelease)) return f;
+    auto it = handles_.find(handle);
+    if (it == handles_.end()) return kSimBadAccess;
+    for (auto& m : mappings_)
+      if (m.second.handle == handle) return kSimBadAccess; // still mapped
+    std::lock_guard<std::mutex> lock(g_sim.mutex);
+    g_sim.free_bytes += it->second;
+    handles_.erase(it);
+    return 0;
+  }
+  int mem_map(uint64_t address, uint64_t bytes, uint64_t handle) override {
+    if (int f = fault(kMemMap)) return f;
+    if (!handles_.count(handle) || handles_[handle] != bytes || !inside_reservation(address, bytes))
+      return kSimBadAccess;
+    if (mappings_.count(address)) return kSimBadAccess;
+    mappings_[address] = Mapping{bytes, handle, false};
+    return 0;
+  }
+  int mem_unmap(uint64_t address, uint64_t bytes) override {
+    if (int f = fault(kMemUnmap)) return f;
+    auto it = mappings_.find(address);
+    if (it == mappings_.end() || it->second.bytes != bytes) return kSimBadAccess;
+    // Scribble over the frame so a stale read after unmapping is visible.
+    std::memset(reinterpret_cast<void*>(address), 0xFF, bytes);
+    mappings_.erase(it);
+    return 0;
+  }
+  int set_access(uint64_t address, uint64_t bytes) override {
+    if (int f = fault(kSetAccess)) return f;
+    uint64_t covered = 0;
+    for (auto& m : mappings_) {
+      if (m.first >= address && m.first + m.second.bytes <= address + bytes) {
+        m.second.accessible = true;
+        covered += m.second.bytes;
+      }
+    }
+    return covered == bytes ? 0 : kSimBadAccess;
+  }
+
+  int host_alloc(uint64_t bytes, void** pointer) override {
+    if (int f = fault(kHostAlloc)) return f;
+    *pointer = std::aligned_alloc(4096, (bytes + 4095) / 4096 * 4096);
+    return *pointer ? 0 : kSimOutOfMemory;
+  }
+  int host_free(void* pointer) override {
+    std::free(pointer);
+    return 0;
+  }
+
+  int stream_create(Stream* stream) override {
+    if (int f = fault(kStreamCreate)) return f;
+    *stream = reinterpret_cast<Stream>(++next_object_);
+    return 0;
+  }
+  int stream_destroy(Stream) override { return 0; }
+  int stream_sync(Stream) override { return 0; }
+  int event_create(Event* event) override {
+    if (int f = fault(kEventCreate)) return f;
+    *event = reinterpret_cast<Event>(++next_object_);
+    return 0;
+  }
+  int event_destroy(Event) override { return 0; }
+  int event_record(Event, Stream) override { return fault(kEventRecord); }
+  int event_query(Event) override { return fault(kEventQuery); }
+  int event_sync(Event) override { return fault(kEventSync); }
+  int event_elapsed_ms(float* ms, Event, Event) override {
+    *ms = 0.f;
+    return 0;
+  }
+  int stream_wait_event(Stream, Event) override { return 0; }
+
+  int copy_h2d_2d(uint64_t dst, uint64_t dst_pitch, const void* src, uint64_t src_pitch,
+                  uint64_t width, uint64_t height, Stream) override {
+    if (int f = fault(kCopyH2D)) return f;
+    if (!accessible(dst, dst_pitch * (height - 1) + width)) return kSimBadAccess;
+    for (uint64_t r = 0; r < height; ++r)
+      std::memcpy(reinterpret_cast<char*>(dst + r * dst_pitch),
+                  static_cast<const char*>(src) + r * src_pitch, width);
+    return 0;
+  }
+  int copy_d2h_2d(void* dst, uint64_t dst_pitch, uint64_t src, uint64_t src_pitch, uint64_t width,
+                  uint64_t height, Stream) override {
+    if (int f = fault(kCopyD2H)) return f;
+    if (!accessible(src, src_pitch * (height - 1) + width)) return kSimBadAccess;
+    for (uint64_t r = 0; r < height; ++r)
+      std::memcpy(static_cast<char*>(dst) + r * dst_pitch,
+                  reinterpret_cast<const char*>(src + r * src_pitch), width);
+    return 0;
+  }
+  int fill_zero(uint64_t dst, uint64_t bytes, Stream) override {
+    if (!accessible(dst, bytes)) return kSimBadAccess;
+    std::memset(reinterpret_cast<void*>(dst), 0, bytes);
+    return 0;
+  }
+
+  int launch_sgemm(const kernels::SgemmLaunch& l, Stream) override {
+    if (int f = fault(kLaunch)) return f;
+    const auto span = [](int64_t rows, int64_t cols, int64_t ld) {
+      return static_cast<uint64_t>(((cols - 1) * ld + rows) * 4);
+    };
+    const int64_t a_rows = l.a_kcontig ? l.k : l.m, a_cols = l.a_kcontig ? l.m : l.k;
+    const int64_t b_rows = l.b_ncontig ? l.n : l.k, b_cols = l.b_ncontig ? l.k : l.n;
+    if (!accessible(reinterpret_cast<uint64_t>(l.a), span(a_rows, a_cols, l.lda)) ||
+        !accessible(reinterpret_cast<uint64_t>(l.b), span(b_rows, b_cols, l.ldb)) ||
+        !accessible(reinterpret_cast<uint64_t>(l.c), span(l.m, l.n, l.ldc)))
+      return kSimBadAccess;
+    for (int64_t j = 0; j < l.n; ++j) {
+      for (int64_t i = 0; i < l.m; ++i) {
+        float acc = 0.f;
+        for (int64_t p = 0; p < l.k; ++p) {
+          const float x = l.a_kcontig ? l.a[p + i * l.lda] : l.a[i + p * l.lda];
+          const float y = l.b_ncontig ? l.b[j + p * l.ldb] : l.b[p + j * l.ldb];
+          acc += x * y;
+        }
+        float& out = l.c[i + j * l.ldc];
+        out = l.beta != 0.f ? l.alpha * acc + l.beta * out : l.alpha * acc;
+      }
+    }
+    std::lock_guard<std::mutex> lock(g_sim.mutex);
+    ++g_sim.kernel_launches;
+    return 0;
+  }
+
+  const char* error_name(int code) override {
+    switch (code) {
+    case kSimFault: return "hostsimInjectedFault";
+    case kSimBadAccess: return "hostsimBadAccess";
+    case kSimOutOfMemory: return "hipErrorOutOfMemory";
+    case 101: return "hipErrorInvalidDevice";
+    default: return "hostsimError";
+    }
+  }
+  bool simulated() const override { return true; }
+
+private:
+  struct Mapping {
+    uint64_t bytes;
+    uint64_t handle;
+    bool accessible;
+  };
+
+  bool inside_reservation(uint64_t address, uint64_t bytes) const {
+    for (auto& r : reservations_)
+      if (address >= r.first && address + bytes <= r.first + r.second) return true;
+    return false;
+  }
+  // Every byte of [address, address+bytes) must lie in mapped, accessible frames.
+  bool accessible(uint64_t address, uint64_t bytes) const {
+    uint64_t cursor = address;
+    const uint64_t end = address + bytes;
+    while (cursor < end) {
+      auto it = mappings_.upper_bound(cursor);
+      if (it == mappings_.begin()) return false;
+      --it;
+      if (!it->second.accessible || cursor >= it->first + it->second.bytes) return false;
+      cursor = it->first + it->second.bytes;
+    }
+    return true;
+  }
+
+  std::map<uint64_t, uint64_t> reservations_;
+  std::map<uint64_t, uint64_t> handles_;
+  std::map<uint64_t, Mapping> mappings_;
+  uint64_t next_handle_ = 0;
+  uint64_t next_object_ = 0x1000;
+};
+
+} // namespace
+
+std::unique_ptr<Device> make_device() { return std::make_unique<HostSimDevice>(); }
+
+} // namespace xvram
+
+// Test-only controls exported by libxvram_hostsim.so.
+extern "C" __attribute__((visibility("default"))) int xvram_hostsim_inject(int site, long skip,
+                                                                           int persistent) {
+  using namespace xvram;
+  if (site < 0 || site >= kSiteCount) return -1;
+  std::lock_guard<std::mutex> lock(g_sim.mutex);
+  g_sim.sites[site].skip = skip;
+  g_sim.sites[site].persistent = persistent != 0;
+  return 0;
+}
+
+extern "C" __attribute__((visibility("default"))) void xvram_hostsim_reset() {
+  using namespace xvram;
+  std::lock_guard<std::mutex> lock(g_sim.mutex);
+  for (auto& s : g_sim.sites) s = Injection{};
+  g_sim.free_bytes = g_sim.total_bytes = 16ull << 30;
+  g_sim.kernel_launches = 0;
+}
+
+extern "C" __attribute__((visibility("default"))) void xvram_hostsim_set_memory(uint64_t free_b,
+                                                                                uint64_t total_b) {
+  using namespace xvram;
+  std::lock_guard<std::mutex> lock(g_sim.mutex);
+  g_sim.free_bytes = free_b;
+  g_sim.total_bytes = total_b;
+}
+
+extern "C" __attribute__((visibility("default"))) uint64_t xvram_hostsim_kernel_launches() {
+  using namespace xvram;
+  std::lock_guard<std::mutex> lock(g_sim.mutex);
+  return g_sim.kernel_launches;
+}

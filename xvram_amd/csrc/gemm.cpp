@@ -1,0 +1,563 @@
+// gemm.cpp — validation, panel planning and pipelined execution of one GEMM.
+#include "gemm.hpp"
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <deque>
+
+namespace xvram {
+
+namespace {
+
+uint64_t element_bytes(uint32_t type) {
+  switch (type) {
+  case XVRAM_DATA_FP16:
+  case XVRAM_DATA_BF16: return 2;
+  case XVRAM_DATA_FP32: return 4;
+  case XVRAM_DATA_FP64: return 8;
+  default: return 0;
+  }
+}
+
+enum class Compute { strict_fp32, fast_tf32, fp64, invalid };
+
+// Compute-mode resolution of the reference session (src/sdk/runtime.cpp:119-135).
+Compute resolve_compute(uint32_t mode, uint32_t a_type) {
+  switch (mode) {
+  case XVRAM_COMPUTE_AUTO:
+    if (a_type == XVRAM_DATA_FP64) return Compute::fp64;
+    if (a_type == XVRAM_DATA_FP16 || a_type == XVRAM_DATA_BF16) return Compute::strict_fp32;
+    return Compute::fast_tf32;
+  case XVRAM_COMPUTE_FP32_STRICT: return Compute::strict_fp32;
+  case XVRAM_COMPUTE_FP32_TF32: return Compute::fast_tf32;
+  case XVRAM_COMPUTE_FP64: return Compute::fp64;
+  default: return Compute::invalid;
+  }
+}
+
+struct Bounds {
+  uint64_t begin = 0, end = 0;
+};
+
+// Per-operand checks in the reference's order (planner.cpp:50-100).
+ProblemError validate_matrix(const MatrixSpec& mx) {
+  if (mx.allocation_id == 0 || mx.allocation_bytes == 0) return ProblemError::invalid_allocation;
+  if (mx.layout != XVRAM_MATRIX_ROW_MAJOR && mx.layout != XVRAM_MATRIX_COLUMN_MAJOR)
+    return ProblemError::invalid_layout;
+  const uint64_t eb = element_bytes(mx.data_type);
+  if (eb == 0) return ProblemError::invalid_element_type;
+  if (mx.rows == 0 || mx.columns == 0) return ProblemError::zero_dimension;
+  const bool row = mx.layout == XVRAM_MATRIX_ROW_MAJOR;
+  const uint64_t required_ld = row ? mx.columns : mx.rows;
+  if (mx.leading_dimension < required_ld) return ProblemError::leading_dimension_too_small;
+  if (mx.leading_dimension > static_cast<uint64_t>(INT_MAX))
+    return ProblemError::integer_limit_exceeded;
+  const uint64_t major = row ? mx.rows : mx.columns;
+  const uint64_t minor = row ? mx.columns : mx.rows;
+  uint64_t last_major = 0, last = 0, bytes = 0, end = 0;
+  if (!checked_mul(major - 1, mx.leading_dimension, last_major))
+    return ProblemError::storage_overflow;
+  if (!checked_add(last_major, minor - 1, last) || !checked_add(last, 1, last))
+    return ProblemError::storage_overflow;
+  if (!checked_mul(last, eb, bytes) || !checked_add(mx.offset_bytes, bytes, end))
+    return ProblemError::storage_overflow;
+  if (mx.offset_bytes >= mx.allocation_bytes || end > mx.allocation_bytes)
+    return ProblemError::storage_out_of_bounds;
+  return ProblemError::none;
+}
+
+bool matrix_bounds(const MatrixSpec& mx, Bounds& out) {
+  const uint64_t eb = element_bytes(mx.data_type);
+  if (eb == 0 || mx.rows == 0 || mx.columns == 0) return false;
+  const bool row = mx.layout == XVRAM_MATRIX_ROW_MAJOR;
+  const uint64_t major = row ? mx.rows : mx.columns;
+  const uint64_t minor = row ? mx.columns : mx.rows;
+  uint64_t elements = 0, bytes = 0, end = 0;
+  if (!checked_mul(major - 1, mx.leading_dimension, elements) ||
+      !checked_add(elements, minor, elements) || !checked_mul(elements, eb, bytes) ||
+      !checked_add(mx.offset_bytes, bytes, end))
+    return false;
+  out = Bounds{mx.offset_bytes, end};
+  return true;
+}
+
+uint64_t isqrt(uint64_t v) {
+  uint64_t r = static_cast<uint64_t>(std::sqrt(static_cast<double>(v)));
+  while (r * r > v) --r;
+  while ((r + 1) * (r + 1) <= v) ++r;
+  return r;
+}
+
+// Geometry of one panel of an operand: x runs along the stored (contiguous)
+// dimension, y along lines.
+struct PanelGeom {
+  uint64_t x0, xn, y0, yn;
+};
+
+PanelKey panel_key(const CanonOperand& op, const PanelGeom& g) {
+  PanelKey key;
+  key.allocation_id = op.allocation_id;
+  key.offset = op.base + (g.x0 + g.y0 * op.ld) * 4;
+  key.width = g.xn * 4;
+  key.height = g.yn;
+  key.pitch = op.ld * 4;
+  return key;
+}
+
+uint64_t packed_ld(const PanelGeom& g) { return round_up(g.xn, 4); }
+uint64_t panel_bytes(uint64_t x_extent, uint64_t lines) { return round_up(x_extent, 4) * 4 * lines; }
+
+// Panel of A' rows [i0, i0+h), k [p0, p0+w).
+PanelGeom a_geom(const CanonOperand& a, uint64_t i0, uint64_t h, uint64_t p0, uint64_t w) {
+  return a.transposed ? PanelGeom{p0, w, i0, h} : PanelGeom{i0, h, p0, w};
+}
+// Panel of B' k [p0, p0+w), columns [j0, j0+g).
+PanelGeom b_geom(const CanonOperand& b, uint64_t p0, uint64_t w, uint64_t j0, uint64_t g) {
+  return b.transposed ? PanelGeom{j0, g, p0, w} : PanelGeom{p0, w, j0, g};
+}
+PanelGeom c_geom(uint64_t i0, uint64_t h, uint64_t j0, uint64_t g) { return PanelGeom{i0, h, j0, g}; }
+
+uint64_t a_panel_bytes(const CanonProblem& p, uint64_t h, uint64_t w) {
+  return p.a.transposed ? panel_bytes(w, h) : panel_bytes(h, w);
+}
+uint64_t b_panel_bytes(const CanonProblem& p, uint64_t w, uint64_t g) {
+  return p.b.transposed ? panel_bytes(g, w) : panel_bytes(w, g);
+}
+uint64_t c_panel_bytes(uint64_t h, uint64_t g) { return panel_bytes(h, g); }
+
+} // namespace
+
+const char* problem_error_name(ProblemError error) {
+  switch (error) {
+  case ProblemError::none: return "none";
+  case ProblemError::zero_dimension: return "zero_dimension";
+  case ProblemError::invalid_allocation: return "invalid_allocation";
+  case ProblemError::invalid_layout: return "invalid_layout";
+  case ProblemError::invalid_operation: return "invalid_operation";
+  case ProblemError::invalid_element_type: return "invalid_element_type";
+  case ProblemError::invalid_compute_mode: return "invalid_compute_mode";
+  case ProblemError::dimension_mismatch: return "dimension_mismatch";
+  case ProblemError::leading_dimension_too_small: return "leading_dimension_too_small";
+  case ProblemError::storage_overflow: return "storage_overflow";
+  case ProblemError::storage_out_of_bounds: return "storage_out_of_bounds";
+  case ProblemError::unsupported_type_combination: return "unsupported_type_combination";
+  case ProblemError::output_aliases_input: return "output_aliases_input";
+  case ProblemError::integer_limit_exceeded: return "integer_limit_exceeded";
+  }
+  return "invalid";
+}
+
+void problem_dims(const GemmSpec& s, uint64_t& m, uint64_t& n, uint64_t& k) {
+  const bool ta = s.operation_a == XVRAM_MATRIX_OP_T;
+  const bool tb = s.operation_b == XVRAM_MATRIX_OP_T;
+  m = ta ? s.a.columns : s.a.rows;
+  k = ta ? s.a.rows : s.a.columns;
+  n = tb ? s.b.rows : s.b.columns;
+}
+
+// GEMM problem validity, rule for rule as the reference's validate_problem
+// (src/gemm/planner.cpp:785-859), including which rule reports first.
+ProblemError validate_problem(const GemmSpec& s, char* operand) {
+  char dummy = 0;
+  char& who = operand ? *operand : dummy;
+  who = 0;
+  uint64_t m, n, k;
+  problem_dims(s, m, n, k);
+  if (m == 0 || n == 0 || k == 0) return ProblemError::zero_dimension;
+  if (s.operation_a != XVRAM_MATRIX_OP_N && s.operation_a != XVRAM_MATRIX_OP_T) {
+    who = 'A';
+    return ProblemError::invalid_operation;
+  }
+  if (s.operation_b != XVRAM_MATRIX_OP_N && s.operation_b != XVRAM_MATRIX_OP_T) {
+    who = 'B';
+    return ProblemError::invalid_operation;
+  }
+  const Compute compute = resolve_compute(s.compute_mode, s.a.data_type);
+  if (compute == Compute::invalid) return ProblemError::invalid_compute_mode;
+  const MatrixSpec* mats[3] = {&s.a, &s.b, &s.c};
+  const char names[3] = {'A', 'B', 'C'};
+  for (int i = 0; i < 3; ++i) {
+    const ProblemError e = validate_matrix(*mats[i]);
+    if (e != ProblemError::none) {
+      who = names[i];
+      return e;
+    }
+  }
+  if ((s.a.allocation_id == s.b.allocation_id && s.a.allocation_bytes != s.b.allocation_bytes) ||
+      (s.a.allocation_id == s.c.allocation_id && s.a.allocation_bytes != s.c.allocation_bytes) ||
+      (s.b.allocation_id == s.c.allocation_id && s.b.allocation_bytes != s.c.allocation_bytes))
+    return ProblemError::invalid_allocation;
+  const bool tb = s.operation_b == XVRAM_MATRIX_OP_T;
+  const uint64_t b_rows = tb ? s.b.columns : s.b.rows;
+  const uint64_t b_cols = tb ? s.b.rows : s.b.columns;
+  if (b_rows != k || b_cols != n || s.c.rows != m || s.c.columns != n)
+    return ProblemError::dimension_mismatch;
+  if (s.a.data_type != s.b.data_type) return ProblemError::unsupported_type_combination;
+  bool supported = false;
+  switch (s.a.data_type) {
+  case XVRAM_DATA_FP16:
+  case XVRAM_DATA_BF16:
+    supported = (s.c.data_type == s.a.data_type || s.c.data_type == XVRAM_DATA_FP32) &&
+                compute == Compute::strict_fp32;
+    break;
+  case XVRAM_DATA_FP32:
+    supported = s.c.data_type == XVRAM_DATA_FP32 &&
+                (compute == Compute::strict_fp32 || compute == Compute::fast_tf32);
+    break;
+  case XVRAM_DATA_FP64:
+    supported = s.c.data_type == XVRAM_DATA_FP64 && compute == Compute::fp64;
+    break;
+  }
+  if (!supported) return ProblemError::unsupported_type_combination;
+  Bounds ab, bb, cb;
+  if (!matrix_bounds(s.a, ab) || !matrix_bounds(s.b, bb) || !matrix_bounds(s.c, cb))
+    return ProblemError::storage_overflow;
+  const auto overlaps = [](const Bounds& l, const Bounds& r) {
+    return l.begin < r.end && r.begin < l.end;
+  };
+  if ((s.a.allocation_id == s.c.allocation_id && overlaps(ab, cb)) ||
+      (s.b.allocation_id == s.c.allocation_id && overlaps(bb, cb))) {
+    who = 'C';
+    return ProblemError::output_aliases_input;
+  }
+  return ProblemError::none;
+}
+
+// Reduces the problem to column-major C. A matrix stored row-major is the
+// column-major storage of its transpose, so each operand's effective
+// operation is op XOR (layout == row-major); a row-major C is handled as
+// C^T = op(B)^T op(A)^T (the operand swap of src/gemm/executor.cpp:191-209).
+CanonProblem canonicalize(const GemmSpec& s) {
+  CanonProblem p;
+  uint64_t m, n, k;
+  problem_dims(s, m, n, k);
+  const bool eop_a = (s.operation_a == XVRAM_MATRIX_OP_T) != (s.a.layout == XVRAM_MATRIX_ROW_MAJOR);
+  const bool eop_b = (s.operation_b == XVRAM_MATRIX_OP_T) != (s.b.layout == XVRAM_MATRIX_ROW_MAJOR);
+  const auto operand = [](const MatrixSpec& mx, bool transposed) {
+    CanonOperand o;
+    o.allocation_id = mx.allocation_id;
+    o.base = mx.offset_bytes;
+    o.ld = mx.leading_dimension;
+    o.transposed = transposed;
+    return o;
+  };
+  p.alpha = static_cast<float>(s.alpha);
+  p.beta = static_cast<float>(s.beta);
+  p.k = k;
+  p.c = operand(s.c, false);
+  if (s.c.layout == XVRAM_MATRIX_COLUMN_MAJOR) {
+    p.m = m;
+    p.n = n;
+    p.a = operand(s.a, eop_a);
+    p.b = operand(s.b, eop_b);
+  } else {
+    p.swapped = true;
+    p.m = n;
+    p.n = m;
+    p.a = operand(s.b, !eop_b);
+    p.b = operand(s.a, !eop_a);
+  }
+  return p;
+}
+
+// Panel planning. Tiles are sized so that each A, B and C panel fits one
+// frame; C blocks (block_m x block_n tiles) stay resident across the whole K
+// loop while A and B panels stream through the remaining frames, and the block
+// shape minimises the scheduled H2D traffic
+//   ceil(tiles_m/block_m)*|B| + ceil(tiles_n/block_n)*|A| (+|C| if beta != 0).
+Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t frame_count,
+                     uint32_t prefetch_distance, GemmPlanData& out) {
+  out = GemmPlanData{};
+  CanonProblem p = canonicalize(spec);
+  out.problem = p;
+  if (frame_count < 3)
+    return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "gemm", "make_plan",
+                      "working_set_too_large: fewer than three cache frames");
+  const uint64_t F = frame_bytes;
+  uint64_t tm, tn, bk;
+  const bool hinted = spec.tile_m_hint || spec.tile_n_hint || spec.tile_k_hint;
+  if (!hinted && a_panel_bytes(p, p.m, p.k) <= F && b_panel_bytes(p, p.k, p.n) <= F &&
+      c_panel_bytes(p.m, p.n) <= F) {
+    tm = p.m;
+    tn = p.n;
+    bk = p.k;
+  } else {
+    uint64_t s = isqrt(F / 4);
+    s = s >= 256 ? s / 256 * 256 : std::max<uint64_t>(16, s / 16 * 16);
+    tm = std::min(p.m, s);
+    tn = std::min(p.n, s);
+    bk = std::min(p.k, s);
+    // Hints are given for the caller's m/n (swapped when C is row-major).
+    const uint64_t hm = p.swapped ? spec.tile_n_hint : spec.tile_m_hint;
+    const uint64_t hn = p.swapped ? spec.tile_m_hint : spec.tile_n_hint;
+    if (hm) tm = std::min(p.m, hm);
+    if (hn) tn = std::min(p.n, hn);
+    if (spec.tile_k_hint) bk = std::min(p.k, spec.tile_k_hint);
+    const auto fits = [&](uint64_t a, uint64_t b, uint64_t c) {
+      return a_panel_bytes(p, a, c) <= F && b_panel_bytes(p, c, b) <= F && c_panel_bytes(a, b) <= F;
+    };
+    // Shrink the largest extent until every panel fits a frame.
+    while (!fits(tm, tn, bk)) {
+      uint64_t* largest = &tm;
+      if (tn > *largest) largest = &tn;
+      if (bk > *largest) largest = &bk;
+      if (*largest <= 16) {
+        return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "gemm", "make_plan",
+                          "working_set_too_large: no tile fits one cache frame");
+      }
+      *largest = std::max<uint64_t>(16, *largest / 2 / 16 * 16);
+    }
+    // Grow extents the problem did not clamp while the panels still fit.
+    if (!hinted) {
+      bool grew = true;
+      while (grew) {
+        grew = false;
+        if (bk < p.k && fits(tm, tn, std::min(p.k, bk * 2))) {
+          bk = std::min(p.k, bk * 2);
+          grew = true;
+        }
+        if (tm < p.m && fits(std::min(p.m, tm * 2), tn, bk)) {
+          tm = std::min(p.m, tm * 2);
+          grew = true;
+        }
+        if (tn < p.n && fits(tm, std::min(p.n, tn * 2), bk)) {
+          tn = std::min(p.n, tn * 2);
+          grew = true;
+        }
+      }
+    }
+  }
+  out.tm = tm;
+  out.tn = tn;
+  out.bk = bk;
+  out.tiles_m = ceil_div(p.m, tm);
+  out.tiles_n = ceil_div(p.n, tn);
+  out.panels_k = ceil_div(p.k, bk);
+
+  // Lookahead: launches whose panels are acquired (and pinned) before they are
+  // enqueued, so copies run ahead of compute. At most 3 frames per launch are
+  // pinned, so keep 3*(lookahead+1) below the frame count.
+  uint32_t lookahead = std::max<uint32_t>(2, 2 * prefetch_distance);
+  lookahead = static_cast<uint32_t>(
+      std::min<uint64_t>(lookahead, frame_count >= 6 ? frame_count / 3 - 1 : 0));
+
+  const uint64_t a_bytes = p.m * p.k * 4, b_bytes = p.k * p.n * 4, c_bytes = p.m * p.n * 4;
+  uint64_t best_gm = 1, best_gn = 1, best_h2d = UINT64_MAX;
+  for (uint64_t gm = 1; gm <= out.tiles_m; ++gm) {
+    for (uint64_t gn = 1; gn <= out.tiles_n; ++gn) {
+      const uint64_t need = gm * gn + gm + gn + 2ull * lookahead;
+      if (need > frame_count && !(gm == 1 && gn == 1)) continue;
+      const uint64_t h2d = ceil_div(out.tiles_m, gm) * b_bytes +
+                           ceil_div(out.tiles_n, gn) * a_bytes + (p.beta != 0.f ? c_bytes : 0);
+      if (h2d < best_h2d || (h2d == best_h2d && gm * gn > best_gm * best_gn)) {
+        best_h2d = h2d;
+        best_gm = gm;
+        best_gn = gn;
+      }
+    }
+  }
+  out.block_m = best_gm;
+  out.block_n = best_gn;
+  if (best_gm * best_gn + best_gm + best_gn + 2ull * lookahead > frame_count) {
+    // Only the 1 x 1 block is possible: shrink the lookahead to fit.
+    const uint64_t spare = frame_count > 3 ? frame_count - 3 : 0;
+    lookahead = static_cast<uint32_t>(std::min<uint64_t>(lookahead, spare / 3));
+  }
+  out.lookahead = lookahead;
+  out.h2d_bytes_planned = best_h2d;
+  out.d2h_bytes_planned = c_bytes;
+
+  // Launch order: blocks in a serpentine; K panels alternate direction from
+  // block to block so the panels loaded last are the first needed next; inside
+  // a K panel, tiles row by row so each A panel serves consecutive launches.
+  const uint64_t blocks_m = ceil_div(out.tiles_m, best_gm);
+  const uint64_t blocks_n = ceil_div(out.tiles_n, best_gn);
+  uint64_t total = 0;
+  if (!checked_mul(out.tiles_m, out.tiles_n, total) || !checked_mul(total, out.panels_k, total) ||
+      total > 100000000ull)
+    return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "gemm", "make_plan", "too_many_tiles");
+  out.launches.reserve(total);
+  uint64_t block_seq = 0;
+  for (uint64_t bi = 0; bi < blocks_m; ++bi) {
+    for (uint64_t s = 0; s < blocks_n; ++s, ++block_seq) {
+      const uint64_t bj = (bi % 2 == 0) ? s : blocks_n - 1 - s;
+      const uint64_t i_begin = bi * best_gm, i_end = std::min(out.tiles_m, i_begin + best_gm);
+      const uint64_t j_begin = bj * best_gn, j_end = std::min(out.tiles_n, j_begin + best_gn);
+      const bool forward = block_seq % 2 == 0;
+      for (uint64_t q = 0; q < out.panels_k; ++q) {
+        const uint64_t kp = forward ? q : out.panels_k - 1 - q;
+        for (uint64_t i = i_begin; i < i_end; ++i) {
+          for (uint64_t j = j_begin; j < j_end; ++j) {
+            TileLaunch l;
+            l.ti = static_cast<uint32_t>(i);
+            l.tj = static_cast<uint32_t>(j);
+            l.kp = static_cast<uint32_t>(kp);
+            l.first_panel = q == 0;
+            l.last_panel = q + 1 == out.panels_k;
+            out.launches.push_back(l);
+          }
+        }
+      }
+    }
+  }
+  return {};
+}
+
+namespace {
+
+struct Acquired {
+  size_t index = 0;
+  Frame* a = nullptr;
+  Frame* b = nullptr;
+  Frame* c = nullptr;
+};
+
+struct LaunchGeom {
+  uint64_t i0, h, j0, g, p0, w;
+};
+
+LaunchGeom launch_geom(const GemmPlanData& plan, const TileLaunch& l) {
+  const CanonProblem& p = plan.problem;
+  LaunchGeom g;
+  g.i0 = l.ti * plan.tm;
+  g.h = std::min(plan.tm, p.m - g.i0);
+  g.j0 = l.tj * plan.tn;
+  g.g = std::min(plan.tn, p.n - g.j0);
+  g.p0 = static_cast<uint64_t>(l.kp) * plan.bk;
+  g.w = std::min(plan.bk, p.k - g.p0);
+  return g;
+}
+
+} // namespace
+
+// Pipelined execution. Panels of the next `lookahead` launches are acquired
+// (H2D copies queued on the copy stream) before each launch is enqueued on the
+// compute stream; the compute stream waits on the fill events of the launch's
+// three frames; every frame's retire event is recorded after its kernel; a C
+// tile is written back on the D2H stream as soon as its last K panel is
+// enqueued. The host blocks only when a frame it wants to refill still has an
+// unretired consumer.
+Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
+                   const GemmHooks& hooks) {
+  const CanonProblem& p = plan.problem;
+  if (Error e = rt.begin_operation()) return e;
+  std::deque<Acquired> window;
+  size_t next = 0;
+  const size_t total = plan.launches.size();
+
+  const auto acquire_launch = [&](size_t idx) -> Error {
+    const TileLaunch& l = plan.launches[idx];
+    const LaunchGeom g = launch_geom(plan, l);
+    Acquired acq;
+    acq.index = idx;
+    const PanelGeom ag = a_geom(p.a, g.i0, g.h, g.p0, g.w);
+    const PanelGeom bg = b_geom(p.b, g.p0, g.w, g.j0, g.g);
+    const PanelGeom cg = c_geom(g.i0, g.h, g.j0, g.g);
+    const bool c_needs_data = !l.first_panel || p.beta != 0.f;
+    if (Error e = rt.acquire(panel_key(p.c, cg), packed_ld(cg) * 4, c_needs_data, acq.c)) return e;
+    if (Error e = rt.acquire(panel_key(p.a, ag), packed_ld(ag) * 4, true, acq.a)) {
+      (void)rt.release_after(*acq.c, rt.compute_stream(), false);
+      return e;
+    }
+    if (Error e = rt.acquire(panel_key(p.b, bg), packed_ld(bg) * 4, true, acq.b)) {
+      (void)rt.release_after(*acq.c, rt.compute_stream(), false);
+      (void)rt.release_after(*acq.a, rt.compute_stream(), false);
+      return e;
+    }
+    window.push_back(acq);
+    return {};
+  };
+
+  Error result;
+  for (size_t idx = 0; idx < total && !result; ++idx) {
+    if (hooks.boundary) {
+      if (Error e = hooks.boundary("before_tile")) {
+        result = e;
+        break;
+      }
+    }
+    while (next <= idx) {
+      if (Error e = acquire_launch(next++)) {
+        result = e;
+        break;
+      }
+    }
+    if (result) break;
+    Acquired acq = window.front();
+    window.pop_front();
+    const TileLaunch& l = plan.launches[idx];
+    const LaunchGeom g = launch_geom(plan, l);
+    const PanelGeom ag = a_geom(p.a, g.i0, g.h, g.p0, g.w);
+    const PanelGeom bg = b_geom(p.b, g.p0, g.w, g.j0, g.g);
+    const PanelGeom cg = c_geom(g.i0, g.h, g.j0, g.g);
+    Stream cs = rt.compute_stream();
+    for (Frame* f : {acq.a, acq.b, acq.c}) {
+      if (Error e = rt.wait_ready(*f, cs)) {
+        result = e;
+        break;
+      }
+    }
+    if (result) break;
+    kernels::SgemmLaunch k;
+    k.a = reinterpret_cast<const float*>(acq.a->address);
+    k.b = reinterpret_cast<const float*>(acq.b->address);
+    k.c = reinterpret_cast<float*>(acq.c->address);
+    k.lda = static_cast<int64_t>(packed_ld(ag));
+    k.ldb = static_cast<int64_t>(packed_ld(bg));
+    k.ldc = static_cast<int64_t>(packed_ld(cg));
+    k.m = static_cast<int>(g.h);
+    k.n = static_cast<int>(g.g);
+    k.k = static_cast<int>(g.w);
+    k.alpha = p.alpha;
+    k.beta = l.first_panel ? p.beta : 1.f;
+    k.a_kcontig = p.a.transposed;
+    k.b_ncontig = p.b.transposed;
+    k.padded = true;
+    TraceInterval iv;
+    iv.kind = 'k';
+    if (Error e = rt.record_kernel(iv.start, iv.stop)) {
+      result = e;
+      break;
+    }
+    if (int rc = rt.device().event_record(iv.start, cs)) {
+      result = rt.device_failure(rc, "gemm", "record");
+      break;
+    }
+    if (int rc = rt.device().launch_sgemm(k, cs)) {
+      result = rt.device_failure(rc, "gemm", "launch_tile");
+      break;
+    }
+    if (int rc = rt.device().event_record(iv.stop, cs)) {
+      result = rt.device_failure(rc, "gemm", "record");
+      break;
+    }
+    rt.trace_push(iv);
+    rt.note_kernel_launched();
+    if (Error e = rt.release_after(*acq.a, cs, false)) { result = e; break; }
+    if (Error e = rt.release_after(*acq.b, cs, false)) { result = e; break; }
+    if (Error e = rt.release_after(*acq.c, cs, true)) { result = e; break; }
+    if (l.last_panel) {
+      if (Error e = rt.writeback_and_evict(*acq.c)) {
+        result = e;
+        break;
+      }
+    }
+    if (hooks.progress) hooks.progress(idx + 1, total);
+    while (next < total && next <= idx + plan.lookahead) {
+      if (Error e = acquire_launch(next++)) {
+        result = e;
+        break;
+      }
+    }
+  }
+  if (result) {
+    // Unpin what was acquired ahead, drop partial C panels, drain the device.
+    rt.discard_dirty();
+    (void)rt.finish_operation(operation_id);
+    return result;
+  }
+  return rt.finish_operation(operation_id);
+}
+
+} // namespace xvram

@@ -1,0 +1,120 @@
+// gemm.hpp — GEMM problem validation, panel planning and the pipelined
+// out-of-core executor.
+//
+// Reference counterparts: src/gemm/planner.hpp/.cpp (validate_problem
+// :785-859, make_plan :1005-1153) and src/gemm/executor.cpp:331-454
+// (execute_tiled_gemm). Validation reproduces the reference rules and error
+// classes exactly; planning and execution are redesigned around panels.
+#pragma once
+
+#include <cstdint>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "runtime.hpp"
+
+namespace xvram {
+
+struct MatrixSpec {
+  uint64_t allocation_id = 0;
+  uint64_t allocation_bytes = 0;
+  uint64_t offset_bytes = 0;
+  uint64_t rows = 0;
+  uint64_t columns = 0;
+  uint64_t leading_dimension = 0;
+  uint32_t layout = XVRAM_MATRIX_ROW_MAJOR;
+  uint32_t data_type = XVRAM_DATA_FP32;
+};
+
+struct GemmSpec {
+  MatrixSpec a, b, c;
+  uint32_t operation_a = XVRAM_MATRIX_OP_N;
+  uint32_t operation_b = XVRAM_MATRIX_OP_N;
+  uint32_t compute_mode = XVRAM_COMPUTE_AUTO;
+  double alpha = 1.0;
+  double beta = 0.0;
+  uint64_t tile_m_hint = 0, tile_n_hint = 0, tile_k_hint = 0;
+};
+
+// Problem error classes in the reference's enumerator order
+// (src/gemm/planner.hpp:69-84).
+enum class ProblemError : int {
+  none = 0,
+  zero_dimension,
+  invalid_allocation,
+  invalid_layout,
+  invalid_operation,
+  invalid_element_type,
+  invalid_compute_mode,
+  dimension_mismatch,
+  leading_dimension_too_small,
+  storage_overflow,
+  storage_out_of_bounds,
+  unsupported_type_combination,
+  output_aliases_input,
+  integer_limit_exceeded,
+};
+
+const char* problem_error_name(ProblemError error);
+
+// m/k from A and op_a, n from B and op_b (src/sdk/runtime.cpp:1303-1308).
+void problem_dims(const GemmSpec& spec, uint64_t& m, uint64_t& n, uint64_t& k);
+
+// The reference's validate_problem, compute mode resolved as
+// src/sdk/runtime.cpp:119-135 does (AUTO -> TF32 for FP32 data).
+ProblemError validate_problem(const GemmSpec& spec, char* operand);
+
+// One operand of the canonical column-major problem. Element (x, y) of the
+// operand's *physical* column-major storage is at base + (x + y*ld)*4; the
+// operand's logical (row, col) maps to (x, y) directly unless `transposed`.
+struct CanonOperand {
+  uint64_t allocation_id = 0;
+  uint64_t base = 0;
+  uint64_t ld = 0;
+  bool transposed = false;
+};
+
+// C' (m x n, column-major) = alpha * op(A') * op(B') + beta * C'.
+struct CanonProblem {
+  uint64_t m = 0, n = 0, k = 0;
+  CanonOperand a, b, c;
+  float alpha = 1.f, beta = 0.f;
+  bool swapped = false; // C was row-major: C' = C^T, A' = B, B' = A
+};
+
+CanonProblem canonicalize(const GemmSpec& spec);
+
+// One tile-kernel launch of a plan: C' tile (ti, tj), K panel kp.
+struct TileLaunch {
+  uint32_t ti = 0, tj = 0, kp = 0;
+  bool first_panel = false; // first K panel applied to this C tile (uses user beta)
+  bool last_panel = false;  // C tile final after this launch (write back)
+};
+
+struct GemmPlanData {
+  CanonProblem problem;
+  uint64_t tm = 0, tn = 0, bk = 0;         // tile / panel extents
+  uint64_t tiles_m = 0, tiles_n = 0, panels_k = 0;
+  uint64_t block_m = 0, block_n = 0;       // C block, in tiles
+  uint32_t lookahead = 0;                  // launches acquired ahead of the enqueue point
+  uint64_t h2d_bytes_planned = 0;          // compulsory traffic of this schedule
+  uint64_t d2h_bytes_planned = 0;
+  std::vector<TileLaunch> launches;
+};
+
+Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t frame_count,
+                     uint32_t prefetch_distance, GemmPlanData& out);
+
+struct GemmHooks {
+  // Called at safe boundaries (before each launch); a returned error stops
+  // execution there.
+  std::function<Error(const char* boundary)> boundary;
+  std::function<void(uint64_t completed, uint64_t total)> progress;
+};
+
+Error execute_gemm(Runtime& runtime, const GemmPlanData& plan, uint64_t operation_id,
+                   const GemmHooks& hooks);
+
+} // namespace xvram

@@ -1,0 +1,34 @@
+// sgemm_launch.hpp — host-side description of one tile-kernel launch.
+//
+// C (m x n, column-major, ldc) = alpha * op(A) * op(B) + beta * C, where
+//   a_kcontig == false: A(i,p) = a[i + p*lda]   (op N on a column-major A)
+//   a_kcontig == true : A(i,p) = a[p + i*lda]   (op T)
+//   b_ncontig == false: B(p,j) = b[p + j*ldb]   (op N)
+//   b_ncontig == true : B(p,j) = b[j + p*ldb]   (op T)
+// beta == 0 means C is not read. `padded` promises that every line of A, B
+// and C may be read as whole 16-byte vectors up to its leading dimension
+// (true for frame-packed panels); without it the kernel uses 32-bit loads.
+#pragma once
+
+#include <cstdint>
+
+namespace xvram::kernels {
+
+struct SgemmLaunch {
+  const float* a = nullptr;
+  const float* b = nullptr;
+  float* c = nullptr;
+  int64_t lda = 0, ldb = 0, ldc = 0;
+  int m = 0, n = 0, k = 0;
+  float alpha = 1.f, beta = 0.f;
+  bool a_kcontig = false;
+  bool b_ncontig = false;
+  bool padded = false;
+};
+
+// Enqueues the launch on `stream` (a hipStream_t); returns a hipError_t.
+int launch_sgemm(const SgemmLaunch& launch, void* stream);
+int sgemm_tile_m();
+int sgemm_tile_n();
+
+} // namespace xvram::kernels
