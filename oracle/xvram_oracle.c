@@ -37,6 +37,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #ifdef _OPENMP
@@ -70,14 +71,38 @@ void oracle_sgemm_f64_columns(int64_t m, int64_t n, int64_t k, double alpha, con
   (void)threads;
 #endif
   for (int64_t column = j_begin; column < j_end; ++column) {
+    /* Row-contiguous A: the same per-element sums (inner = 0..K-1 in order,
+     * so bit-identical results) computed a column at a time, which keeps the
+     * loads unit-stride. */
+    double* col_ref = NULL;
+    double* col_mag = NULL;
+    if (a_rs == 1) {
+      col_ref = (double*)calloc((size_t)m, sizeof(double));
+      col_mag = (double*)calloc((size_t)m, sizeof(double));
+      for (int64_t inner = 0; inner < k; ++inner) {
+        const double y = (double)b[inner * b_rs + column * b_cs];
+        const double ay = fabs(y);
+        const float* acol = a + inner * a_cs;
+        for (int64_t row = 0; row < m; ++row) {
+          const double x = (double)acol[row];
+          col_ref[row] += x * y;
+          col_mag[row] += fabs(x) * ay;
+        }
+      }
+    }
     for (int64_t row = 0; row < m; ++row) {
       double reference = 0.0;
       double magnitude = 0.0;
-      for (int64_t inner = 0; inner < k; ++inner) {
-        const double x = (double)a[row * a_rs + inner * a_cs];
-        const double y = (double)b[inner * b_rs + column * b_cs];
-        reference += x * y;
-        magnitude += fabs(x) * fabs(y);
+      if (col_ref) {
+        reference = col_ref[row];
+        magnitude = col_mag[row];
+      } else {
+        for (int64_t inner = 0; inner < k; ++inner) {
+          const double x = (double)a[row * a_rs + inner * a_cs];
+          const double y = (double)b[inner * b_rs + column * b_cs];
+          reference += x * y;
+          magnitude += fabs(x) * fabs(y);
+        }
       }
       double value = al * reference;
       double scale = fabs(al) * magnitude;
@@ -90,6 +115,8 @@ void oracle_sgemm_f64_columns(int64_t m, int64_t n, int64_t k, double alpha, con
       ref[out] = value;
       if (absab) absab[out] = scale;
     }
+    free(col_ref);
+    free(col_mag);
   }
 }
 

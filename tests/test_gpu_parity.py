@@ -1,0 +1,116 @@
+"""GPU parity: the C-ABI GEMM path on the MI355X against the FP64 CPU oracle.
+
+Acceptance per element: |C - C_ref| <= 4*K*2^-24*(|alpha|(|A||B|)_ij + |beta*C0_ij|)
+(BASELINE.json's bound, extended by the beta term), plus bit-exact equality on
+the reference's analytic integer pattern (exact in FP32 while 28*K < 2^24).
+"""
+import numpy as np
+import pytest
+
+import xvram_amd as xv
+from xvram_amd import abi
+
+from gemm_cases import Problem, pattern_operands, uniform
+
+pytestmark = pytest.mark.gpu
+
+MiB = 1 << 20
+OPS = [(abi.OP_N, abi.OP_N), (abi.OP_N, abi.OP_T), (abi.OP_T, abi.OP_N), (abi.OP_T, abi.OP_T)]
+OP_IDS = ["NN", "NT", "TN", "TT"]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return xv.load()
+
+
+@pytest.fixture(scope="module")
+def resident(lib):
+    """Unrestricted budget, 256 MiB frames: C1/C2 operands are one panel each."""
+    s = xv.Session(lib, chunk_size_bytes=256 * MiB)
+    yield s
+    s.close()
+    t = s.telemetry()
+    assert t.mappings == t.unmaps == t.set_access_calls
+    assert t.physical_handles_created == t.physical_handles_released
+    s.release()
+
+
+def check(oracle, prob, out, label):
+    ref, absab = prob.reference(oracle)
+    bad, max_err, ratio = oracle.check_bound(out, prob.k, ref, absab)
+    print(f"{label}: violations={bad} max_err={max_err:.3e} err/bound={ratio:.3e}", flush=True)
+    assert bad == 0, f"{label}: {bad} elements outside the FP64 bound (max err {max_err})"
+    return ratio
+
+
+def test_c1_1024_nn(resident, oracle_mod):
+    m = n = k = 1024
+    prob = Problem(uniform(oracle_mod, m, k, 101), uniform(oracle_mod, k, n, 102))
+    out = prob.run(resident)
+    assert prob.plan_info.tile_count == 1
+    check(oracle_mod, prob, out, "C1 1024^3 NN")
+    # The reference example's own tolerance holds as well.
+    ref, _ = prob.reference(oracle_mod)
+    assert oracle_mod.check_example_tolerance(out, ref) == 0
+
+
+@pytest.mark.parametrize("ops", OPS, ids=OP_IDS)
+def test_c2_ragged_alpha_beta(resident, oracle_mod, ops):
+    m, n, k = 3001, 2047, 4099
+    prob = Problem(uniform(oracle_mod, m, k, 201), uniform(oracle_mod, k, n, 202),
+                   uniform(oracle_mod, m, n, 203), op_a=ops[0], op_b=ops[1], alpha=1.5, beta=0.5)
+    out = prob.run(resident)
+    check(oracle_mod, prob, out, f"C2 3001x2047x4099 {ops}")
+
+
+@pytest.mark.parametrize("layouts", [(0, 0, 0), (1, 0, 1), (0, 1, 0), (1, 1, 0)],
+                         ids=["RRR", "CRC", "RCR", "CCR"])
+@pytest.mark.parametrize("ops", OPS, ids=OP_IDS)
+def test_layouts_and_padding(resident, oracle_mod, ops, layouts):
+    m, n, k = 301, 173, 259
+    prob = Problem(uniform(oracle_mod, m, k, 301), uniform(oracle_mod, k, n, 302),
+                   uniform(oracle_mod, m, n, 303), op_a=ops[0], op_b=ops[1],
+                   layouts=layouts, alpha=-0.75, beta=2.0, ld_pad=(3, 5, 7))
+    out = prob.run(resident)
+    check(oracle_mod, prob, out, f"layouts {layouts} ops {ops}")
+
+
+def test_beta_zero_never_reads_c(resident, oracle_mod):
+    m, n, k = 777, 555, 333
+    prob = Problem(uniform(oracle_mod, m, k, 401), uniform(oracle_mod, k, n, 402))
+    out = prob.run(resident, c_fill=np.float32(np.nan))
+    assert np.isfinite(out).all()
+    check(oracle_mod, prob, out, "beta=0 over NaN C")
+
+
+@pytest.mark.parametrize("ops", OPS, ids=OP_IDS)
+def test_pattern_bit_exact_out_of_core(lib, oracle_mod, ops):
+    """Analytic pattern, 4 MiB frames and a 14-frame budget: tiled, evicting,
+    exact."""
+    m, n, k = 2500, 2300, 4099
+    a_op, b_op = pattern_operands(m, n, k)
+    with xv.Session(lib, chunk_size_bytes=4 * MiB, cache_target_bytes=14 * 4 * MiB,
+                    workspace_cap_bytes=0, device_headroom_bytes=0) as s:
+        prob = Problem(a_op, b_op, op_a=ops[0], op_b=ops[1])
+        out = prob.run(s)
+        t = s.telemetry()
+        assert prob.plan_info.tile_count > 1
+        assert t.clean_evictions + t.dirty_evictions > 0
+        assert t.dirty_evictions == t.writebacks_completed
+        assert t.resident_bytes_peak <= t.cache_target_bytes
+    expected = oracle_mod.pattern_expected_matrix(m, n, k)
+    assert np.array_equal(out.astype(np.float64), expected)
+
+
+def test_repeat_uses_cached_panels(lib, oracle_mod):
+    m = n = k = 2048
+    prob = Problem(uniform(oracle_mod, m, k, 501), uniform(oracle_mod, k, n, 502))
+    with xv.Session(lib, chunk_size_bytes=64 * MiB) as s:
+        out = prob.run(s, repeat=3)
+        t = s.telemetry()
+        # A and B were copied once; C is write-only (beta = 0) every time.
+        assert t.bytes_h2d == 2 * m * k * 4
+        assert t.bytes_d2h == 3 * m * n * 4
+        assert t.cache_hits > 0
+    check(oracle_mod, prob, out, "repeat x3 2048^3")

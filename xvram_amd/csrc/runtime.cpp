@@ -84,7 +84,7 @@ Error Runtime::setup() {
   t_.cache_target_maximum_bytes = target_bytes_;
 
   arena_bytes_ = capacity_ * frame_bytes_;
-  if (int rc = device_->va_reserve(arena_bytes_, frame_bytes_, &arena_)) {
+  if (int rc = device_->va_reserve(arena_bytes_, granularity_, &arena_)) {
     arena_ = 0;
     return device_failure(rc, "setup", "va_reserve");
   }
@@ -310,13 +310,14 @@ void Runtime::evict_key(Frame& f, bool was_dirty) {
   if (was_dirty) ++t_.dirty_evictions;
 }
 
-// Frame choice (reference acquire_frame, runtime.cpp:3470-3529): a free frame
-// whose last consumer already retired, else a not-yet-created frame, else any
-// free frame, else the least-recently-used unpinned panel — clean panels
-// before dirty ones (a dirty victim is written back first).
+// Frame choice (reference acquire_frame, runtime.cpp:3470-3529): the free
+// frame idle longest, else a not-yet-created frame, else the least-recently-
+// used unpinned panel — clean panels before dirty ones (a dirty victim is
+// written back first). The choice depends only on the schedule, never on how
+// far the device has progressed, so the accounting of a run is reproducible
+// (the host-simulation build produces the same counters).
 Error Runtime::select_frame(Frame*& out) {
-  Frame* free_done = nullptr;
-  Frame* free_pending = nullptr;
+  Frame* free_frame = nullptr;
   Frame* unmapped = nullptr;
   Frame* victim = nullptr;
   for (Frame& f : frames_) {
@@ -326,16 +327,7 @@ Error Runtime::select_frame(Frame*& out) {
     }
     if (f.pins > 0) continue;
     if (!f.keyed) {
-      if (f.retire_pending) {
-        const int q = device_->event_query(f.retire);
-        if (q == 0) f.retire_pending = false;
-        else if (q != 1) return device_failure(q, "cache", "event_query");
-      }
-      if (!f.retire_pending) {
-        if (!free_done || f.last_use < free_done->last_use) free_done = &f;
-      } else if (!free_pending || f.last_use < free_pending->last_use) {
-        free_pending = &f;
-      }
+      if (!free_frame || f.last_use < free_frame->last_use) free_frame = &f;
       continue;
     }
     if (!victim) {
@@ -346,7 +338,7 @@ Error Runtime::select_frame(Frame*& out) {
       if (better) victim = &f;
     }
   }
-  Frame* chosen = free_done;
+  Frame* chosen = free_frame;
   if (!chosen && unmapped) {
     if (Error e = ensure_frame_mapped(*unmapped)) {
       if (e.status != XVRAM_STATUS_DEVICE_OUT_OF_MEMORY) return e;
@@ -354,7 +346,6 @@ Error Runtime::select_frame(Frame*& out) {
       chosen = unmapped;
     }
   }
-  if (!chosen) chosen = free_pending;
   if (!chosen && victim) {
     if (victim->dirty) {
       if (Error e = writeback_and_evict(*victim)) return e;
