@@ -1,0 +1,374 @@
+#!/usr/bin/env python3
+"""bench.py — out-of-core FP32 SGEMM through the xVRAM C ABI on one MI355X.
+
+Default workload (BASELINE.json metric "out-of-core FP32 SGEMM TFLOP/s at 3x
+VRAM budget; H2D GB/s vs link peak"): the north-star GEMM, C = A * B^T with
+M = N = K = 65536 (A, B, C = 3 x 16 GiB of pinned host memory) under a 16 GiB
+VRAM budget (operands = 3x the budget). A "step" is one complete gemm_execute:
+every A/B panel streamed from host RAM, every C tile written back.
+
+Prints one JSON line. ``value`` = 2MNK / wall time per step (inputs resident in
+host memory, as the ABI defines them). ``roofline`` describes the dominant
+kernel (the FP32-MFMA tile kernel): algorithmic FLOPs of its launches divided
+by their summed duration, both from HIP events recorded on the library's
+compute stream around every launch (trace file written by the library).
+``cpu_baseline`` times the FP64 reference loop (the oracle's restatement of
+the reference's CPU GEMM) on a bounded sample of the same product on all host
+cores; the same sample checks the GPU result against the per-element bound.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+GiB = 1 << 30
+MiB = 1 << 20
+FP32_MFMA_PEAK_TFLOPS = 157.3     # 256 CU x 2.4 GHz x 256 FLOP/clk
+PCIE5_X16_THEORETICAL_GBPS = 63.0  # per direction
+
+OP_N, OP_T = 0, 1
+WORKLOADS = {
+    # name: (m, n, k, op_a, op_b, budget, frame, description)
+    "ns65536_nt_16g": (65536, 65536, 65536, OP_N, OP_T, 16 * GiB, 256 * MiB,
+                       "FP32 SGEMM N/T 65536^3, 3 x 16 GiB operands in pinned host RAM, "
+                       "16 GiB VRAM budget (3x)"),
+    "c4_32768_nt_2g": (32768, 32768, 32768, OP_N, OP_T, 2 * GiB, 64 * MiB,
+                       "FP32 SGEMM N/T 32768^3, 3 x 4 GiB operands, 2 GiB VRAM budget"),
+    "resident_8192_nn": (8192, 8192, 8192, OP_N, OP_N, 0, 256 * MiB,
+                         "FP32 SGEMM N/N 8192^3, fully resident (one launch)"),
+    "resident_16384_nt": (16384, 16384, 16384, OP_N, OP_T, 0, 1024 * MiB,
+                          "FP32 SGEMM N/T 16384^3, fully resident (one launch)"),
+}
+DEFAULT = "ns65536_nt_16g"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---- host-link peak (pinned hipMemcpyAsync, measured in the same run) ------------
+
+def link_peak(bytes_per_copy: int = 512 * MiB, repeats: int = 8) -> dict:
+    hip = ctypes.CDLL("libamdhip64.so")
+    vp = ctypes.c_void_p
+    f = ctypes.c_float()
+    h1, h2, d1, d2 = vp(), vp(), vp(), vp()
+    s1, s2 = vp(), vp()
+    ev = [vp() for _ in range(4)]
+
+    def ok(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: {rc}")
+
+    ok(hip.hipSetDevice(0), "hipSetDevice")
+    for p in (h1, h2):
+        ok(hip.hipHostMalloc(ctypes.byref(p), ctypes.c_size_t(bytes_per_copy), 0), "hipHostMalloc")
+    for p in (d1, d2):
+        ok(hip.hipMalloc(ctypes.byref(p), ctypes.c_size_t(bytes_per_copy)), "hipMalloc")
+    for s in (s1, s2):
+        ok(hip.hipStreamCreateWithFlags(ctypes.byref(s), 1), "hipStreamCreate")
+    for e in ev:
+        ok(hip.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+    n = ctypes.c_size_t(bytes_per_copy)
+
+    def timed(pairs):
+        # pairs: list of (stream, dst, src, kind, start_event, stop_event)
+        for s, dst, src, kind, e0, e1 in pairs:
+            ok(hip.hipMemcpyAsync(dst, src, n, kind, s), "warmup copy")
+        ok(hip.hipDeviceSynchronize(), "sync")
+        for s, dst, src, kind, e0, e1 in pairs:
+            ok(hip.hipEventRecord(e0, s), "record")
+        for _ in range(repeats):
+            for s, dst, src, kind, e0, e1 in pairs:
+                ok(hip.hipMemcpyAsync(dst, src, n, kind, s), "copy")
+        for s, dst, src, kind, e0, e1 in pairs:
+            ok(hip.hipEventRecord(e1, s), "record")
+        ok(hip.hipDeviceSynchronize(), "sync")
+        out = []
+        for s, dst, src, kind, e0, e1 in pairs:
+            ok(hip.hipEventElapsedTime(ctypes.byref(f), e0, e1), "elapsed")
+            out.append(repeats * bytes_per_copy / (f.value * 1e-3) / 1e9)
+        return out
+
+    h2d = timed([(s1, d1, h1, 1, ev[0], ev[1])])[0]
+    d2h = timed([(s1, h1, d1, 2, ev[0], ev[1])])[0]
+    duplex = timed([(s1, d1, h1, 1, ev[0], ev[1]), (s2, h2, d2, 2, ev[2], ev[3])])
+    for p in (d1, d2):
+        hip.hipFree(p)
+    for p in (h1, h2):
+        hip.hipHostFree(p)
+    for e in ev:
+        hip.hipEventDestroy(e)
+    for s in (s1, s2):
+        hip.hipStreamDestroy(s)
+    return {"h2d_gbps": round(h2d, 2), "d2h_gbps": round(d2h, 2),
+            "duplex_h2d_gbps": round(duplex[0], 2), "duplex_d2h_gbps": round(duplex[1], 2),
+            "theoretical_gbps": PCIE5_X16_THEORETICAL_GBPS, "bytes_per_copy": bytes_per_copy}
+
+
+# ---- trace analysis ------------------------------------------------------------------
+
+def _union(intervals):
+    total, cur_s, cur_e = 0.0, None, None
+    merged = []
+    for s, e in sorted(intervals):
+        if cur_e is None or s > cur_e:
+            if cur_e is not None:
+                merged.append((cur_s, cur_e))
+            cur_s, cur_e = s, e
+        else:
+            cur_e = max(cur_e, e)
+    if cur_e is not None:
+        merged.append((cur_s, cur_e))
+    for s, e in merged:
+        total += e - s
+    return merged, total
+
+
+def _intersection(a, b):
+    i = j = 0
+    total = 0.0
+    while i < len(a) and j < len(b):
+        s = max(a[i][0], b[j][0])
+        e = min(a[i][1], b[j][1])
+        if e > s:
+            total += e - s
+        if a[i][1] < b[j][1]:
+            i += 1
+        else:
+            j += 1
+    return total
+
+
+def analyse(ops):
+    kernels = [(s, e) for op in ops for s, e, _ in op["kernels"]]
+    h2d = [(s, e) for op in ops for s, e, _ in op["h2d"]]
+    d2h = [(s, e) for op in ops for s, e, _ in op["d2h"]]
+    h2d_bytes = sum(b for op in ops for _, _, b in op["h2d"])
+    d2h_bytes = sum(b for op in ops for _, _, b in op["d2h"])
+    k_union, k_busy = _union(kernels)
+    h_union, h_busy = _union(h2d)
+    d_union, d_busy = _union(d2h)
+    copies_union, copy_busy = _union(h2d + d2h)
+    hidden = _intersection(copies_union, k_union)
+    kernel_ms = sum(e - s for s, e in kernels)
+    return {
+        "launches": len(kernels),
+        "kernel_ms_total": kernel_ms,
+        "kernel_busy_ms": k_busy,
+        "h2d_bytes": h2d_bytes, "d2h_bytes": d2h_bytes,
+        "h2d_busy_ms": h_busy, "d2h_busy_ms": d_busy,
+        "h2d_gbps_while_copying": h2d_bytes / (h_busy * 1e-3) / 1e9 if h_busy else None,
+        "d2h_gbps_while_copying": d2h_bytes / (d_busy * 1e-3) / 1e9 if d_busy else None,
+        "copy_time_hidden_fraction": hidden / copy_busy if copy_busy else None,
+    }
+
+
+# ---- operands ------------------------------------------------------------------------
+
+def synth_lib():
+    lib = ctypes.CDLL(os.path.join(ROOT, "xvram_amd", "lib", "libxvram_synth.so"))
+    fp = ctypes.POINTER(ctypes.c_float)
+    u64 = ctypes.c_uint64
+    lib.synth_fill_uniform.argtypes = [fp, u64, u64, u64]
+    lib.synth_fill_uniform_strided.argtypes = [fp, u64, u64, u64, u64, u64, u64]
+    return lib
+
+
+def fill_allocation(synth, alloc, elements: int, seed: int, chunk_elems: int = 256 * MiB):
+    buf = np.empty(min(chunk_elems, elements), dtype=np.float32)
+    done = 0
+    while done < elements:
+        n = min(chunk_elems, elements - done)
+        view = buf[:n]
+        synth.synth_fill_uniform(view.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), n, seed, done)
+        alloc.write(view, offset=done * 4)
+        done += n
+
+
+def sample_block(synth, rows, cols, seed, first, row_stride, col_stride):
+    out = np.empty(rows * cols, dtype=np.float32)
+    synth.synth_fill_uniform_strided(out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), rows,
+                                     cols, seed, first, row_stride, col_stride)
+    return np.asfortranarray(out.reshape(cols, rows).T)
+
+
+# ---- main ----------------------------------------------------------------------------
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default=DEFAULT)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="target CPU time of the cpu_baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X: the out-of-core path runs on a single GPU "
+              f"(--gpus {args.gpus} is not supported; multi-GPU sharding is a design note only).",
+              file=sys.stderr)
+        return 2
+
+    m, n, k, op_a, op_b, budget, frame, desc = WORKLOADS[args.workload]
+    trace_path = os.path.join(tempfile.mkdtemp(prefix="xvram_bench_"), "trace.jsonl")
+    os.environ["XVRAM_TRACE_FILE"] = trace_path
+
+    import xvram_amd as xv
+
+    log(f"workload {args.workload}: {desc}")
+    t0 = time.time()
+    link = link_peak()
+    log(f"link peak {link} ({time.time() - t0:.1f}s)")
+    synth = synth_lib()
+    lib = xv.load()
+    cfg = dict(chunk_size_bytes=frame)
+    if budget:
+        cfg["cache_target_bytes"] = budget
+    session = xv.Session(lib, **cfg)
+    a_rows, a_cols = (m, k) if op_a == OP_N else (k, m)
+    b_rows, b_cols = (k, n) if op_b == OP_N else (n, k)
+    t0 = time.time()
+    a = session.allocation(a_rows * a_cols * 4)
+    b = session.allocation(b_rows * b_cols * 4)
+    c = session.allocation(m * n * 4)
+    fill_allocation(synth, a, a_rows * a_cols, 1)
+    fill_allocation(synth, b, b_rows * b_cols, 2)
+    log(f"operands ready: {3 * m * n * 4 / GiB:.1f} GiB pinned host ({time.time() - t0:.1f}s)")
+    plan = xv.GemmPlan(session, xv.matrix(a, a_rows, a_cols, a_rows),
+                       xv.matrix(b, b_rows, b_cols, b_rows), xv.matrix(c, m, n, m), op_a, op_b)
+    info = plan.info()
+    log(f"plan: tiles {info.tile_m}x{info.tile_n}x{info.tile_k}, {info.tile_count} launches")
+    for i in range(args.warmup):
+        t = time.perf_counter()
+        plan.execute()
+        log(f"warmup {i}: {time.perf_counter() - t:.3f}s")
+    with open(trace_path, "a"):
+        pass
+    trace_lines_before = sum(1 for _ in open(trace_path))
+    tele0 = session.telemetry()
+    times = []
+    for i in range(args.steps):
+        t = time.perf_counter()
+        plan.execute()
+        times.append(time.perf_counter() - t)
+        log(f"step {i}: {times[-1]:.3f}s = {2.0 * m * n * k / times[-1] / 1e12:.1f} TFLOP/s")
+    tele1 = session.telemetry()
+    ops = [json.loads(line) for line in open(trace_path).readlines()[trace_lines_before:]]
+    stats = analyse(ops)
+
+    flops = 2.0 * m * n * k
+    step_s = sum(times) / len(times)
+    value = flops / step_s / 1e12
+    kernel_tflops = flops * args.steps / (stats["kernel_ms_total"] * 1e-3) / 1e12
+    launches_per_step = stats["launches"] / args.steps
+
+    # Sample check + CPU baseline on the same sample: C[0:sr, 0:sc] with full K.
+    import oracle
+
+    sr, sc = min(m, 1024), min(n, 64)
+    a_s = sample_block(synth, sr, k, 1, 0, 1 if op_a == OP_N else k, m if op_a == OP_N else 1)
+    b_s = sample_block(synth, k, sc, 2, 0, 1 if op_b == OP_N else n, k if op_b == OP_N else 1)
+    got = np.empty((sc, sr), dtype=np.float32)
+    for j in range(sc):
+        c.read_into(got[j], offset=(j * m) * 4)
+    got = np.asfortranarray(got.T)
+    threads = os.cpu_count() or 1
+    t = time.perf_counter()
+    ref, absab = oracle.sgemm_f64(a_s, b_s, threads=threads)
+    cpu_s = time.perf_counter() - t
+    bad, max_err, ratio = oracle.check_bound(got, k, ref, absab)
+    log(f"sample {sr}x{sc}: violations={bad} max_err={max_err:.3e} err/bound={ratio:.3e}")
+    cpu = None
+    if not args.no_cpu_baseline:
+        # Scale the column count so the timed CPU work is about --cpu-seconds.
+        cols = max(sc, int(sc * args.cpu_seconds / max(cpu_s, 1e-3)))
+        cols = min(cols, n)
+        b_cpu = sample_block(synth, k, cols, 2, 0, 1 if op_b == OP_N else n,
+                             k if op_b == OP_N else 1)
+        t = time.perf_counter()
+        oracle.sgemm_f64(a_s, b_cpu, threads=threads)
+        cpu_s = time.perf_counter() - t
+        cpu = {"value": round(2.0 * sr * cols * k / cpu_s / 1e12, 6), "unit": "TFLOP/s",
+               "cores": threads, "kind": "port",
+               "sample": f"C[0:{sr}, 0:{cols}] of the same {m}x{n}x{k} product with full K "
+                         f"(FP64 accumulation over FP32 inputs, {cpu_s:.1f} s on {threads} threads)"}
+
+    # HBM traffic per launch from the committed rocprofv3 --pmc summary, if any.
+    traffic = None
+    traffic_file = os.path.join(ROOT, "profiles", f"traffic_sgemm_mfma_{args.workload}.txt")
+    if os.path.exists(traffic_file):
+        for line in open(traffic_file):
+            if line.startswith("traffic_bytes_per_launch:"):
+                traffic = int(float(line.split(":", 1)[1]))
+
+    h2d_gbps = stats["h2d_gbps_while_copying"]
+    result = {
+        "metric": "out-of-core FP32 SGEMM TFLOP/s at 3x VRAM budget; H2D GB/s vs link peak",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded U[-1,1) operands, counter-based generator)",
+        "config": {"workload": args.workload, "description": desc, "m": m, "n": n, "k": k,
+                   "op_a": "NT"[op_a], "op_b": "NT"[op_b], "vram_budget_bytes": budget,
+                   "frame_bytes": frame, "tile": [info.tile_m, info.tile_n, info.tile_k],
+                   "launches_per_step": launches_per_step, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(kernel_tflops, 3),
+                     "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(kernel_tflops / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+        "link": {
+            "h2d_gbps_while_copying": round(h2d_gbps, 2) if h2d_gbps else None,
+            "d2h_gbps_while_copying": round(stats["d2h_gbps_while_copying"], 2)
+            if stats["d2h_gbps_while_copying"] else None,
+            "measured_peak": link,
+            "h2d_frac_of_measured_peak": round(h2d_gbps / link["h2d_gbps"], 4) if h2d_gbps else None,
+            "h2d_bytes_per_step": stats["h2d_bytes"] // args.steps,
+            "d2h_bytes_per_step": stats["d2h_bytes"] // args.steps,
+            "copy_time_hidden_fraction": round(stats["copy_time_hidden_fraction"], 4)
+            if stats["copy_time_hidden_fraction"] is not None else None,
+        },
+        "roofline_wall": {
+            "t_roof_s": max(flops / (FP32_MFMA_PEAK_TFLOPS * 1e12),
+                            (a_rows * a_cols + b_rows * b_cols) * 4 / (link["h2d_gbps"] * 1e9),
+                            m * n * 4 / (link["d2h_gbps"] * 1e9)),
+            "frac": None,
+        },
+        "kernel_ms_per_launch": round(stats["kernel_ms_total"] / max(1, stats["launches"]), 4),
+        "cache": {f: getattr(tele1, f) - getattr(tele0, f) for f in (
+            "bytes_h2d", "bytes_d2h", "cache_hits", "cache_misses", "clean_evictions",
+            "dirty_evictions", "writebacks_completed", "handle_reuses", "event_boundaries")},
+        "sample_check": {"elements": sr * sc, "violations": bad, "max_err_over_bound": ratio},
+    }
+    result["roofline_wall"]["frac"] = round(result["roofline_wall"]["t_roof_s"] / step_s, 4)
+    plan.release()
+    session.close()
+    t = session.telemetry()
+    result["teardown"] = {"mappings": t.mappings, "unmaps": t.unmaps,
+                          "handles_created": t.physical_handles_created,
+                          "handles_released": t.physical_handles_released}
+    session.release()
+    print(json.dumps(result), flush=True)
+    return 0 if bad == 0 else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

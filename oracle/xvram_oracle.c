@@ -48,7 +48,12 @@
  * base[r * rs + c * cs] (elements). Column-major storage with ld and op N is
  * rs = 1, cs = ld; op T is rs = ld, cs = 1; row-major swaps the two. */
 
-static inline double rnd_f32(double v) { return (double)(float)v; }
+/* Rounds to FP32 through a volatile so the compiler cannot fold the
+ * double -> float -> double round trip away (gcc 11 -O3 did). */
+static inline double rnd_f32(double v) {
+  volatile float f = (float)v;
+  return (double)f;
+}
 
 /*
  * C_ref(i,j) = alpha32 * sum_p a(i,p) * b(p,j) + beta32 * c0(i,j), FP64

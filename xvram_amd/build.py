@@ -2,6 +2,7 @@
 
   lib/libxvram.so          the product: C++20 host runtime + gfx950 HIP kernel,
                            exporting only ``xvram_get_api@@XVRAM_0.1``;
+  lib/libxvram_synth.so    seeded synthetic operands for the benchmark;
   lib/libxvram_hostsim.so  the same host runtime over a host-memory device
                            simulation, for CPU-only tests (never used on the
                            product path).
@@ -77,6 +78,10 @@ def build(hostsim: bool = True, product: bool = True, verbose: bool = True) -> N
         os.replace(out + ".tmp", out)
         if verbose:
             print(f"built {out}")
+    synth = os.path.join(LIB, "libxvram_synth.so")
+    _run(["gcc", "-std=c11", "-O3", "-fopenmp", "-fPIC", "-shared", "-o", synth + ".tmp",
+          os.path.join(CSRC, "synth.c"), "-lm"])
+    os.replace(synth + ".tmp", synth)
     if hostsim:
         objs = [os.path.join(OBJ, "sim_" + s.replace(".cpp", ".o"))
                 for s in HOST_SOURCES + ["device_hostsim.cpp"]]
