@@ -151,19 +151,29 @@ def _intersection(a, b):
 
 
 def analyse(ops):
-    kernels = [(s, e) for op in ops for s, e, _ in op["kernels"]]
-    h2d = [(s, e) for op in ops for s, e, _ in op["h2d"]]
-    d2h = [(s, e) for op in ops for s, e, _ in op["d2h"]]
-    h2d_bytes = sum(b for op in ops for _, _, b in op["h2d"])
-    d2h_bytes = sum(b for op in ops for _, _, b in op["d2h"])
-    k_union, k_busy = _union(kernels)
-    h_union, h_busy = _union(h2d)
-    d_union, d_busy = _union(d2h)
-    copies_union, copy_busy = _union(h2d + d2h)
-    hidden = _intersection(copies_union, k_union)
-    kernel_ms = sum(e - s for s, e in kernels)
+    """Busy times per operation (each operation's times are relative to its own
+    start event, so intervals of different operations are never merged)."""
+    k_busy = h_busy = d_busy = copy_busy = hidden = kernel_ms = 0.0
+    launches = h2d_bytes = d2h_bytes = 0
+    for op in ops:
+        kernels = [(s, e) for s, e, _ in op["kernels"]]
+        h2d = [(s, e) for s, e, _ in op["h2d"]]
+        d2h = [(s, e) for s, e, _ in op["d2h"]]
+        h2d_bytes += sum(b for _, _, b in op["h2d"])
+        d2h_bytes += sum(b for _, _, b in op["d2h"])
+        launches += len(kernels)
+        kernel_ms += sum(e - s for s, e in kernels)
+        k_union, kb = _union(kernels)
+        hb = _union(h2d)[1]
+        db = _union(d2h)[1]
+        copies_union, cb = _union(h2d + d2h)
+        k_busy += kb
+        h_busy += hb
+        d_busy += db
+        copy_busy += cb
+        hidden += _intersection(copies_union, k_union)
     return {
-        "launches": len(kernels),
+        "launches": launches,
         "kernel_ms_total": kernel_ms,
         "kernel_busy_ms": k_busy,
         "h2d_bytes": h2d_bytes, "d2h_bytes": d2h_bytes,
@@ -214,6 +224,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--trace-out", default=None,
+                    help="also keep the library's per-operation trace (JSON lines) here")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: the out-of-core path runs on a single GPU "
@@ -266,6 +278,9 @@ def main() -> int:
         log(f"step {i}: {times[-1]:.3f}s = {2.0 * m * n * k / times[-1] / 1e12:.1f} TFLOP/s")
     tele1 = session.telemetry()
     ops = [json.loads(line) for line in open(trace_path).readlines()[trace_lines_before:]]
+    if args.trace_out:
+        with open(args.trace_out, "w") as out:
+            out.writelines(json.dumps(op) + "\n" for op in ops)
     stats = analyse(ops)
 
     flops = 2.0 * m * n * k
