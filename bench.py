@@ -116,6 +116,23 @@ def link_peak(bytes_per_copy: int = 512 * MiB, repeats: int = 8) -> dict:
             "theoretical_gbps": PCIE5_X16_THEORETICAL_GBPS, "bytes_per_copy": bytes_per_copy}
 
 
+def copy_calibration(nbytes: int) -> None:
+    """Four device-to-device hipMemcpy calls of nbytes (HIP runs them as a copy kernel)."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    for p in (src, dst):
+        if hip.hipMalloc(ctypes.byref(p), ctypes.c_size_t(nbytes)) != 0:
+            raise RuntimeError("hipMalloc failed")
+    hip.hipMemset(src, 1, ctypes.c_size_t(nbytes))
+    for _ in range(4):
+        if hip.hipMemcpy(dst, src, ctypes.c_size_t(nbytes), 3) != 0:
+            raise RuntimeError("hipMemcpy failed")
+    hip.hipDeviceSynchronize()
+    hip.hipFree(src)
+    hip.hipFree(dst)
+    log(f"copy calibration: 4 x {nbytes} bytes device-to-device")
+
+
 # ---- trace analysis ------------------------------------------------------------------
 
 def _union(intervals):
@@ -226,7 +243,13 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--trace-out", default=None,
                     help="also keep the library's per-operation trace (JSON lines) here")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run 4 device-to-device copies of BYTES (a plain copy kernel of "
+                         "known size, used to scale rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: the out-of-core path runs on a single GPU "
               f"(--gpus {args.gpus} is not supported; multi-GPU sharding is a design note only).",

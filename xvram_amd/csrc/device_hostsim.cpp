@@ -212,6 +212,12 @@ public:
 
   int launch_sgemm(const kernels::SgemmLaunch& l, Stream) override {
     if (int f = fault(kLaunch)) return f;
+    // Same launch contract as the gfx950 kernel (sgemm_launch.hpp).
+    const bool aligned = reinterpret_cast<uintptr_t>(l.a) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(l.b) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(l.c) % 16 == 0 && l.lda % 4 == 0 &&
+                         l.ldb % 4 == 0 && l.ldc % 4 == 0 && l.padded;
+    if (l.m <= 0 || l.n <= 0 || l.k <= 0 || !aligned) return 1; // hipErrorInvalidValue
     const auto span = [](int64_t rows, int64_t cols, int64_t ld) {
       return static_cast<uint64_t>(((cols - 1) * ld + rows) * 4);
     };

@@ -5,9 +5,10 @@
 //   a_kcontig == true : A(i,p) = a[p + i*lda]   (op T)
 //   b_ncontig == false: B(p,j) = b[p + j*ldb]   (op N)
 //   b_ncontig == true : B(p,j) = b[j + p*ldb]   (op T)
-// beta == 0 means C is not read. `padded` promises that every line of A, B
-// and C may be read as whole 16-byte vectors up to its leading dimension
-// (true for frame-packed panels); without it the kernel uses 32-bit loads.
+// beta == 0 means C is not read. The kernel requires 16-byte aligned bases,
+// leading dimensions that are multiples of 4 floats and `padded` = true (every
+// line may be read as whole 16-byte vectors up to its leading dimension), which
+// frame-packed panels always satisfy; anything else returns hipErrorInvalidValue.
 #pragma once
 
 #include <cstdint>
