@@ -22,7 +22,7 @@ PRODUCT_LIB = os.path.join(LIB_DIR, "libxvram.so")
 HOSTSIM_LIB = os.path.join(LIB_DIR, "libxvram_hostsim.so")
 
 __all__ = ["Library", "Session", "Allocation", "GemmPlan", "Operation", "XvramError", "abi",
-           "load", "PRODUCT_LIB", "HOSTSIM_LIB"]
+           "TransactionView", "access", "matrix", "load", "PRODUCT_LIB", "HOSTSIM_LIB"]
 
 
 class XvramError(RuntimeError):
@@ -105,6 +105,58 @@ class Session:
     def drain(self, timeout_ms: int = abi.TIMEOUT_INFINITE) -> None:
         self.check(self.api.session_drain(self.handle, timeout_ms), "session_drain")
 
+    def prefetch(self, ranges, deadline_ms: int = 0) -> "Operation":
+        """prefetch_submit over ``ranges`` (a list of :func:`access` records)."""
+        arr = (abi.AccessRange * len(ranges))(*ranges)
+        desc = abi.PrefetchDesc()
+        desc.struct_size = ctypes.sizeof(desc)
+        desc.ranges = ctypes.cast(arr, ctypes.POINTER(abi.AccessRange)) if ranges else None
+        desc.range_count = len(ranges)
+        desc.deadline_ms = deadline_ms
+        handle = ctypes.c_void_p()
+        self.check(self.api.prefetch_submit(self.handle, ctypes.byref(desc), ctypes.byref(handle)),
+                   "prefetch_submit")
+        return Operation(self, handle)
+
+    def _transaction_desc(self, ranges, callback, workspace_bytes, deadline_ms):
+        def trampoline(ctx_ptr, _user, err_ptr):
+            try:
+                result = callback(TransactionView(ctx_ptr.contents))
+                return abi.SUCCESS if result is None else int(result)
+            except Exception as exc:  # reported through the callback error record
+                msg = f"{type(exc).__name__}: {exc}".encode()[:255]
+                err_ptr.contents.message = msg
+                return abi.CALLBACK_FAILED
+        cb = abi.TransactionCallback(trampoline)
+        arr = (abi.AccessRange * len(ranges))(*ranges)
+        desc = abi.TransactionDesc()
+        desc.struct_size = ctypes.sizeof(desc)
+        desc.ranges = ctypes.cast(arr, ctypes.POINTER(abi.AccessRange)) if ranges else None
+        desc.range_count = len(ranges)
+        desc.workspace_bytes = workspace_bytes
+        desc.deadline_ms = deadline_ms
+        desc.callback = cb
+        return desc, (cb, arr)
+
+    def transaction(self, ranges, callback, workspace_bytes: int = 0,
+                    deadline_ms: int = 0) -> "Operation":
+        """transaction_submit: ``callback(view)`` runs on the session worker with
+        the working set resident; it returns None (success) or a status."""
+        desc, keep = self._transaction_desc(ranges, callback, workspace_bytes, deadline_ms)
+        handle = ctypes.c_void_p()
+        self.check(self.api.transaction_submit(self.handle, ctypes.byref(desc),
+                                               ctypes.byref(handle)), "transaction_submit")
+        op = Operation(self, handle)
+        op._keep = keep  # the callback must outlive the queued operation
+        return op
+
+    def execute_transaction(self, ranges, callback, workspace_bytes: int = 0,
+                            deadline_ms: int = 0, timeout_ms: int = abi.TIMEOUT_INFINITE) -> None:
+        desc, keep = self._transaction_desc(ranges, callback, workspace_bytes, deadline_ms)
+        status = self.api.transaction_execute(self.handle, ctypes.byref(desc), timeout_ms)
+        del keep
+        self.check(status, "transaction_execute")
+
     def close(self, timeout_ms: int = abi.TIMEOUT_INFINITE) -> None:
         if self.handle:
             self.check(self.api.session_close(self.handle, timeout_ms), "session_close")
@@ -166,6 +218,28 @@ class Allocation:
             self.session.check(self.session.api.allocation_release(self.handle),
                                "allocation_release")
             self.handle = None
+
+
+def access(allocation: Allocation, offset: int, length: int,
+           mode: int = abi.ACCESS_READ) -> abi.AccessRange:
+    r = abi.AccessRange()
+    r.allocation = allocation.handle.value if allocation is not None else None
+    r.offset_bytes, r.length_bytes, r.mode = offset, length, mode
+    return r
+
+
+class TransactionView:
+    """What a transaction callback sees: the resolved ranges (allocation id,
+    offset, length, device address, mode), the workspace and the stream."""
+
+    def __init__(self, ctx: abi.TransactionContext):
+        self.operation_id = ctx.operation_id
+        self.transaction_id = ctx.transaction_id
+        self.ranges = [(r.allocation_id, r.offset_bytes, r.length_bytes, r.device_address, r.mode)
+                       for r in (ctx.ranges[i] for i in range(ctx.range_count))]
+        self.workspace_address = ctx.workspace_device_address
+        self.workspace_bytes = ctx.workspace_bytes
+        self.stream = ctx.native_stream
 
 
 def matrix(allocation: Allocation, rows: int, columns: int, ld: int,

@@ -25,6 +25,9 @@ HOST_OUT_OF_MEMORY, DEVICE_OUT_OF_MEMORY, BUDGET_PRESSURE, BUSY, NOT_READY = 5, 
 TIMEOUT, CORRUPTION, CALLBACK_FAILED, CUDA_ERROR, CUBLAS_ERROR = 10, 11, 12, 13, 14
 POISONED, CLEANUP_FAILED, CLOSED, CANCELLED, INTERNAL = 15, 16, 17, 18, 19
 
+NATIVE_ERROR_NONE, NATIVE_ERROR_CUDA, NATIVE_ERROR_CUBLAS = 0, 1, 2
+NATIVE_ERROR_PLATFORM, NATIVE_ERROR_CALLBACK, NATIVE_ERROR_INTERNAL = 3, 4, 5
+
 CONTEXT_ISOLATED, CONTEXT_ATTACH_CURRENT = 0, 1
 CACHE_POLICY_CLOCK, CACHE_POLICY_LRU = 0, 1
 ALLOCATION_NORMAL, ALLOCATION_HOT, ALLOCATION_STREAMING = 0, 1, 2

@@ -206,9 +206,11 @@ Error validate_session_config(const xvram_session_config_v1* c) {
 
 // src/sdk/api.cpp:236-276.
 Error collect_accesses(const std::shared_ptr<SessionState>& owner, const xvram_access_range_v1* ranges,
-                       uint64_t count, const char* operation) {
+                       uint64_t count, const char* operation, std::vector<Session::Access>& out) {
   if (count == 0) return invalid(operation, "at least one access range is required");
   if (ranges == nullptr) return invalid(operation, "range array is null");
+  if (count > out.max_size()) return invalid(operation, "range count is too large");
+  out.reserve(static_cast<size_t>(count));
   for (uint64_t i = 0; i < count; ++i) {
     const xvram_access_range_v1& r = ranges[i];
     if (r.allocation == nullptr || !r.allocation->backend)
@@ -220,6 +222,7 @@ Error collect_accesses(const std::shared_ptr<SessionState>& owner, const xvram_a
     if (r.length_bytes == 0) return invalid(operation, "access range length must be non-zero");
     if (r.offset_bytes > UINT64_MAX - r.length_bytes)
       return invalid(operation, "access range overflows uint64");
+    out.push_back(Session::Access{r.allocation->backend, r.offset_bytes, r.length_bytes, r.mode});
   }
   return {};
 }
@@ -376,9 +379,9 @@ xvram_status XVRAM_CALL allocation_get_info_entry(xvram_allocation a,
     local.alignment_bytes = a->backend->desc.alignment_bytes;
     local.priority = a->backend->desc.priority;
     local.flags = 0;
-    // GEMM panels are cached by rectangle, not at a per-allocation device
-    // address, so no stable per-allocation virtual address is promised.
-    local.stable_virtual_address = 0;
+    // Transactions see each allocation at one device VA reserved on first use
+    // and kept until release.
+    local.stable_virtual_address = 1;
     *out = local;
     return {};
   });
@@ -467,9 +470,12 @@ xvram_status XVRAM_CALL prefetch_submit_entry(xvram_session s, const xvram_prefe
     if (d->flags != 0 || !all_zero(d->reserved, 2))
       return invalid("prefetch_submit", "unknown flags or non-zero reserved field");
     if (Error e = validate_deadline(d->deadline_ms, "prefetch_submit")) return e;
-    if (Error e = collect_accesses(s->state, d->ranges, d->range_count, "prefetch_submit")) return e;
-    return make_error(XVRAM_STATUS_UNSUPPORTED, "sdk", "prefetch_submit",
-                      "linear-range prefetch is not implemented on this device path");
+    std::vector<Session::Access> accesses;
+    if (Error e = collect_accesses(s->state, d->ranges, d->range_count, "prefetch_submit", accesses))
+      return e;
+    std::shared_ptr<Operation> op;
+    if (Error e = s->state->backend->submit_prefetch(std::move(accesses), d->deadline_ms, op)) return e;
+    return wrap_operation(s->state, std::move(op), out);
   });
 }
 
@@ -487,9 +493,14 @@ xvram_status XVRAM_CALL transaction_submit_entry(xvram_session s, const xvram_tr
     if (d->workspace_bytes > s->state->workspace_cap_bytes)
       return invalid("transaction_submit", "transaction workspace exceeds the session cap");
     if (Error e = validate_deadline(d->deadline_ms, "transaction_submit")) return e;
-    if (Error e = collect_accesses(s->state, d->ranges, d->range_count, "transaction_submit")) return e;
-    return make_error(XVRAM_STATUS_UNSUPPORTED, "sdk", "transaction_submit",
-                      "linear-range transactions are not implemented on this device path");
+    std::vector<Session::Access> accesses;
+    if (Error e = collect_accesses(s->state, d->ranges, d->range_count, "transaction_submit", accesses))
+      return e;
+    std::shared_ptr<Operation> op;
+    if (Error e = s->state->backend->submit_transaction(std::move(accesses), d->workspace_bytes,
+                                                        d->deadline_ms, d->callback, d->user_data, op))
+      return e;
+    return wrap_operation(s->state, std::move(op), out);
   });
 }
 

@@ -9,9 +9,12 @@
 // Simulation rules: every call completes synchronously; a reserved VA range is
 // backed by host memory so mapped frames are ordinary pointers; accesses to
 // unmapped frames are detected and fail the call; the tile "kernel" is a
-// plain loop with the SgemmLaunch semantics (beta == 0 never reads C).
+// plain loop with the SgemmLaunch semantics (beta == 0 never reads C). An
+// event records the host clock, so the time between two events is the host
+// time of the work done between their records.
 // Faults can be injected per call site (xvram_hostsim_inject), and the
 // reported device memory can be set (xvram_hostsim_set_memory).
+#include <chrono>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -177,11 +180,17 @@ public:
     return 0;
   }
   int event_destroy(Event) override { return 0; }
-  int event_record(Event, Stream) override { return fault(kEventRecord); }
+  int event_record(Event event, Stream) override {
+    if (int f = fault(kEventRecord)) return f;
+    recorded_[event] = std::chrono::steady_clock::now();
+    return 0;
+  }
   int event_query(Event) override { return fault(kEventQuery); }
   int event_sync(Event) override { return fault(kEventSync); }
-  int event_elapsed_ms(float* ms, Event, Event) override {
-    *ms = 0.f;
+  int event_elapsed_ms(float* ms, Event start, Event stop) override {
+    auto a = recorded_.find(start), b = recorded_.find(stop);
+    if (a == recorded_.end() || b == recorded_.end()) return kSimBadAccess;
+    *ms = std::chrono::duration<float, std::milli>(b->second - a->second).count();
     return 0;
   }
   int stream_wait_event(Stream, Event) override { return 0; }
@@ -284,6 +293,7 @@ private:
   std::map<uint64_t, uint64_t> reservations_;
   std::map<uint64_t, uint64_t> handles_;
   std::map<uint64_t, Mapping> mappings_;
+  std::map<Event, std::chrono::steady_clock::time_point> recorded_;
   uint64_t next_handle_ = 0;
   uint64_t next_object_ = 0x1000;
 };

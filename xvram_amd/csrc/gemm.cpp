@@ -267,7 +267,7 @@ CanonProblem canonicalize(const GemmSpec& s) {
 // shape minimises the scheduled H2D traffic
 //   ceil(tiles_m/block_m)*|B| + ceil(tiles_n/block_n)*|A| (+|C| if beta != 0).
 Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t frame_count,
-                     uint32_t prefetch_distance, GemmPlanData& out) {
+                     uint32_t prefetch_distance, uint64_t max_launch_flops, GemmPlanData& out) {
   out = GemmPlanData{};
   CanonProblem p = canonicalize(spec);
   out.problem = p;
@@ -277,7 +277,12 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t frame_
   const uint64_t F = frame_bytes;
   uint64_t tm, tn, bk;
   const bool hinted = spec.tile_m_hint || spec.tile_n_hint || spec.tile_k_hint;
-  if (!hinted && a_panel_bytes(p, p.m, p.k) <= F && b_panel_bytes(p, p.k, p.n) <= F &&
+  const auto launch_flops = [](uint64_t a, uint64_t b, uint64_t c) {
+    return 2.0 * static_cast<double>(a) * static_cast<double>(b) * static_cast<double>(c);
+  };
+  const bool over_cap = max_launch_flops != 0 &&
+                        launch_flops(p.m, p.n, p.k) > static_cast<double>(max_launch_flops);
+  if (!hinted && !over_cap && a_panel_bytes(p, p.m, p.k) <= F && b_panel_bytes(p, p.k, p.n) <= F &&
       c_panel_bytes(p.m, p.n) <= F) {
     tm = p.m;
     tn = p.n;
@@ -326,6 +331,15 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t frame_
           grew = true;
         }
       }
+    }
+    // Keep every launch well inside the transaction duration guard: split K
+    // first (the C tile stays resident across K panels), then the larger of
+    // the tile extents.
+    while (max_launch_flops != 0 &&
+           launch_flops(tm, tn, bk) > static_cast<double>(max_launch_flops)) {
+      uint64_t* cut = bk > 2048 ? &bk : (tm >= tn ? &tm : &tn);
+      if (*cut <= 256) break; // a launch this small cannot approach any guard
+      *cut = std::max<uint64_t>(256, *cut / 2 / 16 * 16);
     }
   }
   out.tm = tm;

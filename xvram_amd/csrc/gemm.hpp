@@ -104,8 +104,14 @@ struct GemmPlanData {
   std::vector<TileLaunch> launches;
 };
 
+// Floating-point rate assumed when sizing launches against the transaction
+// duration guard: well under the tile kernel's sustained FP32 rate, so a launch
+// planned at the cap finishes in a fraction of the guard.
+constexpr double kGuardPlanningFlopsPerMs = 4.0e10; // 40 TFLOP/s
+
+// max_launch_flops caps 2*tm*tn*bk of every launch (0 = no cap).
 Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t frame_count,
-                     uint32_t prefetch_distance, GemmPlanData& out);
+                     uint32_t prefetch_distance, uint64_t max_launch_flops, GemmPlanData& out);
 
 struct GemmHooks {
   // Called at safe boundaries (before each launch); a returned error stops

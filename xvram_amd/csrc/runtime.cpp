@@ -1,4 +1,4 @@
-// runtime.cpp — host backing, VRAM frame pool and panel cache (see runtime.hpp).
+// runtime.cpp — host backing, VRAM frame pool, panel/chunk cache, transactions.
 #include "runtime.hpp"
 
 #include <algorithm>
@@ -14,7 +14,43 @@ namespace {
 
 uint64_t lcm64(uint64_t a, uint64_t b) { return a / std::gcd(a, b) * b; }
 
+// Combined access of two overlapping spans (the reference ORs mode bits:
+// anything that both reads and writes is read_write).
+uint32_t combine_modes(uint32_t a, uint32_t b) {
+  if (a == b) return a;
+  return XVRAM_ACCESS_READ_WRITE;
+}
+
 } // namespace
+
+bool keys_overlap(const PanelKey& a, const PanelKey& b) {
+  if (a.allocation_id != b.allocation_id) return false;
+  if (a.offset >= b.end() || b.offset >= a.end()) return false;
+  if (a.pitch == b.pitch && a.pitch > 0 && a.height > 1 && b.height > 1) {
+    const uint64_t P = a.pitch;
+    const uint64_t ar = a.offset / P, ac = a.offset % P;
+    const uint64_t br = b.offset / P, bc = b.offset % P;
+    if (ac + a.width <= P && bc + b.width <= P) {
+      const bool rows = ar < br + b.height && br < ar + a.height;
+      const bool cols = ac < bc + b.width && bc < ac + a.width;
+      return rows && cols;
+    }
+    return true;
+  }
+  // A contiguous range against a strided rectangle: test the rectangle's lines.
+  const PanelKey* line = a.height == 1 ? &a : (b.height == 1 ? &b : nullptr);
+  if (line == nullptr) return true; // different pitches: conservative
+  const PanelKey& s = line == &a ? b : a;
+  const uint64_t lo = line->offset, hi = line->offset + line->width;
+  uint64_t l = 0;
+  if (lo > s.offset + s.width && s.pitch > 0) l = (lo - s.offset - s.width) / s.pitch;
+  for (; l < s.height; ++l) {
+    const uint64_t start = s.offset + l * s.pitch;
+    if (start >= hi) break;
+    if (lo < start + s.width) return true;
+  }
+  return false;
+}
 
 Runtime::Runtime(RuntimeConfig config) : config_(config), device_(make_device()) {
   if (const char* path = std::getenv("XVRAM_TRACE_FILE"); path != nullptr && *path != '\0')
@@ -43,7 +79,7 @@ Error Runtime::poison(std::string_view stage, std::string_view operation,
 
 // Session setup (reference src/residency/runtime.cpp:212-596): bind the
 // device, align the frame size to the VMM granularity, derive the budget from
-// hipMemGetInfo, reserve the frame arena and create the three streams.
+// hipMemGetInfo, reserve the panel arena and create the three streams.
 Error Runtime::setup() {
   if (int rc = device_->init(config_.device_ordinal)) return device_failure(rc, "setup", "init");
   int version = 0;
@@ -91,13 +127,13 @@ Error Runtime::setup() {
   frames_.resize(capacity_);
   for (uint64_t i = 0; i < capacity_; ++i) {
     frames_[i].index = i;
-    frames_[i].address = arena_ + i * frame_bytes_;
+    frames_[i].slot = arena_ + i * frame_bytes_;
   }
   if (int rc = device_->stream_create(&compute_)) return device_failure(rc, "setup", "stream");
   if (int rc = device_->stream_create(&h2d_)) return device_failure(rc, "setup", "stream");
   if (int rc = device_->stream_create(&d2h_)) return device_failure(rc, "setup", "stream");
   if (int rc = device_->event_create(&op_start_)) return device_failure(rc, "setup", "event");
-  t_.flags = XVRAM_TELEMETRY_NO_PHYSICAL_ALIASES;
+  t_.flags = XVRAM_TELEMETRY_NO_PHYSICAL_ALIASES | XVRAM_TELEMETRY_STABLE_VIRTUAL_ADDRESSES;
   setup_done_ = true;
   return {};
 }
@@ -110,7 +146,8 @@ Error Runtime::drain() {
 }
 
 // Teardown (reference runtime.cpp:1540-1857): wait for the device, unmap and
-// release every frame, free the arena, streams, events and host backing.
+// release every frame, free the VA reservations, streams, events and host
+// backing.
 Error Runtime::close() {
   if (closed_) return {};
   closed_ = true;
@@ -126,11 +163,14 @@ Error Runtime::close() {
   for (Stream s : {h2d_, compute_, d2h_})
     if (s) note(device_->stream_sync(s), "stream_sync");
   for (Frame& f : frames_) {
-    if (f.keyed) evict_key(f, false);
-    if (f.mapped) {
-      note(device_->mem_unmap(f.address, frame_bytes_), "unmap");
+    if (f.keyed) {
+      index_.erase(f.key);
+      f.keyed = false;
+    }
+    if (f.mapped_at) {
+      note(device_->mem_unmap(f.mapped_at, frame_bytes_), "unmap");
       ++t_.unmaps;
-      f.mapped = false;
+      f.mapped_at = 0;
     }
     if (f.handle) {
       note(device_->mem_release(f.handle), "release");
@@ -141,11 +181,18 @@ Error Runtime::close() {
     if (f.retire) device_->event_destroy(f.retire);
     f.ready = f.retire = nullptr;
   }
+  if (workspace_va_) {
+    note(device_->mem_unmap(workspace_va_, workspace_bytes_), "unmap");
+    ++t_.unmaps;
+    note(device_->mem_release(workspace_handle_), "release");
+    ++t_.physical_handles_released;
+    note(device_->va_free(workspace_va_, workspace_bytes_), "va_free");
+    workspace_va_ = 0;
+  }
   if (arena_) note(device_->va_free(arena_, arena_bytes_), "va_free");
   arena_ = 0;
   for (Event e : event_pool_) device_->event_destroy(e);
   for (Event e : events_in_use_) device_->event_destroy(e);
-  for (auto& [key, e] : pending_writebacks_) (void)key, (void)e;
   event_pool_.clear();
   events_in_use_.clear();
   pending_writebacks_.clear();
@@ -153,7 +200,10 @@ Error Runtime::close() {
   for (Stream s : {h2d_, compute_, d2h_})
     if (s) device_->stream_destroy(s);
   compute_ = h2d_ = d2h_ = nullptr;
-  for (auto& [id, a] : allocations_) device_->host_free(a.host);
+  for (auto& [id, a] : allocations_) {
+    if (a.va) note(device_->va_free(a.va, a.va_bytes), "va_free");
+    device_->host_free(a.host);
+  }
   allocations_.clear();
   t_.resident_bytes = 0;
   return first;
@@ -192,6 +242,9 @@ void Runtime::parallel_copy(void* dst, const void* src, uint64_t bytes) {
 Error Runtime::allocate(uint64_t bytes, uint64_t alignment, uint32_t priority,
                         HostAllocation*& out) {
   if (poisoned_) return make_error(XVRAM_STATUS_POISONED, "allocation", "create", "session is poisoned");
+  if (launches_blocked_)
+    return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "allocation", "allocate",
+                      "allocation size or runtime state is invalid");
   void* host = nullptr;
   if (int rc = device_->host_alloc(bytes, &host)) {
     if (rc == 2 /* out of memory */)
@@ -222,6 +275,13 @@ Error Runtime::release(uint64_t id) {
   HostAllocation* a = find(id);
   if (!a) return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "allocation", "release", "unknown allocation");
   if (Error e = invalidate(id, 0, a->bytes)) return e;
+  if (a->va) {
+    for (Frame& f : frames_)
+      if (f.mapped_at >= a->va && f.mapped_at < a->va + a->va_bytes)
+        if (Error e = unmap_frame(f)) return e;
+    if (int rc = device_->va_free(a->va, a->va_bytes)) return device_failure(rc, "allocation", "va_free");
+    a->va = 0;
+  }
   device_->host_free(a->host);
   pinned_bytes_ -= a->bytes;
   allocations_.erase(id);
@@ -236,7 +296,7 @@ Error Runtime::write(uint64_t id, uint64_t offset, const void* source, uint64_t 
     return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "allocation", "write",
                       "write range exceeds the allocation");
   if (poisoned_) return make_error(XVRAM_STATUS_POISONED, "allocation", "write", "session is poisoned");
-  // Cached panels overlapping the range become stale: drop them first.
+  // Cached entries overlapping the range become stale: drop them first.
   if (Error e = invalidate(id, offset, end)) return e;
   parallel_copy(a->host + offset, source, bytes);
   return {};
@@ -250,16 +310,22 @@ Error Runtime::read(uint64_t id, uint64_t offset, void* destination, uint64_t by
     return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "allocation", "read",
                       "read range exceeds the allocation");
   if (poisoned_) return make_error(XVRAM_STATUS_POISONED, "allocation", "read", "session is poisoned");
-  // Operations write their dirty panels back before completing, so the host
+  // Operations write their dirty entries back before completing, so the host
   // copy is authoritative here.
   parallel_copy(destination, a->host + offset, bytes);
   return {};
 }
 
-// ---- frame pool --------------------------------------------------------------
+// ---- frames ----------------------------------------------------------------
 
-Error Runtime::ensure_frame_mapped(Frame& f) {
-  if (f.mapped) return {};
+// A frame's handle is mapped at one address at a time: its arena slot while
+// it holds a panel, the chunk's address inside the owning allocation's VA
+// while it holds a chunk. Moving it waits for its last consumer first.
+Error Runtime::map_frame_at(Frame& f, uint64_t address) {
+  if (f.mapped_at == address) {
+    f.address = address;
+    return {};
+  }
   if (!f.handle) {
     uint64_t handle = 0;
     if (int rc = device_->mem_create(frame_bytes_, &handle)) {
@@ -271,11 +337,14 @@ Error Runtime::ensure_frame_mapped(Frame& f) {
     f.handle = handle;
     ++t_.physical_handles_created;
   }
-  if (int rc = device_->mem_map(f.address, frame_bytes_, f.handle))
+  if (f.mapped_at)
+    if (Error e = unmap_frame(f)) return e;
+  if (int rc = device_->mem_map(address, frame_bytes_, f.handle))
     return device_failure(rc, "cache", "mem_map");
-  f.mapped = true;
+  f.mapped_at = address;
+  f.address = address;
   ++t_.mappings;
-  if (int rc = device_->set_access(f.address, frame_bytes_))
+  if (int rc = device_->set_access(address, frame_bytes_))
     return device_failure(rc, "cache", "set_access");
   ++t_.set_access_calls;
   if (!f.ready)
@@ -285,7 +354,17 @@ Error Runtime::ensure_frame_mapped(Frame& f) {
   return {};
 }
 
-// A frame is handed out for a new panel only after its last consumer's event
+Error Runtime::unmap_frame(Frame& f) {
+  if (!f.mapped_at) return {};
+  if (Error e = wait_retired(f)) return e;
+  if (int rc = device_->mem_unmap(f.mapped_at, frame_bytes_))
+    return device_failure(rc, "cache", "mem_unmap");
+  ++t_.unmaps;
+  f.mapped_at = 0;
+  return {};
+}
+
+// A frame is handed out for a new entry only after its last consumer's event
 // has retired; the host checks (and if necessary waits for) that event.
 Error Runtime::wait_retired(Frame& f) {
   if (!f.retire_pending) return {};
@@ -300,29 +379,32 @@ Error Runtime::wait_retired(Frame& f) {
   return {};
 }
 
-void Runtime::evict_key(Frame& f, bool was_dirty) {
-  if (!f.keyed) return;
+Error Runtime::evict_key(Frame& f, bool was_dirty) {
+  if (!f.keyed) return {};
   index_.erase(f.key);
   f.keyed = false;
   f.dirty = false;
   f.ready_pending = false;
   t_.resident_bytes -= frame_bytes_;
   if (was_dirty) ++t_.dirty_evictions;
+  // A chunk frame stays mapped at the chunk's address until the frame is
+  // reused (map_frame_at moves it) or the chunk is acquired again (it is then
+  // taken back without a remap).
+  return {};
 }
 
 // Frame choice (reference acquire_frame, runtime.cpp:3470-3529): the free
 // frame idle longest, else a not-yet-created frame, else the least-recently-
-// used unpinned panel — clean panels before dirty ones (a dirty victim is
+// used unpinned entry — clean entries before dirty ones (a dirty victim is
 // written back first). The choice depends only on the schedule, never on how
-// far the device has progressed, so the accounting of a run is reproducible
-// (the host-simulation build produces the same counters).
+// far the device has progressed, so the accounting of a run is reproducible.
 Error Runtime::select_frame(Frame*& out) {
   Frame* free_frame = nullptr;
-  Frame* unmapped = nullptr;
+  Frame* uncreated = nullptr;
   Frame* victim = nullptr;
   for (Frame& f : frames_) {
-    if (!f.mapped) {
-      if (!unmapped) unmapped = &f;
+    if (!f.handle) {
+      if (!uncreated) uncreated = &f;
       continue;
     }
     if (f.pins > 0) continue;
@@ -338,19 +420,12 @@ Error Runtime::select_frame(Frame*& out) {
       if (better) victim = &f;
     }
   }
-  Frame* chosen = free_frame;
-  if (!chosen && unmapped) {
-    if (Error e = ensure_frame_mapped(*unmapped)) {
-      if (e.status != XVRAM_STATUS_DEVICE_OUT_OF_MEMORY) return e;
-    } else {
-      chosen = unmapped;
-    }
-  }
+  Frame* chosen = free_frame ? free_frame : uncreated;
   if (!chosen && victim) {
     if (victim->dirty) {
       if (Error e = writeback_and_evict(*victim)) return e;
     } else {
-      evict_key(*victim, false);
+      if (Error e = evict_key(*victim, false)) return e;
       ++t_.clean_evictions;
     }
     chosen = victim;
@@ -376,6 +451,44 @@ Error Runtime::take_event(Event& out) {
   return {};
 }
 
+Error Runtime::fill_entry(Frame& f, const PanelKey& key, uint64_t packed_pitch, bool needs_data) {
+  ++t_.cache_misses;
+  f.keyed = true;
+  f.key = key;
+  f.packed_pitch = packed_pitch;
+  f.pins = 1;
+  f.dirty = false;
+  f.last_use = ++tick_;
+  index_[key] = f.index;
+  t_.resident_bytes += frame_bytes_;
+  t_.resident_bytes_peak = std::max(t_.resident_bytes_peak, t_.resident_bytes);
+  if (!needs_data) return {};
+  for (const auto& [written, done] : pending_writebacks_) {
+    // Host bytes this fill reads may still be in flight from a write-back.
+    if (!keys_overlap(written, key)) continue;
+    if (int rc = device_->stream_wait_event(h2d_, done))
+      return device_failure(rc, "cache", "stream_wait");
+  }
+  HostAllocation* a = find(key.allocation_id);
+  if (!a || key.end() > a->bytes)
+    return make_error(XVRAM_STATUS_INTERNAL, "cache", "fill", "entry outside its allocation");
+  TraceInterval iv;
+  iv.kind = 'h';
+  iv.bytes = key.bytes();
+  if (Error e = take_event(iv.start)) return e;
+  if (int rc = device_->event_record(iv.start, h2d_)) return device_failure(rc, "cache", "record");
+  if (int rc = device_->copy_h2d_2d(f.address, packed_pitch, a->host + key.offset, key.pitch,
+                                    key.width, key.height, h2d_))
+    return device_failure(rc, "cache", "copy_h2d");
+  if (Error e = take_event(iv.stop)) return e;
+  if (int rc = device_->event_record(iv.stop, h2d_)) return device_failure(rc, "cache", "record");
+  trace_.push_back(iv);
+  if (int rc = device_->event_record(f.ready, h2d_)) return device_failure(rc, "cache", "record");
+  f.ready_pending = true;
+  t_.bytes_h2d += key.bytes();
+  return {};
+}
+
 Error Runtime::acquire(const PanelKey& key, uint64_t packed_pitch, bool needs_data, Frame*& out) {
   if (poisoned_) return make_error(XVRAM_STATUS_POISONED, "cache", "acquire", "session is poisoned");
   if (packed_pitch < key.width || packed_pitch * key.height > frame_bytes_)
@@ -396,46 +509,14 @@ Error Runtime::acquire(const PanelKey& key, uint64_t packed_pitch, bool needs_da
     if (f.dirty) {
       if (Error e = writeback_and_evict(f)) return e;
     } else {
-      evict_key(f, false);
+      if (Error e = evict_key(f, false)) return e;
       ++t_.clean_evictions;
     }
   }
   Frame* f = nullptr;
   if (Error e = select_frame(f)) return e;
-  ++t_.cache_misses;
-  f->keyed = true;
-  f->key = key;
-  f->packed_pitch = packed_pitch;
-  f->pins = 1;
-  f->dirty = false;
-  f->last_use = ++tick_;
-  index_[key] = f->index;
-  t_.resident_bytes += frame_bytes_;
-  t_.resident_bytes_peak = std::max(t_.resident_bytes_peak, t_.resident_bytes);
-  if (auto wb = pending_writebacks_.find(key); wb != pending_writebacks_.end()) {
-    // The host copy of this rectangle is still being written back.
-    if (int rc = device_->stream_wait_event(h2d_, wb->second))
-      return device_failure(rc, "cache", "stream_wait");
-  }
-  if (needs_data) {
-    HostAllocation* a = find(key.allocation_id);
-    if (!a || key.end() > a->bytes)
-      return make_error(XVRAM_STATUS_INTERNAL, "cache", "acquire", "panel outside its allocation");
-    TraceInterval iv;
-    iv.kind = 'h';
-    iv.bytes = key.bytes();
-    if (Error e = take_event(iv.start)) return e;
-    if (int rc = device_->event_record(iv.start, h2d_)) return device_failure(rc, "cache", "record");
-    if (int rc = device_->copy_h2d_2d(f->address, packed_pitch, a->host + key.offset, key.pitch,
-                                      key.width, key.height, h2d_))
-      return device_failure(rc, "cache", "copy_h2d");
-    if (Error e = take_event(iv.stop)) return e;
-    if (int rc = device_->event_record(iv.stop, h2d_)) return device_failure(rc, "cache", "record");
-    trace_.push_back(iv);
-    if (int rc = device_->event_record(f->ready, h2d_)) return device_failure(rc, "cache", "record");
-    f->ready_pending = true;
-    t_.bytes_h2d += key.bytes();
-  }
+  if (Error e = map_frame_at(*f, f->slot)) return e;
+  if (Error e = fill_entry(*f, key, packed_pitch, needs_data)) return e;
   out = f;
   return {};
 }
@@ -457,14 +538,26 @@ Error Runtime::release_after(Frame& f, Stream stream, bool dirty) {
   return {};
 }
 
+// Clean, idle entries whose bytes intersect bytes just written back are stale.
+Error Runtime::drop_overlapping(const PanelKey& written, const Frame* except) {
+  for (Frame& f : frames_) {
+    if (&f == except || !f.keyed || f.pins > 0 || f.dirty) continue;
+    if (!keys_overlap(f.key, written)) continue;
+    if (Error e = wait_retired(f)) return e;
+    if (Error e = evict_key(f, false)) return e;
+    ++t_.clean_evictions;
+  }
+  return {};
+}
+
 // Dirty write-back (reference writeback, runtime.cpp:3899-4262): the D2H copy
-// is ordered after the frame's last kernel and becomes the frame's retire
-// event, so the frame is refilled only after the host rectangle is current.
+// is ordered after the frame's last consumer and becomes the frame's retire
+// event, so the frame is refilled only after the host bytes are current.
 Error Runtime::writeback_and_evict(Frame& f) {
   if (!f.keyed || !f.dirty || f.pins > 0)
-    return make_error(XVRAM_STATUS_INTERNAL, "cache", "writeback", "frame is not an idle dirty panel");
+    return make_error(XVRAM_STATUS_INTERNAL, "cache", "writeback", "frame is not an idle dirty entry");
   HostAllocation* a = find(f.key.allocation_id);
-  if (!a) return make_error(XVRAM_STATUS_INTERNAL, "cache", "writeback", "panel owner is gone");
+  if (!a) return make_error(XVRAM_STATUS_INTERNAL, "cache", "writeback", "entry owner is gone");
   if (f.retire_pending)
     if (int rc = device_->stream_wait_event(d2h_, f.retire))
       return device_failure(rc, "cache", "stream_wait");
@@ -481,26 +574,33 @@ Error Runtime::writeback_and_evict(Frame& f) {
   trace_.push_back(iv);
   if (int rc = device_->event_record(f.retire, d2h_)) return device_failure(rc, "cache", "record");
   f.retire_pending = true;
-  pending_writebacks_[f.key] = iv.stop;
-  t_.bytes_d2h += f.key.bytes();
+  const PanelKey written = f.key;
+  pending_writebacks_[written] = iv.stop;
+  t_.bytes_d2h += written.bytes();
   ++t_.writebacks_completed;
-  evict_key(f, true);
-  return {};
+  if (Error e = evict_key(f, true)) return e;
+  return drop_overlapping(written, &f);
 }
 
 Error Runtime::invalidate(uint64_t allocation_id, uint64_t begin, uint64_t end) {
+  if (end <= begin) return {};
+  PanelKey range;
+  range.allocation_id = allocation_id;
+  range.offset = begin;
+  range.width = end - begin;
+  range.height = 1;
+  range.pitch = end - begin;
+  range.kind = EntryKind::chunk;
   for (Frame& f : frames_) {
-    if (!f.keyed || f.key.allocation_id != allocation_id) continue;
-    if (f.key.offset >= end || f.key.end() <= begin) continue;
+    if (!f.keyed || !keys_overlap(f.key, range)) continue;
     if (f.pins > 0)
-      return make_error(XVRAM_STATUS_BUSY, "cache", "invalidate", "panel is in use by an operation");
+      return make_error(XVRAM_STATUS_BUSY, "cache", "invalidate", "entry is in use by an operation");
     if (f.dirty) {
       if (Error e = writeback_and_evict(f)) return e;
-      for (Stream s : {d2h_})
-        if (int rc = device_->stream_sync(s)) return device_failure(rc, "cache", "stream_sync");
+      if (int rc = device_->stream_sync(d2h_)) return device_failure(rc, "cache", "stream_sync");
     } else {
       if (Error e = wait_retired(f)) return e;
-      evict_key(f, false);
+      if (Error e = evict_key(f, false)) return e;
       ++t_.clean_evictions;
     }
   }
@@ -509,17 +609,268 @@ Error Runtime::invalidate(uint64_t allocation_id, uint64_t begin, uint64_t end) 
 
 void Runtime::discard_dirty() {
   for (Frame& f : frames_) {
-    if (f.keyed && f.dirty) {
-      f.pins = 0;
-      evict_key(f, false);
-    }
     f.pins = 0;
+    if (f.keyed && f.dirty) (void)evict_key(f, false);
   }
 }
 
+// ---- transactions and prefetch -----------------------------------------------
+
+Error Runtime::reserve_allocation_va(HostAllocation& a) {
+  if (a.va) return {};
+  const uint64_t bytes = round_up(a.bytes, frame_bytes_);
+  uint64_t va = 0;
+  if (int rc = device_->va_reserve(bytes, granularity_, &va))
+    return device_failure(rc, "transaction", "va_reserve");
+  a.va = va;
+  a.va_bytes = bytes;
+  return {};
+}
+
+// One workspace region of the session's workspace cap, created on first use
+// (the cap is already excluded from the frame budget).
+Error Runtime::ensure_workspace(uint64_t bytes) {
+  if (bytes == 0 || workspace_va_) return {};
+  const uint64_t size = round_up(std::max<uint64_t>(config_.workspace_reserve_bytes, 1), granularity_);
+  uint64_t va = 0, handle = 0;
+  if (int rc = device_->va_reserve(size, granularity_, &va))
+    return device_failure(rc, "transaction", "workspace_reserve");
+  if (int rc = device_->mem_create(size, &handle)) {
+    (void)device_->va_free(va, size);
+    return device_failure(rc, "transaction", "workspace_create");
+  }
+  ++t_.physical_handles_created;
+  if (int rc = device_->mem_map(va, size, handle)) return device_failure(rc, "transaction", "workspace_map");
+  ++t_.mappings;
+  if (int rc = device_->set_access(va, size)) return device_failure(rc, "transaction", "workspace_access");
+  ++t_.set_access_calls;
+  workspace_va_ = va;
+  workspace_bytes_ = size;
+  workspace_handle_ = handle;
+  t_.workspace_bytes = size;
+  return {};
+}
+
+// Normalisation and chunk split (reference core::normalize_and_split_accesses,
+// src/residency/core.cpp:128-276): overlapping accesses merge with their modes
+// combined; each touched chunk records whether it must be loaded (anything but
+// one write-only span covering the whole chunk) and whether it is written.
+Error Runtime::plan_chunks(const std::vector<AccessSpan>& ranges, std::vector<ChunkUse>& chunks,
+                           std::vector<AccessSpan>& normalized, const char* operation) {
+  chunks.clear();
+  normalized.clear();
+  const auto rejected = [&](const char* reason) {
+    return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "transaction", operation,
+                      std::string("invalid access ranges: ") + reason);
+  };
+  if (ranges.empty()) return rejected("zero_length");
+  std::map<uint64_t, std::vector<AccessSpan>> by_alloc;
+  for (const AccessSpan& r : ranges) {
+    if (r.mode != XVRAM_ACCESS_READ && r.mode != XVRAM_ACCESS_READ_WRITE &&
+        r.mode != XVRAM_ACCESS_WRITE_ONLY)
+      return rejected("invalid_access_mode");
+    if (r.length == 0) return rejected("zero_length");
+    HostAllocation* a = find(r.allocation_id);
+    uint64_t end = 0;
+    if (!a) return rejected("unknown_allocation");
+    if (!checked_add(r.offset, r.length, end)) return rejected("range_overflow");
+    if (r.offset >= a->bytes || end > a->bytes) return rejected("range_out_of_bounds");
+    by_alloc[r.allocation_id].push_back(r);
+  }
+  for (auto& [id, list] : by_alloc) {
+    std::vector<uint64_t> cuts;
+    for (const AccessSpan& r : list) {
+      cuts.push_back(r.offset);
+      cuts.push_back(r.offset + r.length);
+    }
+    std::sort(cuts.begin(), cuts.end());
+    cuts.erase(std::unique(cuts.begin(), cuts.end()), cuts.end());
+    for (size_t i = 0; i + 1 < cuts.size(); ++i) {
+      const uint64_t lo = cuts[i], hi = cuts[i + 1];
+      bool covered = false;
+      uint32_t mode = XVRAM_ACCESS_READ;
+      for (const AccessSpan& r : list) {
+        if (r.offset <= lo && hi <= r.offset + r.length) {
+          mode = covered ? combine_modes(mode, r.mode) : r.mode;
+          covered = true;
+        }
+      }
+      if (!covered) continue;
+      if (!normalized.empty() && normalized.back().allocation_id == id &&
+          normalized.back().offset + normalized.back().length == lo && normalized.back().mode == mode) {
+        normalized.back().length += hi - lo;
+      } else {
+        normalized.push_back(AccessSpan{id, lo, hi - lo, mode});
+      }
+    }
+  }
+  for (const AccessSpan& s : normalized) {
+    const HostAllocation* a = find(s.allocation_id);
+    const uint64_t first = s.offset / frame_bytes_, last = (s.offset + s.length - 1) / frame_bytes_;
+    for (uint64_t c = first; c <= last; ++c) {
+      const uint64_t c_lo = c * frame_bytes_;
+      const uint64_t c_hi = std::min(a->bytes, c_lo + frame_bytes_);
+      const uint64_t lo = std::max(s.offset, c_lo), hi = std::min(s.offset + s.length, c_hi);
+      const bool full_write_only = s.mode == XVRAM_ACCESS_WRITE_ONLY && lo == c_lo && hi == c_hi;
+      if (chunks.empty() || chunks.back().allocation_id != s.allocation_id ||
+          chunks.back().index != c) {
+        ChunkUse u;
+        u.allocation_id = s.allocation_id;
+        u.index = c;
+        u.needs_data = !full_write_only;
+        u.writes = s.mode != XVRAM_ACCESS_READ;
+        chunks.push_back(u);
+      } else {
+        // A second span in the same chunk: the chunk is no longer one full write-only span.
+        chunks.back().needs_data = true;
+        chunks.back().writes = chunks.back().writes || s.mode != XVRAM_ACCESS_READ;
+      }
+    }
+  }
+  return {};
+}
+
+Error Runtime::acquire_chunk(ChunkUse& use) {
+  HostAllocation* a = find(use.allocation_id);
+  if (!a) return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "transaction", "acquire", "unknown allocation");
+  if (Error e = reserve_allocation_va(*a)) return e;
+  PanelKey key;
+  key.allocation_id = use.allocation_id;
+  key.offset = use.index * frame_bytes_;
+  key.width = std::min(frame_bytes_, a->bytes - key.offset);
+  key.height = 1;
+  key.pitch = key.width;
+  key.kind = EntryKind::chunk;
+  auto it = index_.find(key);
+  if (it != index_.end()) {
+    Frame& f = frames_[it->second];
+    ++f.pins;
+    f.last_use = ++tick_;
+    ++t_.cache_hits;
+    use.frame = &f;
+    return {};
+  }
+  const uint64_t address = a->va + key.offset;
+  Frame* f = nullptr;
+  for (Frame& g : frames_) {
+    // The frame that last held this chunk may still be mapped at its address.
+    if (g.mapped_at == address && !g.keyed && g.pins == 0) {
+      if (Error e = wait_retired(g)) return e;
+      ++t_.handle_reuses;
+      f = &g;
+      break;
+    }
+  }
+  if (!f)
+    if (Error e = select_frame(f)) return e;
+  if (Error e = map_frame_at(*f, address)) return e;
+  use.frame = f;
+  use.filled_empty = !use.needs_data;
+  return fill_entry(*f, key, key.width, use.needs_data);
+}
+
+// A working-set transaction (reference Runtime::execute/acquire_external/
+// seal/poll, runtime.cpp:1012-1495): make every touched chunk resident at its
+// stable address, run the caller's work on the compute stream, write back what
+// it wrote, and measure the work's GPU time against the duration guard.
+Error Runtime::run_transaction(const std::vector<AccessSpan>& ranges, uint64_t workspace_bytes,
+                               const TransactionBody& body, uint64_t operation_id) {
+  if (Error e = begin_operation()) return e;
+  std::vector<ChunkUse> chunks;
+  std::vector<AccessSpan> normalized;
+  Error result = plan_chunks(ranges, chunks, normalized, "normalize_accesses");
+  if (!result && chunks.size() > capacity_)
+    result = make_error(XVRAM_STATUS_BUDGET_PRESSURE, "transaction", "working_set",
+                        "declared working set exceeds the cache target");
+  if (!result) result = ensure_workspace(workspace_bytes);
+  for (size_t i = 0; !result && i < chunks.size(); ++i)
+    if (Error e = acquire_chunk(chunks[i])) result = e;
+  // Leaves the cache as if the callback had never run: unpins, and drops every
+  // chunk the work may have written or that was mapped without its data.
+  const auto abandon = [&]() {
+    for (ChunkUse& u : chunks) {
+      if (!u.frame) continue;
+      if (u.frame->pins > 0) --u.frame->pins;
+      if (u.writes || u.filled_empty) {
+        u.frame->dirty = false;
+        (void)evict_key(*u.frame, false);
+      }
+    }
+  };
+  if (result) {
+    abandon();
+    (void)finish_operation(operation_id);
+    return result;
+  }
+  for (ChunkUse& u : chunks)
+    if (Error e = wait_ready(*u.frame, compute_)) return e;
+  std::vector<ResolvedSpan> resolved;
+  resolved.reserve(normalized.size());
+  for (const AccessSpan& s : normalized)
+    resolved.push_back(ResolvedSpan{s, find(s.allocation_id)->va + s.offset});
+  TraceInterval iv;
+  iv.kind = 't';
+  if (Error e = record_kernel(iv.start, iv.stop)) return e;
+  if (int rc = device_->event_record(iv.start, compute_)) return device_failure(rc, "transaction", "record");
+  bool skipped = false;
+  Error body_error;
+  try {
+    body_error = body(resolved, workspace_bytes ? workspace_va_ : 0, workspace_bytes, compute_, skipped);
+  } catch (...) {
+    body_error = exception_error("transaction_callback");
+    body_error.status = XVRAM_STATUS_CALLBACK_FAILED;
+  }
+  if (int rc = device_->event_record(iv.stop, compute_)) return device_failure(rc, "transaction", "record");
+  if (body_error) {
+    // A skipped callback enqueued nothing; a failed one may have enqueued work
+    // (the reference's failed_after_possible_submission), which poisons the
+    // session once the streams have drained.
+    abandon();
+    (void)finish_operation(operation_id);
+    if (!skipped) {
+      poisoned_ = true;
+      t_.poisoned = 1;
+    }
+    return body_error;
+  }
+  trace_.push_back(iv);
+  for (ChunkUse& u : chunks)
+    if (Error e = release_after(*u.frame, compute_, u.writes)) return e;
+  for (ChunkUse& u : chunks) {
+    if (u.frame->dirty)
+      if (Error e = writeback_and_evict(*u.frame)) return e;
+  }
+  ++transactions_in_operation_;
+  return finish_operation(operation_id);
+}
+
+Error Runtime::run_prefetch(const std::vector<AccessSpan>& ranges, uint64_t operation_id) {
+  if (Error e = begin_operation()) return e;
+  std::vector<ChunkUse> chunks;
+  std::vector<AccessSpan> normalized;
+  Error result = plan_chunks(ranges, chunks, normalized, "prefetch");
+  if (!result && chunks.size() > capacity_)
+    result = make_error(XVRAM_STATUS_BUDGET_PRESSURE, "transaction", "prefetch",
+                        "prefetch working set exceeds the cache target");
+  for (size_t i = 0; !result && i < chunks.size(); ++i) {
+    chunks[i].needs_data = true; // a prefetched chunk must hold valid data
+    if (Error e = acquire_chunk(chunks[i])) result = e;
+    else result = release_after(*chunks[i].frame, h2d_, false);
+  }
+  Error finish = finish_operation(operation_id);
+  return result ? result : finish;
+}
+
+// ---- operation bracketing ------------------------------------------------------
+
 Error Runtime::begin_operation() {
   if (poisoned_) return make_error(XVRAM_STATUS_POISONED, "operation", "begin", "session is poisoned");
+  if (launches_blocked_)
+    return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "operation", "begin",
+                      "runtime is not ready: launches are blocked after device work exceeded "
+                      "the transaction duration guard");
   kernels_in_operation_ = 0;
+  transactions_in_operation_ = 0;
   trace_.clear();
   if (int rc = device_->event_record(op_start_, compute_)) return device_failure(rc, "operation", "record");
   for (Stream s : {h2d_, d2h_})
@@ -532,8 +883,10 @@ Error Runtime::record_kernel(Event& start, Event& stop) {
   return take_event(stop);
 }
 
-// End of an operation: wait for the three streams, then fold the kernel and
-// copy intervals into telemetry (and the optional trace file).
+// End of an operation: wait for the three streams, fold the kernel, callback
+// and copy intervals into telemetry (and the optional trace file), and apply
+// the duration guard (reference runtime.cpp:1396-1408: work longer than
+// max_transaction_ms blocks further launches and fails with a timeout).
 Error Runtime::finish_operation(uint64_t operation_id) {
   Error first;
   for (Stream s : {h2d_, compute_, d2h_}) {
@@ -546,13 +899,14 @@ Error Runtime::finish_operation(uint64_t operation_id) {
     if (!first) f.retire_pending = false;
   }
   pending_writebacks_.clear();
+  bool guard_tripped = false;
   if (!first) {
     FILE* out = nullptr;
     if (tracing()) out = std::fopen(trace_path_.c_str(), "a");
     if (out) std::fprintf(out, "{\"operation_id\": %llu", static_cast<unsigned long long>(operation_id));
-    const char* names[3] = {"kernels", "h2d", "d2h"};
-    const char kinds[3] = {'k', 'h', 'd'};
-    for (int c = 0; c < 3; ++c) {
+    const char* names[4] = {"kernels", "h2d", "d2h", "transactions"};
+    const char kinds[4] = {'k', 'h', 'd', 't'};
+    for (int c = 0; c < 4; ++c) {
       if (out) std::fprintf(out, ", \"%s\": [", names[c]);
       bool comma = false;
       for (const TraceInterval& iv : trace_) {
@@ -560,9 +914,14 @@ Error Runtime::finish_operation(uint64_t operation_id) {
         float s = 0.f, e = 0.f;
         if (device_->event_elapsed_ms(&s, op_start_, iv.start) != 0) s = 0.f;
         if (device_->event_elapsed_ms(&e, op_start_, iv.stop) != 0) e = s;
-        if (iv.kind == 'k') {
+        if (iv.kind == 'k' || iv.kind == 't') {
           float d = 0.f;
-          if (device_->event_elapsed_ms(&d, iv.start, iv.stop) == 0) t_.last_transaction_ms = d;
+          if (device_->event_elapsed_ms(&d, iv.start, iv.stop) == 0) {
+            t_.last_transaction_ms = d;
+            if (config_.max_transaction_ms > 0 &&
+                static_cast<double>(d) > static_cast<double>(config_.max_transaction_ms))
+              guard_tripped = true;
+          }
         }
         if (out) {
           std::fprintf(out, "%s[%.6f, %.6f, %llu]", comma ? ", " : "", s, e,
@@ -576,11 +935,12 @@ Error Runtime::finish_operation(uint64_t operation_id) {
       std::fprintf(out, "}\n");
       std::fclose(out);
     }
-    t_.transactions_completed += kernels_in_operation_;
+    t_.transactions_completed += kernels_in_operation_ + transactions_in_operation_;
     t_.algorithm_selections += kernels_in_operation_;
   }
   trace_.clear();
   kernels_in_operation_ = 0;
+  transactions_in_operation_ = 0;
   for (Event e : events_in_use_) event_pool_.push_back(e);
   events_in_use_.clear();
   uint64_t free_bytes = 0, total_bytes = 0;
@@ -588,6 +948,12 @@ Error Runtime::finish_operation(uint64_t operation_id) {
     ++t_.budget_sample_count;
     t_.cuda_free_bytes_minimum = std::min(t_.cuda_free_bytes_minimum, free_bytes);
     t_.cuda_free_bytes_end = free_bytes;
+  }
+  if (!first && guard_tripped) {
+    launches_blocked_ = true;
+    ++t_.watchdog_rejections;
+    return make_error(XVRAM_STATUS_TIMEOUT, "transaction", "duration_guard",
+                      "device work exceeded the configured transaction duration");
   }
   return first;
 }

@@ -1,24 +1,31 @@
-// runtime.hpp — host backing, the VRAM frame pool and the panel cache.
+// runtime.hpp — host backing, the VRAM frame pool and the residency cache.
 //
 // Reference counterpart: residency::Runtime (src/residency/runtime.hpp:317-372,
-// runtime.cpp:212-596 setup, :3470-3529 acquire_frame, :3531-3897
-// ensure_resident, :3899-4262 writeback, :1540-1857 close). The reference
-// caches 64 MiB linear chunks of each allocation; a column panel with a large
-// leading dimension touches every chunk. This runtime caches *panels*: the
-// unit of residency is one packed 2-D sub-matrix (a strided rectangle of an
-// allocation), copied with one hipMemcpy2DAsync into one frame.
+// runtime.cpp:212-596 setup, :598-727 allocate, :1012-1495 transactions,
+// :3470-3529 acquire_frame, :3531-3897 ensure_resident, :3899-4262 writeback,
+// :1540-1857 close).
 //
-// Frames: `capacity` physical handles of `frame_bytes` each (hipMemCreate),
-// created lazily and mapped once into a single hipMemAddressReserve arena
-// under the budget `target_bytes`. A frame is refilled only after the host has
-// seen the hipEvent of its last consumer (the last kernel that read it, or the
-// write-back copy that drained it) complete.
+// Cache entries come in two kinds:
+//   * panels — a packed 2-D sub-matrix (a strided rectangle of an allocation)
+//     filled with one hipMemcpy2DAsync; the GEMM executor's unit. Panel frames
+//     live at their fixed slot in one hipMemAddressReserve arena.
+//   * chunks — frame-sized linear pieces of an allocation used by working-set
+//     transactions and prefetch; a chunk frame is mapped at the chunk's stable
+//     address inside the allocation's own VA reservation (reserved on first
+//     use), so a transaction sees each allocation as one contiguous range.
+// Frames are `frame_bytes` hipMemCreate handles, created lazily up to the
+// budget. A frame is refilled, unmapped or remapped only after the host has
+// seen the hipEvent of its last consumer (kernel, callback work or write-back)
+// complete. Dirty entries are written back before the operation that dirtied
+// them completes; clean entries overlapping written-back bytes are dropped.
 //
-// Streams: one compute stream (tile kernels), one H2D copy stream and one D2H
-// copy stream, all at the default priority; they are ordered with events only.
+// Streams: one compute stream (tile kernels, transaction callbacks), one H2D
+// copy stream and one D2H copy stream, all at the default priority; ordered
+// with events only.
 #pragma once
 
 #include <cstdint>
+#include <functional>
 #include <map>
 #include <memory>
 #include <string>
@@ -45,24 +52,31 @@ struct HostAllocation {
   uint64_t bytes = 0;
   uint64_t alignment = 0;
   uint32_t priority = 0;
-  char* host = nullptr; // pinned backing store (authoritative copy)
+  char* host = nullptr;  // pinned backing store (authoritative copy)
+  uint64_t va = 0;       // stable device VA for chunk mappings (0 until first use)
+  uint64_t va_bytes = 0;
 };
 
+enum class EntryKind : uint32_t { panel = 0, chunk = 1 };
+
 // A strided rectangle of an allocation: `height` lines of `width` bytes, the
-// first at byte `offset`, consecutive lines `pitch` bytes apart.
+// first at byte `offset`, consecutive lines `pitch` bytes apart (a chunk is one
+// line).
 struct PanelKey {
   uint64_t allocation_id = 0;
   uint64_t offset = 0;
   uint64_t width = 0;
   uint64_t height = 0;
   uint64_t pitch = 0;
+  EntryKind kind = EntryKind::panel;
 
   bool operator==(const PanelKey& o) const {
     return allocation_id == o.allocation_id && offset == o.offset && width == o.width &&
-           height == o.height && pitch == o.pitch;
+           height == o.height && pitch == o.pitch && kind == o.kind;
   }
   bool operator<(const PanelKey& o) const {
     if (allocation_id != o.allocation_id) return allocation_id < o.allocation_id;
+    if (kind != o.kind) return kind < o.kind;
     if (offset != o.offset) return offset < o.offset;
     if (width != o.width) return width < o.width;
     if (height != o.height) return height < o.height;
@@ -72,11 +86,16 @@ struct PanelKey {
   uint64_t bytes() const { return width * height; }
 };
 
+// True when the byte sets of two rectangles of one allocation intersect
+// (exact for rectangles of equal pitch, conservative otherwise).
+bool keys_overlap(const PanelKey& a, const PanelKey& b);
+
 struct Frame {
   uint64_t index = 0;
-  uint64_t address = 0;
-  uint64_t handle = 0;
-  bool mapped = false;
+  uint64_t slot = 0;      // this frame's address in the panel arena
+  uint64_t address = 0;   // where the current entry is mapped
+  uint64_t mapped_at = 0; // current mapping (0 = unmapped)
+  uint64_t handle = 0;    // physical handle (0 = not created yet)
   bool keyed = false;
   PanelKey key;
   uint64_t packed_pitch = 0;
@@ -95,8 +114,27 @@ struct TraceInterval {
   Event start = nullptr;
   Event stop = nullptr;
   uint64_t bytes = 0;
-  char kind = 'k'; // 'k' kernel, 'h' H2D, 'd' D2H
+  char kind = 'k'; // 'k' kernel, 'h' H2D, 'd' D2H, 't' transaction callback work
 };
+
+// One access of a working-set transaction (allocation-relative bytes).
+struct AccessSpan {
+  uint64_t allocation_id = 0;
+  uint64_t offset = 0;
+  uint64_t length = 0;
+  uint32_t mode = XVRAM_ACCESS_READ;
+};
+
+struct ResolvedSpan {
+  AccessSpan span;
+  uint64_t device_address = 0;
+};
+
+// The work a transaction enqueues with its working set resident. Returns an
+// error to fail the transaction; `skipped` reports that nothing was enqueued.
+using TransactionBody =
+    std::function<Error(const std::vector<ResolvedSpan>& ranges, uint64_t workspace_address,
+                        uint64_t workspace_bytes, Stream stream, bool& skipped)>;
 
 class Runtime {
 public:
@@ -123,7 +161,7 @@ public:
   Error read(uint64_t id, uint64_t offset, void* destination, uint64_t bytes);
   HostAllocation* find(uint64_t id);
 
-  // ---- panel cache ----
+  // ---- panel cache (GEMM) ----
   // Makes `key` resident in a frame with packed line pitch `packed_pitch` and
   // pins it. needs_data=false (a write-only panel) skips the H2D copy.
   Error acquire(const PanelKey& key, uint64_t packed_pitch, bool needs_data, Frame*& out);
@@ -131,17 +169,26 @@ public:
   Error wait_ready(Frame& frame, Stream stream);
   // Unpins after the consumer enqueued on `stream`; records the retire event.
   Error release_after(Frame& frame, Stream stream, bool dirty);
-  // Writes a dirty panel back to its host rectangle (D2H stream, ordered after
-  // the frame's last consumer) and removes it from the cache.
+  // Writes a dirty entry back to its host bytes (D2H stream, ordered after the
+  // frame's last consumer), removes it from the cache and drops clean entries
+  // that overlap the written bytes.
   Error writeback_and_evict(Frame& frame);
-  // Drops every cached panel (write-back first if dirty=keep) of an allocation
-  // overlapping [begin, end); used by allocation_write and release.
+  // Drops every cached entry of an allocation overlapping [begin, end);
+  // used by allocation_write and release.
   Error invalidate(uint64_t allocation_id, uint64_t begin, uint64_t end);
-  // Discards dirty panels without writing them back (failed operation).
+  // Discards dirty entries without writing them back (failed operation).
   void discard_dirty();
+
+  // ---- working-set transactions and prefetch ----
+  Error run_transaction(const std::vector<AccessSpan>& ranges, uint64_t workspace_bytes,
+                        const TransactionBody& body, uint64_t operation_id);
+  Error run_prefetch(const std::vector<AccessSpan>& ranges, uint64_t operation_id);
+
+  // ---- operation bracketing ----
   // Marks the start of an operation: every stream is ordered after it.
   Error begin_operation();
-  // Waits for every stream; records trace intervals of the finished operation.
+  // Waits for every stream; folds kernel/copy intervals into telemetry, applies
+  // the duration guard, writes the optional trace line.
   Error finish_operation(uint64_t operation_id);
 
   // Kernel bookkeeping used by the executor.
@@ -159,10 +206,27 @@ public:
   void trace_push(const TraceInterval& interval) { trace_.push_back(interval); }
 
 private:
-  Error ensure_frame_mapped(Frame& frame);
+  struct ChunkUse {
+    uint64_t allocation_id = 0;
+    uint64_t index = 0;
+    bool needs_data = true;
+    bool writes = false;
+    bool filled_empty = false; // mapped on a miss without loading its bytes
+    Frame* frame = nullptr;
+  };
+
+  Error map_frame_at(Frame& frame, uint64_t address);
+  Error unmap_frame(Frame& frame);
   Error select_frame(Frame*& out);
+  Error fill_entry(Frame& f, const PanelKey& key, uint64_t packed_pitch, bool needs_data);
   Error wait_retired(Frame& frame);
-  void evict_key(Frame& frame, bool was_dirty);
+  Error evict_key(Frame& frame, bool was_dirty);
+  Error drop_overlapping(const PanelKey& written, const Frame* except);
+  Error reserve_allocation_va(HostAllocation& a);
+  Error ensure_workspace(uint64_t bytes);
+  Error plan_chunks(const std::vector<AccessSpan>& ranges, std::vector<ChunkUse>& chunks,
+                    std::vector<AccessSpan>& normalized, const char* operation);
+  Error acquire_chunk(ChunkUse& use);
   void parallel_copy(void* dst, const void* src, uint64_t bytes);
 
   RuntimeConfig config_;
@@ -170,6 +234,7 @@ private:
   bool setup_done_ = false;
   bool closed_ = false;
   bool poisoned_ = false;
+  bool launches_blocked_ = false;
 
   uint64_t granularity_ = 0;
   uint64_t frame_bytes_ = 0;
@@ -180,6 +245,10 @@ private:
   std::vector<Frame> frames_;
   std::map<PanelKey, uint64_t> index_; // key -> frame index
   uint64_t tick_ = 0;
+
+  uint64_t workspace_va_ = 0;
+  uint64_t workspace_bytes_ = 0;
+  uint64_t workspace_handle_ = 0;
 
   Stream compute_ = nullptr;
   Stream h2d_ = nullptr;
@@ -193,12 +262,13 @@ private:
   uint64_t pinned_bytes_ = 0;
 
   // Write-backs still in flight in this operation: a later refill of the same
-  // panel waits for them.
+  // entry waits for them.
   std::map<PanelKey, Event> pending_writebacks_;
 
   std::string trace_path_;
   std::vector<TraceInterval> trace_;
   uint64_t kernels_in_operation_ = 0;
+  uint64_t transactions_in_operation_ = 0;
 
   xvram_session_telemetry_v1 t_{};
 };

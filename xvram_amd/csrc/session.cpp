@@ -319,8 +319,10 @@ Error Session::create_gemm_plan(const GemmSpec& spec_in, std::shared_ptr<Allocat
     record->b = b;
     record->c = c;
     record->deadline_ms = deadline_ms;
+    const double cap = static_cast<double>(runtime_.config().max_transaction_ms) *
+                       kGuardPlanningFlopsPerMs;
     return make_gemm_plan(spec, runtime_.frame_bytes(), runtime_.frame_capacity(),
-                          config_.prefetch_distance, record->plan);
+                          config_.prefetch_distance, static_cast<uint64_t>(cap), record->plan);
   });
   if (e) return e;
   out = std::move(record);
@@ -344,6 +346,101 @@ Error Session::submit_gemm(const std::shared_ptr<GemmPlanRecord>& plan,
         return execute_gemm(runtime_, plan->plan, op.id(), hooks);
       },
       units, plan->deadline_ms, out);
+}
+
+namespace {
+
+// src/sdk/runtime.cpp:827-842: a released allocation cannot be named.
+Error convert_accesses(const std::vector<Session::Access>& in, std::vector<AccessSpan>& out,
+                       const char* operation) {
+  out.clear();
+  out.reserve(in.size());
+  for (const Session::Access& a : in) {
+    if (!a.allocation || a.allocation->released)
+      return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "transaction", operation,
+                        "allocation is released or belongs to another backend");
+    out.push_back(AccessSpan{a.allocation->id, a.offset, a.length, a.mode});
+  }
+  return {};
+}
+
+template <size_t N>
+std::string bounded_text(const char (&text)[N]) {
+  size_t n = 0;
+  while (n < N && text[n] != '\0') ++n;
+  return std::string(text, n);
+}
+
+} // namespace
+
+// src/sdk/runtime.cpp:394-414.
+Error Session::submit_prefetch(std::vector<Access> accesses, uint64_t deadline_ms,
+                               std::shared_ptr<Operation>& out) {
+  std::vector<AccessSpan> spans;
+  if (Error e = convert_accesses(accesses, spans, "prefetch")) return e;
+  return enqueue(
+      [this, spans = std::move(spans), accesses = std::move(accesses)](Operation& op) -> Error {
+        if (Error d = op.deadline_error("operation", "pre_launch_deadline")) return d;
+        return runtime_.run_prefetch(spans, op.id());
+      },
+      1, deadline_ms, out);
+}
+
+// src/sdk/runtime.cpp:416-499: the callback runs on the worker with the
+// working set resident, sees the resolved stable addresses and the compute
+// stream, and its failure is reported with the callback's own status and
+// error text (native domain CALLBACK).
+Error Session::submit_transaction(std::vector<Access> accesses, uint64_t workspace_bytes,
+                                  uint64_t deadline_ms, xvram_transaction_callback_v1 callback,
+                                  void* user_data, std::shared_ptr<Operation>& out) {
+  if (workspace_bytes > config_.workspace_cap_bytes)
+    return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "transaction", "workspace",
+                      "transaction workspace exceeds the session workspace cap");
+  std::vector<AccessSpan> spans;
+  if (Error e = convert_accesses(accesses, spans, "transaction")) return e;
+  const uint64_t transaction_id = next_transaction_id_.fetch_add(1);
+  return enqueue(
+      [this, spans = std::move(spans), accesses = std::move(accesses), workspace_bytes, callback,
+       user_data, transaction_id](Operation& op) -> Error {
+        if (Error d = op.deadline_error("operation", "pre_launch_deadline")) return d;
+        TransactionBody body = [&](const std::vector<ResolvedSpan>& ranges, uint64_t ws_address,
+                                   uint64_t ws_bytes, Stream stream, bool& skipped) -> Error {
+          if (Error d = op.deadline_error("operation", "post_residency_deadline")) {
+            skipped = true;
+            return d;
+          }
+          std::vector<xvram_resolved_range_v1> resolved;
+          resolved.reserve(ranges.size());
+          for (const ResolvedSpan& r : ranges)
+            resolved.push_back(xvram_resolved_range_v1{r.span.allocation_id, r.span.offset,
+                                                       r.span.length, r.device_address,
+                                                       r.span.mode, 0u});
+          xvram_transaction_context_v1 context{};
+          context.struct_size = sizeof(context);
+          context.operation_id = op.id();
+          context.transaction_id = transaction_id;
+          context.ranges = resolved.data();
+          context.range_count = resolved.size();
+          context.workspace_device_address = ws_address;
+          context.workspace_bytes = ws_bytes;
+          context.native_stream = static_cast<uint64_t>(reinterpret_cast<uintptr_t>(stream));
+          xvram_error_info_v1 native = XVRAM_ERROR_INFO_V1_INIT;
+          const xvram_status status = callback(&context, user_data, &native);
+          if (status == XVRAM_STATUS_SUCCESS) return {};
+          Error e;
+          e.status = status;
+          e.native_domain = XVRAM_NATIVE_ERROR_CALLBACK;
+          e.native_code = native.native_code;
+          e.stage = bounded_text(native.stage);
+          e.operation = bounded_text(native.operation);
+          e.native_name = bounded_text(native.native_name);
+          e.message = bounded_text(native.message);
+          if (e.message.empty()) e.message = "transaction callback failed";
+          return e;
+        };
+        return runtime_.run_transaction(spans, workspace_bytes, body, op.id());
+      },
+      1, deadline_ms, out);
 }
 
 Error Session::telemetry(xvram_session_telemetry_v1& out) const {

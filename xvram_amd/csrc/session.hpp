@@ -87,6 +87,20 @@ public:
                          uint64_t deadline_ms, std::shared_ptr<GemmPlanRecord>& out);
   Error submit_gemm(const std::shared_ptr<GemmPlanRecord>& plan, std::shared_ptr<Operation>& out);
 
+  // One access of a transaction or prefetch, with the record kept alive until
+  // the operation has run.
+  struct Access {
+    std::shared_ptr<AllocationRecord> allocation;
+    uint64_t offset = 0;
+    uint64_t length = 0;
+    uint32_t mode = XVRAM_ACCESS_READ;
+  };
+  Error submit_prefetch(std::vector<Access> accesses, uint64_t deadline_ms,
+                        std::shared_ptr<Operation>& out);
+  Error submit_transaction(std::vector<Access> accesses, uint64_t workspace_bytes,
+                           uint64_t deadline_ms, xvram_transaction_callback_v1 callback,
+                           void* user_data, std::shared_ptr<Operation>& out);
+
   Error telemetry(xvram_session_telemetry_v1& out) const;
   Error drain(uint64_t timeout_ms);
   Error close(uint64_t timeout_ms);
@@ -125,6 +139,7 @@ private:
   Error setup_error_;
   std::shared_ptr<Operation> close_operation_;
   std::atomic<uint64_t> next_operation_id_{1};
+  std::atomic<uint64_t> next_transaction_id_{1};
 
   mutable std::mutex telemetry_mutex_;
   xvram_session_telemetry_v1 telemetry_{};
