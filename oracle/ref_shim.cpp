@@ -1,14 +1,21 @@
 // ref_shim.cpp — C entry points over the reference's own planner and pattern
 // sources, compiled in place from /root/reference by oracle/Makefile into
 // oracle/_ref/libxvram_ref.so. TEST INFRASTRUCTURE ONLY: used by tests/ to
-// pin the oracle's pattern restatement and the library's GEMM-problem
-// validation against the reference implementation itself.
+// pin the oracle's pattern restatement, the library's GEMM-problem
+// validation, its access normalisation and its entry-state table against the
+// reference implementation itself.
 //   - ref_pattern_*      -> src/gemm_bench/pattern.cpp:207-237
 //   - ref_validate_problem -> src/gemm/planner.cpp:785-859
+//   - ref_legal_transition -> src/residency/core.cpp:304-332
+//   - ref_normalize        -> src/residency/core.cpp:128-276
 #include "gemm/planner.hpp"
 #include "gemm_bench/pattern.hpp"
+#include "residency/core.hpp"
 
 #include <cstdint>
+#include <cstdio>
+#include <string>
+#include <vector>
 
 extern "C" {
 
@@ -65,5 +72,55 @@ int ref_validate_problem(const RefMatrix* a, const RefMatrix* b, const RefMatrix
                                 : (compute == 1 ? ComputeMode::fast_tf32 : ComputeMode::strict_fp32);
   p.beta = beta;
   return static_cast<int>(validate_problem(p).error);
+}
+
+int ref_legal_transition(int from, int to) {
+  using xvram::residency::ChunkState;
+  return xvram::residency::is_legal_transition(static_cast<ChunkState>(from),
+                                               static_cast<ChunkState>(to))
+             ? 1
+             : 0;
+}
+
+// Same flat-array contract as the library's hostsim hook: allocations as
+// (id, bytes), ranges as (id, offset, length, mode); outputs normalised ranges
+// as quads and chunks as (id, index, valid_bytes, requires_h2d, marks_dirty).
+int ref_normalize(const uint64_t* allocs, uint64_t n_allocs, const uint64_t* ranges,
+                  uint64_t n_ranges, uint64_t chunk_bytes, uint64_t* out_ranges,
+                  uint64_t* n_out_ranges, uint64_t* out_chunks, uint64_t* n_out_chunks,
+                  char* error, uint64_t error_len) {
+  using namespace xvram::residency;
+  std::vector<AllocationLayout> layouts;
+  for (uint64_t i = 0; i < n_allocs; ++i)
+    layouts.push_back(AllocationLayout{AllocationId{allocs[2 * i]}, allocs[2 * i + 1]});
+  std::vector<AccessRange> in;
+  for (uint64_t i = 0; i < n_ranges; ++i)
+    in.push_back(AccessRange{AllocationId{ranges[4 * i]}, ranges[4 * i + 1], ranges[4 * i + 2],
+                             static_cast<AccessMode>(ranges[4 * i + 3])});
+  const AccessPlanResult plan = normalize_and_split_accesses(layouts, in, chunk_bytes);
+  if (!plan) {
+    std::snprintf(error, error_len, "%s", std::string(access_plan_error_name(plan.error)).c_str());
+    return 1;
+  }
+  if (plan.normalized_ranges.size() > *n_out_ranges || plan.chunks.size() > *n_out_chunks)
+    return 2;
+  for (size_t i = 0; i < plan.normalized_ranges.size(); ++i) {
+    const AccessRange& r = plan.normalized_ranges[i];
+    out_ranges[4 * i] = r.allocation_id.value;
+    out_ranges[4 * i + 1] = r.offset_bytes;
+    out_ranges[4 * i + 2] = r.length_bytes;
+    out_ranges[4 * i + 3] = static_cast<uint64_t>(r.mode);
+  }
+  for (size_t i = 0; i < plan.chunks.size(); ++i) {
+    const ChunkAccessPlan& c = plan.chunks[i];
+    out_chunks[5 * i] = c.key.allocation_id.value;
+    out_chunks[5 * i + 1] = c.key.chunk_index;
+    out_chunks[5 * i + 2] = c.valid_bytes;
+    out_chunks[5 * i + 3] = c.requires_h2d ? 1 : 0;
+    out_chunks[5 * i + 4] = c.marks_dirty ? 1 : 0;
+  }
+  *n_out_ranges = plan.normalized_ranges.size();
+  *n_out_chunks = plan.chunks.size();
+  return 0;
 }
 }

@@ -51,6 +51,7 @@ def close_balanced(s):
     t = s.telemetry()
     assert t.mappings == t.unmaps == t.set_access_calls
     assert t.physical_handles_created == t.physical_handles_released
+    assert t.unsafe_transitions == 0 and t.unsafe_remaps == 0
     s.release()
 
 

@@ -181,6 +181,7 @@ def test_random_transactions_match_model(sim):
         assert np.array_equal(a.read(), model)
         t = s.telemetry()
         assert t.clean_evictions + t.dirty_evictions > 0
+        assert t.unsafe_transitions == 0 and t.unsafe_remaps == 0
         assert len(bases) == 1  # one base address for the allocation throughout
 
 
@@ -454,3 +455,4 @@ def test_teardown_balances_mappings(sim):
         assert t.mappings == t.unmaps
         assert t.physical_handles_created == t.physical_handles_released
         assert t.resident_bytes == 0
+        assert t.unsafe_transitions == 0 and t.unsafe_remaps == 0

@@ -15,6 +15,7 @@
 // Faults can be injected per call site (xvram_hostsim_inject), and the
 // reported device memory can be set (xvram_hostsim_set_memory).
 #include <chrono>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -23,6 +24,7 @@
 #include <vector>
 
 #include "device.hpp"
+#include "runtime.hpp"
 
 namespace xvram {
 namespace {
@@ -335,4 +337,56 @@ extern "C" __attribute__((visibility("default"))) uint64_t xvram_hostsim_kernel_
   using namespace xvram;
   std::lock_guard<std::mutex> lock(g_sim.mutex);
   return g_sim.kernel_launches;
+}
+
+// ---- pure host logic of the runtime, exposed for differential tests ----------
+
+// The entry-state transition table (1 = legal).
+extern "C" __attribute__((visibility("default"))) int xvram_hostsim_legal_transition(int from,
+                                                                                     int to) {
+  using xvram::EntryState;
+  return xvram::is_legal_transition(static_cast<EntryState>(from), static_cast<EntryState>(to))
+             ? 1
+             : 0;
+}
+
+// normalize_accesses over flat arrays: allocations as (id, bytes) pairs, ranges
+// as (id, offset, length, mode) quads. Outputs normalised ranges as quads and
+// chunks as (id, index, valid_bytes, requires_h2d, marks_dirty); *n_out_* hold
+// the capacities (in records) on entry and the counts on return. Returns 0,
+// 1 with the problem's name in `error`, or 2 when a capacity is too small.
+extern "C" __attribute__((visibility("default"))) int xvram_hostsim_normalize(
+    const uint64_t* allocs, uint64_t n_allocs, const uint64_t* ranges, uint64_t n_ranges,
+    uint64_t chunk_bytes, uint64_t* out_ranges, uint64_t* n_out_ranges, uint64_t* out_chunks,
+    uint64_t* n_out_chunks, char* error, uint64_t error_len) {
+  std::vector<xvram::AllocationExtent> extents;
+  for (uint64_t i = 0; i < n_allocs; ++i) extents.push_back({allocs[2 * i], allocs[2 * i + 1]});
+  std::vector<xvram::AccessSpan> spans;
+  for (uint64_t i = 0; i < n_ranges; ++i)
+    spans.push_back({ranges[4 * i], ranges[4 * i + 1], ranges[4 * i + 2],
+                     static_cast<uint32_t>(ranges[4 * i + 3])});
+  std::vector<xvram::AccessSpan> normalized;
+  std::vector<xvram::ChunkPlan> chunks;
+  const char* problem = xvram::normalize_accesses(extents, spans, chunk_bytes, normalized, chunks);
+  if (problem) {
+    std::snprintf(error, error_len, "%s", problem);
+    return 1;
+  }
+  if (normalized.size() > *n_out_ranges || chunks.size() > *n_out_chunks) return 2;
+  for (size_t i = 0; i < normalized.size(); ++i) {
+    out_ranges[4 * i] = normalized[i].allocation_id;
+    out_ranges[4 * i + 1] = normalized[i].offset;
+    out_ranges[4 * i + 2] = normalized[i].length;
+    out_ranges[4 * i + 3] = normalized[i].mode;
+  }
+  for (size_t i = 0; i < chunks.size(); ++i) {
+    out_chunks[5 * i] = chunks[i].allocation_id;
+    out_chunks[5 * i + 1] = chunks[i].index;
+    out_chunks[5 * i + 2] = chunks[i].valid_bytes;
+    out_chunks[5 * i + 3] = chunks[i].requires_h2d ? 1 : 0;
+    out_chunks[5 * i + 4] = chunks[i].marks_dirty ? 1 : 0;
+  }
+  *n_out_ranges = normalized.size();
+  *n_out_chunks = chunks.size();
+  return 0;
 }

@@ -23,6 +23,24 @@ uint32_t combine_modes(uint32_t a, uint32_t b) {
 
 } // namespace
 
+bool is_legal_transition(EntryState from, EntryState to) {
+  using S = EntryState;
+  if (to == S::poisoned) return true;
+  switch (from) {
+  case S::host_clean: return to == S::prefetch_queued || to == S::mapping;
+  case S::prefetch_queued: return to == S::host_clean || to == S::mapping;
+  case S::mapping: return to == S::host_clean || to == S::h2d_in_flight || to == S::resident_clean;
+  case S::h2d_in_flight: return to == S::resident_clean;
+  case S::resident_clean: return to == S::resident_dirty || to == S::evicting;
+  case S::resident_dirty: return to == S::writeback_queued || to == S::evicting;
+  case S::writeback_queued: return to == S::d2h_in_flight;
+  case S::d2h_in_flight: return to == S::resident_clean;
+  case S::evicting: return to == S::host_clean;
+  case S::poisoned: return false;
+  }
+  return false;
+}
+
 bool keys_overlap(const PanelKey& a, const PanelKey& b) {
   if (a.allocation_id != b.allocation_id) return false;
   if (a.offset >= b.end() || b.offset >= a.end()) return false;
@@ -339,6 +357,7 @@ Error Runtime::map_frame_at(Frame& f, uint64_t address) {
   }
   if (f.mapped_at)
     if (Error e = unmap_frame(f)) return e;
+  check_generation(f);
   if (int rc = device_->mem_map(address, frame_bytes_, f.handle))
     return device_failure(rc, "cache", "mem_map");
   f.mapped_at = address;
@@ -354,9 +373,28 @@ Error Runtime::map_frame_at(Frame& f, uint64_t address) {
   return {};
 }
 
+void Runtime::move(Frame& f, EntryState to) {
+  if (!is_legal_transition(f.state, to)) ++t_.unsafe_transitions;
+  f.state = to;
+}
+
+// Every remap, unmap and refill happens only after the host has seen the
+// frame's latest retire event complete; anything else is counted.
+void Runtime::check_generation(const Frame& f) {
+  if (f.completed != f.generation) ++t_.unsafe_remaps;
+}
+
+Error Runtime::record_retire(Frame& f, Stream stream) {
+  if (int rc = device_->event_record(f.retire, stream)) return device_failure(rc, "cache", "record");
+  f.retire_pending = true;
+  ++f.generation;
+  return {};
+}
+
 Error Runtime::unmap_frame(Frame& f) {
   if (!f.mapped_at) return {};
   if (Error e = wait_retired(f)) return e;
+  check_generation(f);
   if (int rc = device_->mem_unmap(f.mapped_at, frame_bytes_))
     return device_failure(rc, "cache", "mem_unmap");
   ++t_.unmaps;
@@ -376,6 +414,8 @@ Error Runtime::wait_retired(Frame& f) {
     return device_failure(q, "cache", "event_query");
   }
   f.retire_pending = false;
+  f.completed = f.generation;
+  if (f.state == EntryState::evicting) move(f, EntryState::host_clean);
   return {};
 }
 
@@ -387,6 +427,13 @@ Error Runtime::evict_key(Frame& f, bool was_dirty) {
   f.ready_pending = false;
   t_.resident_bytes -= frame_bytes_;
   if (was_dirty) ++t_.dirty_evictions;
+  if (f.state == EntryState::mapping) {
+    move(f, EntryState::host_clean); // never filled: roll back
+  } else {
+    if (f.state == EntryState::h2d_in_flight) move(f, EntryState::resident_clean);
+    move(f, EntryState::evicting);
+    if (!f.retire_pending) move(f, EntryState::host_clean);
+  }
   // A chunk frame stays mapped at the chunk's address until the frame is
   // reused (map_frame_at moves it) or the chunk is acquired again (it is then
   // taken back without a remap).
@@ -436,6 +483,7 @@ Error Runtime::select_frame(Frame*& out) {
   if (Error e = wait_retired(*chosen)) return e;
   if (chosen->used_before) ++t_.handle_reuses;
   chosen->used_before = true;
+  move(*chosen, EntryState::mapping);
   out = chosen;
   return {};
 }
@@ -462,7 +510,12 @@ Error Runtime::fill_entry(Frame& f, const PanelKey& key, uint64_t packed_pitch, 
   index_[key] = f.index;
   t_.resident_bytes += frame_bytes_;
   t_.resident_bytes_peak = std::max(t_.resident_bytes_peak, t_.resident_bytes);
-  if (!needs_data) return {};
+  check_generation(f);
+  if (!needs_data) {
+    move(f, EntryState::resident_clean);
+    return {};
+  }
+  move(f, EntryState::h2d_in_flight);
   for (const auto& [written, done] : pending_writebacks_) {
     // Host bytes this fill reads may still be in flight from a write-back.
     if (!keys_overlap(written, key)) continue;
@@ -521,29 +574,36 @@ Error Runtime::acquire(const PanelKey& key, uint64_t packed_pitch, bool needs_da
   return {};
 }
 
+// Orders `stream` after the fill; from then on the entry's bytes are resident
+// for everything enqueued on that stream.
 Error Runtime::wait_ready(Frame& f, Stream stream) {
   if (!f.ready_pending) return {};
   if (int rc = device_->stream_wait_event(stream, f.ready))
     return device_failure(rc, "cache", "stream_wait");
+  if (f.state == EntryState::h2d_in_flight) move(f, EntryState::resident_clean);
   return {};
 }
 
 Error Runtime::release_after(Frame& f, Stream stream, bool dirty) {
   if (f.pins <= 0) return make_error(XVRAM_STATUS_INTERNAL, "cache", "release", "frame is not pinned");
-  if (int rc = device_->event_record(f.retire, stream)) return device_failure(rc, "cache", "record");
-  f.retire_pending = true;
+  if (Error e = record_retire(f, stream)) return e;
   --f.pins;
+  if (dirty && f.state != EntryState::resident_dirty) {
+    if (f.state == EntryState::h2d_in_flight) move(f, EntryState::resident_clean);
+    move(f, EntryState::resident_dirty);
+  }
   f.dirty = f.dirty || dirty;
   f.last_use = ++tick_;
   return {};
 }
 
 // Clean, idle entries whose bytes intersect bytes just written back are stale.
+// Dropping the key is enough: the frame itself is reused only after its
+// retire event (select_frame waits for it).
 Error Runtime::drop_overlapping(const PanelKey& written, const Frame* except) {
   for (Frame& f : frames_) {
     if (&f == except || !f.keyed || f.pins > 0 || f.dirty) continue;
     if (!keys_overlap(f.key, written)) continue;
-    if (Error e = wait_retired(f)) return e;
     if (Error e = evict_key(f, false)) return e;
     ++t_.clean_evictions;
   }
@@ -561,6 +621,7 @@ Error Runtime::writeback_and_evict(Frame& f) {
   if (f.retire_pending)
     if (int rc = device_->stream_wait_event(d2h_, f.retire))
       return device_failure(rc, "cache", "stream_wait");
+  move(f, EntryState::writeback_queued);
   TraceInterval iv;
   iv.kind = 'd';
   iv.bytes = f.key.bytes();
@@ -569,11 +630,14 @@ Error Runtime::writeback_and_evict(Frame& f) {
   if (int rc = device_->copy_d2h_2d(a->host + f.key.offset, f.key.pitch, f.address, f.packed_pitch,
                                     f.key.width, f.key.height, d2h_))
     return device_failure(rc, "cache", "copy_d2h");
+  move(f, EntryState::d2h_in_flight);
   if (Error e = take_event(iv.stop)) return e;
   if (int rc = device_->event_record(iv.stop, d2h_)) return device_failure(rc, "cache", "record");
   trace_.push_back(iv);
-  if (int rc = device_->event_record(f.retire, d2h_)) return device_failure(rc, "cache", "record");
-  f.retire_pending = true;
+  if (Error e = record_retire(f, d2h_)) return e;
+  // The frame now matches what the host will hold once the copy retires; its
+  // retire event (the copy) gates any reuse.
+  move(f, EntryState::resident_clean);
   const PanelKey written = f.key;
   pending_writebacks_[written] = iv.stop;
   t_.bytes_d2h += written.bytes();
@@ -651,37 +715,33 @@ Error Runtime::ensure_workspace(uint64_t bytes) {
   return {};
 }
 
-// Normalisation and chunk split (reference core::normalize_and_split_accesses,
-// src/residency/core.cpp:128-276): overlapping accesses merge with their modes
-// combined; each touched chunk records whether it must be loaded (anything but
-// one write-only span covering the whole chunk) and whether it is written.
-Error Runtime::plan_chunks(const std::vector<AccessSpan>& ranges, std::vector<ChunkUse>& chunks,
-                           std::vector<AccessSpan>& normalized, const char* operation) {
-  chunks.clear();
+const char* normalize_accesses(const std::vector<AllocationExtent>& allocations,
+                               const std::vector<AccessSpan>& ranges, uint64_t chunk_bytes,
+                               std::vector<AccessSpan>& normalized,
+                               std::vector<ChunkPlan>& chunks) {
   normalized.clear();
-  const auto rejected = [&](const char* reason) {
-    return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "transaction", operation,
-                      std::string("invalid access ranges: ") + reason);
-  };
-  if (ranges.empty()) return rejected("zero_length");
-  std::map<uint64_t, std::vector<AccessSpan>> by_alloc;
+  chunks.clear();
+  std::map<uint64_t, uint64_t> sizes;
+  for (const AllocationExtent& a : allocations) sizes[a.id] = a.bytes;
+  std::map<uint64_t, std::vector<const AccessSpan*>> by_alloc;
   for (const AccessSpan& r : ranges) {
     if (r.mode != XVRAM_ACCESS_READ && r.mode != XVRAM_ACCESS_READ_WRITE &&
         r.mode != XVRAM_ACCESS_WRITE_ONLY)
-      return rejected("invalid_access_mode");
-    if (r.length == 0) return rejected("zero_length");
-    HostAllocation* a = find(r.allocation_id);
+      return "invalid_access_mode";
+    if (r.length == 0) return "zero_length";
+    auto size = sizes.find(r.allocation_id);
+    if (size == sizes.end()) return "unknown_allocation";
     uint64_t end = 0;
-    if (!a) return rejected("unknown_allocation");
-    if (!checked_add(r.offset, r.length, end)) return rejected("range_overflow");
-    if (r.offset >= a->bytes || end > a->bytes) return rejected("range_out_of_bounds");
-    by_alloc[r.allocation_id].push_back(r);
+    if (!checked_add(r.offset, r.length, end)) return "range_overflow";
+    if (r.offset >= size->second || end > size->second) return "range_out_of_bounds";
+    by_alloc[r.allocation_id].push_back(&r);
   }
-  for (auto& [id, list] : by_alloc) {
+  for (const auto& [id, list] : by_alloc) {
     std::vector<uint64_t> cuts;
-    for (const AccessSpan& r : list) {
-      cuts.push_back(r.offset);
-      cuts.push_back(r.offset + r.length);
+    cuts.reserve(2 * list.size());
+    for (const AccessSpan* r : list) {
+      cuts.push_back(r->offset);
+      cuts.push_back(r->offset + r->length);
     }
     std::sort(cuts.begin(), cuts.end());
     cuts.erase(std::unique(cuts.begin(), cuts.end()), cuts.end());
@@ -689,43 +749,65 @@ Error Runtime::plan_chunks(const std::vector<AccessSpan>& ranges, std::vector<Ch
       const uint64_t lo = cuts[i], hi = cuts[i + 1];
       bool covered = false;
       uint32_t mode = XVRAM_ACCESS_READ;
-      for (const AccessSpan& r : list) {
-        if (r.offset <= lo && hi <= r.offset + r.length) {
-          mode = covered ? combine_modes(mode, r.mode) : r.mode;
+      for (const AccessSpan* r : list) {
+        if (r->offset <= lo && hi <= r->offset + r->length) {
+          mode = covered ? combine_modes(mode, r->mode) : r->mode;
           covered = true;
         }
       }
       if (!covered) continue;
-      if (!normalized.empty() && normalized.back().allocation_id == id &&
-          normalized.back().offset + normalized.back().length == lo && normalized.back().mode == mode) {
-        normalized.back().length += hi - lo;
+      AccessSpan* last = normalized.empty() ? nullptr : &normalized.back();
+      if (last && last->allocation_id == id && last->offset + last->length == lo &&
+          last->mode == mode) {
+        last->length += hi - lo;
       } else {
         normalized.push_back(AccessSpan{id, lo, hi - lo, mode});
       }
     }
   }
   for (const AccessSpan& s : normalized) {
-    const HostAllocation* a = find(s.allocation_id);
-    const uint64_t first = s.offset / frame_bytes_, last = (s.offset + s.length - 1) / frame_bytes_;
+    const uint64_t bytes = sizes[s.allocation_id];
+    const uint64_t first = s.offset / chunk_bytes, last = (s.offset + s.length - 1) / chunk_bytes;
     for (uint64_t c = first; c <= last; ++c) {
-      const uint64_t c_lo = c * frame_bytes_;
-      const uint64_t c_hi = std::min(a->bytes, c_lo + frame_bytes_);
+      const uint64_t c_lo = c * chunk_bytes;
+      const uint64_t c_hi = std::min(bytes, c_lo + chunk_bytes);
       const uint64_t lo = std::max(s.offset, c_lo), hi = std::min(s.offset + s.length, c_hi);
       const bool full_write_only = s.mode == XVRAM_ACCESS_WRITE_ONLY && lo == c_lo && hi == c_hi;
       if (chunks.empty() || chunks.back().allocation_id != s.allocation_id ||
           chunks.back().index != c) {
-        ChunkUse u;
-        u.allocation_id = s.allocation_id;
-        u.index = c;
-        u.needs_data = !full_write_only;
-        u.writes = s.mode != XVRAM_ACCESS_READ;
-        chunks.push_back(u);
+        chunks.push_back(ChunkPlan{s.allocation_id, c, c_hi - c_lo, !full_write_only,
+                                   s.mode != XVRAM_ACCESS_READ});
       } else {
-        // A second span in the same chunk: the chunk is no longer one full write-only span.
-        chunks.back().needs_data = true;
-        chunks.back().writes = chunks.back().writes || s.mode != XVRAM_ACCESS_READ;
+        // A second span in the chunk: it is no longer one full write-only span.
+        chunks.back().requires_h2d = true;
+        chunks.back().marks_dirty = chunks.back().marks_dirty || s.mode != XVRAM_ACCESS_READ;
       }
     }
+  }
+  return nullptr;
+}
+
+Error Runtime::plan_chunks(const std::vector<AccessSpan>& ranges, std::vector<ChunkUse>& chunks,
+                           std::vector<AccessSpan>& normalized, const char* operation) {
+  chunks.clear();
+  std::vector<AllocationExtent> extents;
+  extents.reserve(allocations_.size());
+  for (const auto& [id, a] : allocations_) extents.push_back(AllocationExtent{id, a.bytes});
+  std::vector<ChunkPlan> plans;
+  const char* problem = ranges.empty()
+                            ? "zero_length"
+                            : normalize_accesses(extents, ranges, frame_bytes_, normalized, plans);
+  if (problem)
+    return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "transaction", operation,
+                      std::string("invalid access ranges: ") + problem);
+  chunks.reserve(plans.size());
+  for (const ChunkPlan& p : plans) {
+    ChunkUse u;
+    u.allocation_id = p.allocation_id;
+    u.index = p.index;
+    u.needs_data = p.requires_h2d;
+    u.writes = p.marks_dirty;
+    chunks.push_back(u);
   }
   return {};
 }
@@ -756,6 +838,7 @@ Error Runtime::acquire_chunk(ChunkUse& use) {
     // The frame that last held this chunk may still be mapped at its address.
     if (g.mapped_at == address && !g.keyed && g.pins == 0) {
       if (Error e = wait_retired(g)) return e;
+      move(g, EntryState::mapping);
       ++t_.handle_reuses;
       f = &g;
       break;
@@ -896,7 +979,13 @@ Error Runtime::finish_operation(uint64_t operation_id) {
   }
   for (Frame& f : frames_) {
     f.ready_pending = false;
-    if (!first) f.retire_pending = false;
+    if (first) continue;
+    // Every stream has drained: all fills landed and every retire event of
+    // this operation has completed.
+    f.retire_pending = false;
+    f.completed = f.generation;
+    if (f.state == EntryState::h2d_in_flight) move(f, EntryState::resident_clean);
+    if (f.state == EntryState::evicting) move(f, EntryState::host_clean);
   }
   pending_writebacks_.clear();
   bool guard_tripped = false;

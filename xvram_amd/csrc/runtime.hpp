@@ -90,6 +90,27 @@ struct PanelKey {
 // (exact for rectangles of equal pitch, conservative otherwise).
 bool keys_overlap(const PanelKey& a, const PanelKey& b);
 
+// Entry states and their legal transitions: the reference's chunk state
+// machine (src/residency/core.hpp:102-113, core.cpp:304-332) applied to every
+// cache entry (panel or chunk), plus one edge of this design:
+// resident_dirty -> evicting, the discard of a failed operation's unwritten
+// output (the host copy stays authoritative; the reference poisons instead).
+// An illegal move is counted in telemetry (unsafe_transitions), never taken
+// silently.
+enum class EntryState : uint32_t {
+  host_clean,
+  prefetch_queued,
+  mapping,
+  h2d_in_flight,
+  resident_clean,
+  resident_dirty,
+  writeback_queued,
+  d2h_in_flight,
+  evicting,
+  poisoned,
+};
+bool is_legal_transition(EntryState from, EntryState to);
+
 struct Frame {
   uint64_t index = 0;
   uint64_t slot = 0;      // this frame's address in the panel arena
@@ -107,6 +128,12 @@ struct Frame {
   Event retire = nullptr; // recorded after the last consumer (kernel or write-back)
   bool retire_pending = false;
   bool used_before = false;
+  EntryState state = EntryState::host_clean;
+  // Event generations (reference core.cpp begin/complete_event_generation):
+  // `generation` counts retire-event records, `completed` the last one the
+  // host has seen finish. A frame is remapped or refilled only when equal.
+  uint64_t generation = 0;
+  uint64_t completed = 0;
 };
 
 // Per-operation intervals for the optional trace file (XVRAM_TRACE_FILE).
@@ -129,6 +156,36 @@ struct ResolvedSpan {
   AccessSpan span;
   uint64_t device_address = 0;
 };
+
+struct AllocationExtent {
+  uint64_t id = 0;
+  uint64_t bytes = 0;
+};
+
+// One chunk a transaction touches: the bytes it holds (`valid_bytes`, short
+// for an allocation's last chunk), whether its current bytes must be loaded
+// (anything but one write-only span over all valid bytes) and whether the
+// transaction writes it.
+struct ChunkPlan {
+  uint64_t allocation_id = 0;
+  uint64_t index = 0;
+  uint64_t valid_bytes = 0;
+  bool requires_h2d = true;
+  bool marks_dirty = false;
+};
+
+// Access normalisation and chunk split (reference
+// core::normalize_and_split_accesses, src/residency/core.cpp:128-276):
+// per allocation in id order, the ranges are cut at every boundary, each piece
+// takes the combined mode of the ranges covering it (read + write-only =
+// read-write), adjacent pieces of equal mode merge; chunks follow in
+// (allocation, index) order. Returns nullptr, or the name of the first
+// problem in input order: invalid_access_mode, zero_length,
+// unknown_allocation, range_overflow, range_out_of_bounds.
+const char* normalize_accesses(const std::vector<AllocationExtent>& allocations,
+                               const std::vector<AccessSpan>& ranges, uint64_t chunk_bytes,
+                               std::vector<AccessSpan>& normalized,
+                               std::vector<ChunkPlan>& chunks);
 
 // The work a transaction enqueues with its working set resident. Returns an
 // error to fail the transaction; `skipped` reports that nothing was enqueued.
@@ -215,6 +272,9 @@ private:
     Frame* frame = nullptr;
   };
 
+  void move(Frame& frame, EntryState to);
+  void check_generation(const Frame& frame);
+  Error record_retire(Frame& frame, Stream stream);
   Error map_frame_at(Frame& frame, uint64_t address);
   Error unmap_frame(Frame& frame);
   Error select_frame(Frame*& out);
