@@ -50,6 +50,10 @@ WORKLOADS = {
                           "FP32 SGEMM N/T 16384^3, fully resident (one launch)"),
 }
 DEFAULT = "ns65536_nt_16g"
+# Config 5: 8 x [Y = ReLU(X W^T + b)], X 256 x 16384 ~ N(0,1), W 16384 x 16384 and
+# b ~ N(0, 1/16384), 2 GiB budget of 64 MiB frames; one step = one 8-layer forward.
+CHAIN = {"name": "c5_chain_2g", "layers": 8, "batch": 256, "width": 16384,
+         "budget": 2 * GiB, "frame": 64 * MiB}
 
 
 def log(msg: str) -> None:
@@ -209,7 +213,15 @@ def synth_lib():
     u64 = ctypes.c_uint64
     lib.synth_fill_uniform.argtypes = [fp, u64, u64, u64]
     lib.synth_fill_uniform_strided.argtypes = [fp, u64, u64, u64, u64, u64, u64]
+    lib.synth_fill_normal.argtypes = [fp, u64, u64, u64, ctypes.c_double]
     return lib
+
+
+def normal(synth, count: int, seed: int, sigma: float) -> np.ndarray:
+    out = np.empty(count, dtype=np.float32)
+    synth.synth_fill_normal(out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), count, seed, 0,
+                            sigma)
+    return out
 
 
 def fill_allocation(synth, alloc, elements: int, seed: int, chunk_elems: int = 256 * MiB):
@@ -230,6 +242,165 @@ def sample_block(synth, rows, cols, seed, first, row_stride, col_stride):
     return np.asfortranarray(out.reshape(cols, rows).T)
 
 
+# ---- config 5: the inference chain ---------------------------------------------------
+
+def run_chain(args, xv, lib, synth, link) -> int:
+    """One step = one forward of CHAIN["layers"] x [Y = ReLU(X W^T + b)]: each
+    layer is one GEMM plan with a fused bias+ReLU epilogue (extension table),
+    the 8 operations are submitted back to back, weights stream from pinned host
+    memory through the 2 GiB budget."""
+    import oracle
+
+    L, batch, width = CHAIN["layers"], CHAIN["batch"], CHAIN["width"]
+    std = width ** -0.5
+    session = xv.Session(lib, chunk_size_bytes=CHAIN["frame"], cache_target_bytes=CHAIN["budget"])
+    t0 = time.time()
+    acts = [session.allocation(batch * width * 4) for _ in range(L + 1)]
+    x0 = normal(synth, batch * width, 5000, 1.0)
+    acts[0].write(x0)
+    weights, biases, plans = [], [], []
+    for l in range(L):
+        w_alloc = session.allocation(width * width * 4)
+        w_alloc.write(normal(synth, width * width, 6000 + l, std))
+        b_alloc = session.allocation(width * 4)
+        b_alloc.write(normal(synth, width, 7000 + l, std))
+        weights.append(w_alloc)
+        biases.append(b_alloc)
+        plans.append(xv.GemmPlan(
+            session, xv.matrix(acts[l], batch, width, width, xv.abi.ROW_MAJOR),
+            xv.matrix(w_alloc, width, width, width, xv.abi.ROW_MAJOR),
+            xv.matrix(acts[l + 1], batch, width, width, xv.abi.ROW_MAJOR), OP_N, OP_T,
+            epilogue=xv.epilogue(b_alloc, xv.abi.BIAS_PER_COLUMN, relu=True)))
+    info = plans[0].info()
+    log(f"chain ready: {L} x {width * width * 4 / GiB:.0f} GiB weights ({time.time() - t0:.1f}s); "
+        f"layer plan tiles {info.tile_m}x{info.tile_n}x{info.tile_k}, {info.tile_count} launches")
+
+    def forward():
+        ops = [p.submit() for p in plans]
+        for op in ops:
+            st, res = op.wait()
+            if st != 0 or res.result != 0:
+                raise RuntimeError(f"layer failed: {st} {res.result} {op.error().message}")
+            op.release()
+
+    trace_path = os.environ["XVRAM_TRACE_FILE"]
+    for i in range(args.warmup):
+        t = time.perf_counter()
+        forward()
+        log(f"warmup {i}: {time.perf_counter() - t:.3f}s")
+    with open(trace_path, "a"):
+        pass
+    before = sum(1 for _ in open(trace_path))
+    tele0 = session.telemetry()
+    times = []
+    flops = 2.0 * L * batch * width * width
+    for i in range(args.steps):
+        t = time.perf_counter()
+        forward()
+        times.append(time.perf_counter() - t)
+        log(f"step {i}: {times[-1]:.3f}s = {flops / times[-1] / 1e12:.1f} TFLOP/s")
+    tele1 = session.telemetry()
+    ops = [json.loads(line) for line in open(trace_path).readlines()[before:]]
+    stats = analyse(ops)
+    step_s = sum(times) / len(times)
+
+    # Per-layer check on the first `rows` batch rows (rows are independent through
+    # the chain): FP64 forward of the FP32 input each layer actually consumed.
+    rows = 8
+    worst = 0.0
+    violations = 0
+    y64 = x0.reshape(batch, width)[:rows].astype(np.float64)
+    for l in range(L):
+        xin = acts[l].read(rows * width * 4, dtype=np.float32).reshape(rows, width).astype(np.float64)
+        got = acts[l + 1].read(rows * width * 4, dtype=np.float32).reshape(rows, width)
+        w = normal(synth, width * width, 6000 + l, std).reshape(width, width).astype(np.float64)
+        bvec = normal(synth, width, 7000 + l, std).astype(np.float64)
+        pre = xin @ w.T + bvec
+        absab = np.abs(xin) @ np.abs(w).T + np.abs(bvec)
+        bound = 4 * width * 2.0 ** -24 * absab
+        err = np.abs(got - np.maximum(pre, 0.0))
+        violations += int(np.count_nonzero(err > bound))
+        worst = max(worst, float((err / np.maximum(bound, 1e-300)).max()))
+        y64 = np.maximum(y64 @ w.T + bvec, 0.0)
+        del w, absab
+    final = acts[L].read(rows * width * 4, dtype=np.float32).reshape(rows, width)
+    e2e = float(np.abs(final - y64).max() / max(np.abs(y64).max(), 1e-300))
+    log(f"chain check rows 0:{rows}: violations={violations} err/bound={worst:.3e} "
+        f"end-to-end rel={e2e:.3e}")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        # The oracle's FP64 loop on layer 0: Y[0:r, 0:width] with full K, r scaled
+        # from a probe so the timed work is about --cpu-seconds (at most the batch).
+        threads = os.cpu_count() or 1
+        w0t = np.asfortranarray(normal(synth, width * width, 6000, std).reshape(width, width).T)
+        x_all = x0.reshape(batch, width)
+        t = time.perf_counter()
+        oracle.sgemm_f64(np.asfortranarray(x_all[:1]), w0t, threads=threads)
+        probe = time.perf_counter() - t
+        r = int(min(batch, max(1, args.cpu_seconds / max(probe, 1e-3))))
+        t = time.perf_counter()
+        oracle.sgemm_f64(np.asfortranarray(x_all[:r]), w0t, threads=threads)
+        cpu_s = time.perf_counter() - t
+        cpu = {"value": round(2.0 * r * width * width / cpu_s / 1e12, 6), "unit": "TFLOP/s",
+               "cores": threads, "kind": "port",
+               "sample": f"layer 0, Y[0:{r}, 0:{width}] with full K={width} (FP64 accumulation "
+                         f"over FP32 inputs, {cpu_s:.1f} s on {threads} threads)"}
+        del w0t
+
+    h2d_compulsory = L * (width * width * 4 + width * 4 + batch * width * 4)
+    d2h_compulsory = L * batch * width * 4
+    t_roof = max(flops / (FP32_MFMA_PEAK_TFLOPS * 1e12), h2d_compulsory / (link["h2d_gbps"] * 1e9),
+                 d2h_compulsory / (link["d2h_gbps"] * 1e9))
+    kernel_tflops = flops * args.steps / (stats["kernel_ms_total"] * 1e-3) / 1e12
+    h2d_gbps = stats["h2d_gbps_while_copying"]
+    result = {
+        "metric": "config-5 inference chain FP32 TFLOP/s (8 x Linear 16384 + bias + ReLU, "
+                  "2 GiB budget); H2D GB/s vs link peak",
+        "value": round(flops / step_s / 1e12, 3), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_s * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (seeded N(0,1) input, N(0,1/16384) weights and biases)",
+        "config": {"workload": CHAIN["name"], "layers": L, "batch": batch, "width": width,
+                   "vram_budget_bytes": CHAIN["budget"], "frame_bytes": CHAIN["frame"],
+                   "tile": [info.tile_m, info.tile_n, info.tile_k],
+                   "launches_per_step": stats["launches"] / args.steps,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(kernel_tflops, 3),
+                     "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(kernel_tflops / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None},
+        "roofline_wall": {"t_roof_s": t_roof, "bound": "h2d link", "frac": round(t_roof / step_s, 4)},
+        "cpu_baseline": cpu,
+        "link": {
+            "h2d_gbps_while_copying": round(h2d_gbps, 2) if h2d_gbps else None,
+            "measured_peak": link,
+            "h2d_frac_of_measured_peak": round(h2d_gbps / link["h2d_gbps"], 4) if h2d_gbps else None,
+            "h2d_bytes_per_step": stats["h2d_bytes"] // args.steps,
+            "h2d_compulsory_bytes_per_step": h2d_compulsory,
+            "d2h_bytes_per_step": stats["d2h_bytes"] // args.steps,
+            "copy_time_hidden_fraction": round(stats["copy_time_hidden_fraction"], 4)
+            if stats["copy_time_hidden_fraction"] is not None else None,
+        },
+        "cache": {f: getattr(tele1, f) - getattr(tele0, f) for f in (
+            "bytes_h2d", "bytes_d2h", "cache_hits", "cache_misses", "clean_evictions",
+            "dirty_evictions", "writebacks_completed", "handle_reuses")},
+        "sample_check": {"rows": rows, "elements": rows * width * L, "violations": violations,
+                         "max_err_over_bound": worst, "end_to_end_rel_vs_fp64": e2e},
+    }
+    for p in plans:
+        p.release()
+    session.close()
+    t = session.telemetry()
+    result["teardown"] = {"mappings": t.mappings, "unmaps": t.unmaps,
+                          "handles_created": t.physical_handles_created,
+                          "handles_released": t.physical_handles_released,
+                          "unsafe_transitions": t.unsafe_transitions,
+                          "unsafe_remaps": t.unsafe_remaps}
+    session.release()
+    print(json.dumps(result), flush=True)
+    return 0 if violations == 0 else 1
+
+
 # ---- main ----------------------------------------------------------------------------
 
 def main() -> int:
@@ -237,7 +408,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default=DEFAULT)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + [CHAIN["name"]], default=DEFAULT)
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -256,18 +427,21 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
-    m, n, k, op_a, op_b, budget, frame, desc = WORKLOADS[args.workload]
     trace_path = os.path.join(tempfile.mkdtemp(prefix="xvram_bench_"), "trace.jsonl")
     os.environ["XVRAM_TRACE_FILE"] = trace_path
 
     import xvram_amd as xv
 
-    log(f"workload {args.workload}: {desc}")
     t0 = time.time()
     link = link_peak()
     log(f"link peak {link} ({time.time() - t0:.1f}s)")
     synth = synth_lib()
     lib = xv.load()
+    if args.workload == CHAIN["name"]:
+        log(f"workload {args.workload}")
+        return run_chain(args, xv, lib, synth, link)
+    m, n, k, op_a, op_b, budget, frame, desc = WORKLOADS[args.workload]
+    log(f"workload {args.workload}: {desc}")
     cfg = dict(chunk_size_bytes=frame)
     if budget:
         cfg["cache_target_bytes"] = budget

@@ -1,10 +1,12 @@
 """xvram_amd — MI355X-native out-of-core FP32 SGEMM behind the xVRAM v1 C ABI.
 
 The product is the native library ``lib/libxvram.so`` (C++20 host runtime +
-gfx950 FP32-MFMA kernel) whose only export is ``xvram_get_api``. This module is
-a thin Python client of that C ABI (ctypes), used by the tests and the bench the
-same way a C caller uses the function table. There is no Python or CPU
-fallback: if the native library is missing, loading raises.
+gfx950 FP32-MFMA kernel). It exports ``xvram_get_api`` (the reference's v1
+table) and ``xvram_amd_get_ext`` (this build's extension table: GEMM plans with
+a fused bias/ReLU epilogue). This module is a thin Python client of that C ABI
+(ctypes), used by the tests and the bench the same way a C caller uses the
+function tables. There is no Python or CPU fallback: if the native library is
+missing, loading raises.
 """
 from __future__ import annotations
 
@@ -22,7 +24,8 @@ PRODUCT_LIB = os.path.join(LIB_DIR, "libxvram.so")
 HOSTSIM_LIB = os.path.join(LIB_DIR, "libxvram_hostsim.so")
 
 __all__ = ["Library", "Session", "Allocation", "GemmPlan", "Operation", "XvramError", "abi",
-           "TransactionView", "access", "matrix", "load", "PRODUCT_LIB", "HOSTSIM_LIB"]
+           "TransactionView", "access", "epilogue", "matrix", "load", "PRODUCT_LIB",
+           "HOSTSIM_LIB"]
 
 
 class XvramError(RuntimeError):
@@ -56,6 +59,14 @@ class Library:
         status = get_api(abi.ABI_VERSION_1, ctypes.sizeof(self.api), ctypes.byref(self.api))
         if status != abi.SUCCESS:
             raise XvramError(status, "xvram_get_api")
+        get_ext = self.dll.xvram_amd_get_ext
+        get_ext.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
+        get_ext.restype = ctypes.c_uint32
+        self.get_ext = get_ext
+        self.ext = abi.ExtV1()
+        status = get_ext(abi.EXT_VERSION_1, ctypes.sizeof(self.ext), ctypes.byref(self.ext))
+        if status != abi.SUCCESS:
+            raise XvramError(status, "xvram_amd_get_ext")
 
     def status_name(self, status: int) -> str:
         return self.api.status_name(status).decode()
@@ -284,11 +295,23 @@ class Operation:
             self.handle = None
 
 
+def epilogue(bias: Optional[Allocation] = None, axis: int = abi.BIAS_NONE, offset: int = 0,
+             relu: bool = False) -> abi.EpilogueV1:
+    """A fused-epilogue record for GemmPlan(..., epilogue=...)."""
+    e = abi.epilogue_init()
+    e.bias = bias.handle.value if bias is not None else None
+    e.bias_offset_bytes = offset
+    e.bias_axis = axis
+    e.activation = abi.ACTIVATION_RELU if relu else abi.ACTIVATION_NONE
+    return e
+
+
 class GemmPlan:
     def __init__(self, session: Session, a: abi.Matrix, b: abi.Matrix, c: abi.Matrix,
                  op_a: int = abi.OP_N, op_b: int = abi.OP_N, alpha: float = 1.0,
                  beta: float = 0.0, compute_mode: int = abi.COMPUTE_AUTO,
-                 tile_hints=(0, 0, 0), deadline_ms: int = 0):
+                 tile_hints=(0, 0, 0), deadline_ms: int = 0,
+                 epilogue: Optional[abi.EpilogueV1] = None):
         self.session = session
         desc = abi.gemm_desc_init()
         desc.a, desc.b, desc.c = a, b, c
@@ -299,8 +322,13 @@ class GemmPlan:
         desc.deadline_ms = deadline_ms
         self.desc = desc
         handle = ctypes.c_void_p()
-        session.check(session.api.gemm_plan_create(session.handle, ctypes.byref(desc),
-                                                   ctypes.byref(handle)), "gemm_plan_create")
+        if epilogue is None:
+            status = session.api.gemm_plan_create(session.handle, ctypes.byref(desc),
+                                                  ctypes.byref(handle))
+        else:
+            status = session.lib.ext.gemm_plan_create_epilogue(
+                session.handle, ctypes.byref(desc), ctypes.byref(epilogue), ctypes.byref(handle))
+        session.check(status, "gemm_plan_create")
         self.handle = handle
 
     def info(self) -> abi.GemmPlanInfo:

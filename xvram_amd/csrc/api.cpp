@@ -526,13 +526,34 @@ xvram_status XVRAM_CALL transaction_execute_entry(xvram_session s, const xvram_t
   return result;
 }
 
-xvram_status XVRAM_CALL gemm_plan_create_entry(xvram_session s, const xvram_gemm_desc_v1* d,
-                                               xvram_gemm_plan* out) noexcept {
+// gemm_plan_create, with an optional fused epilogue (extension table).
+xvram_status create_plan(xvram_session s, const xvram_gemm_desc_v1* d,
+                         const xvram_amd_epilogue_v1* epilogue, xvram_gemm_plan* out) noexcept {
   if (out == nullptr) return XVRAM_STATUS_INVALID_ARGUMENT;
   *out = nullptr;
   if (s == nullptr || !s->state) return XVRAM_STATUS_INVALID_ARGUMENT;
   return boundary(s->state, "gemm_plan_create", [&]() -> Error {
     if (!has_v1_size(d)) return incompatible("gemm_plan_create", "GEMM descriptor is null or smaller than v1");
+    std::shared_ptr<AllocationRecord> bias;
+    EpilogueSpec ep;
+    if (epilogue != nullptr) {
+      if (epilogue->struct_size < sizeof(xvram_amd_epilogue_v1))
+        return incompatible("gemm_plan_create", "epilogue descriptor is smaller than v1");
+      if (epilogue->flags != 0 || !all_zero(epilogue->reserved, 2))
+        return invalid("gemm_plan_create", "unknown epilogue flags or non-zero reserved field");
+      if (epilogue->bias != nullptr) {
+        if (!epilogue->bias->backend || epilogue->bias->owner.get() != s->state.get())
+          return invalid("gemm_plan_create", "bias allocation belongs to another session");
+        bias = epilogue->bias->backend;
+      }
+      ep.bias_offset_bytes = epilogue->bias_offset_bytes;
+      ep.bias_axis = epilogue->bias_axis;
+      ep.activation = epilogue->activation;
+      if (ep.bias_axis != XVRAM_AMD_BIAS_NONE && !bias)
+        return invalid("gemm_plan_create", "bias axis given without a bias allocation");
+      if (ep.bias_axis == XVRAM_AMD_BIAS_NONE && bias)
+        return invalid("gemm_plan_create", "a bias allocation needs a bias axis");
+    }
     if (d->flags != 0 || d->reserved0 != 0 || !all_zero(d->reserved, 3))
       return invalid("gemm_plan_create", "unknown GEMM flags or non-zero reserved field");
     const bool ops_ok = d->operation_a <= XVRAM_MATRIX_OP_T && d->operation_b <= XVRAM_MATRIX_OP_T;
@@ -551,10 +572,12 @@ xvram_status XVRAM_CALL gemm_plan_create_entry(xvram_session s, const xvram_gemm
     spec.tile_m_hint = d->tile_m_hint;
     spec.tile_n_hint = d->tile_n_hint;
     spec.tile_k_hint = d->tile_k_hint;
+    spec.epilogue = ep;
     std::shared_ptr<GemmPlanRecord> rec;
     if (Error e = s->state->backend->create_gemm_plan(spec, d->a.allocation->backend,
                                                       d->b.allocation->backend,
-                                                      d->c.allocation->backend, d->deadline_ms, rec))
+                                                      d->c.allocation->backend, d->deadline_ms, rec,
+                                                      bias))
       return e;
     auto* handle = new (std::nothrow) xvram_gemm_plan_t{s->state, rec};
     if (handle == nullptr)
@@ -563,6 +586,22 @@ xvram_status XVRAM_CALL gemm_plan_create_entry(xvram_session s, const xvram_gemm
     *out = handle;
     return {};
   });
+}
+
+xvram_status XVRAM_CALL gemm_plan_create_entry(xvram_session s, const xvram_gemm_desc_v1* d,
+                                               xvram_gemm_plan* out) noexcept {
+  return create_plan(s, d, nullptr, out);
+}
+
+xvram_status XVRAM_CALL gemm_plan_create_epilogue_entry(xvram_session s,
+                                                        const xvram_gemm_desc_v1* d,
+                                                        const xvram_amd_epilogue_v1* epilogue,
+                                                        xvram_gemm_plan* out) noexcept {
+  if (epilogue == nullptr) {
+    if (out != nullptr) *out = nullptr;
+    return XVRAM_STATUS_INVALID_ARGUMENT;
+  }
+  return create_plan(s, d, epilogue, out);
 }
 
 xvram_status XVRAM_CALL gemm_plan_get_info_entry(xvram_gemm_plan p, xvram_gemm_plan_info_v1* out) noexcept {
@@ -714,8 +753,31 @@ const xvram_api_v1& api_v1() noexcept {
   return api;
 }
 
+const xvram_amd_ext_v1& ext_v1() {
+  static const xvram_amd_ext_v1 ext = [] {
+    xvram_amd_ext_v1 v{};
+    v.struct_size = sizeof(v);
+    v.ext_version = XVRAM_AMD_EXT_VERSION_1;
+    v.gemm_plan_create_epilogue = &gemm_plan_create_epilogue_entry;
+    return v;
+  }();
+  return ext;
+}
+
 } // namespace
 } // namespace xvram
+
+// The extension table of this build (no reference counterpart).
+extern "C" XVRAM_API xvram_status XVRAM_CALL xvram_amd_get_ext(uint32_t requested_version,
+                                                               uint32_t caller_size, void* out_ext) {
+  if (requested_version == XVRAM_AMD_EXT_VERSION_1) {
+    if (out_ext == nullptr || caller_size < sizeof(xvram_amd_ext_v1))
+      return XVRAM_STATUS_INVALID_ARGUMENT;
+    std::memcpy(out_ext, &xvram::ext_v1(), sizeof(xvram_amd_ext_v1));
+    return XVRAM_STATUS_SUCCESS;
+  }
+  return XVRAM_STATUS_INCOMPATIBLE_ABI;
+}
 
 extern "C" XVRAM_API xvram_status XVRAM_CALL xvram_get_api(uint32_t requested_abi_version,
                                                            uint32_t caller_api_size, void* out_api) {

@@ -2,6 +2,7 @@
 #pragma once
 
 #include <xvram/xvram.h>
+#include <xvram/xvram_amd_ext.h>
 
 #include <chrono>
 #include <cstdint>

@@ -238,6 +238,9 @@ public:
         !accessible(reinterpret_cast<uint64_t>(l.b), span(b_rows, b_cols, l.ldb)) ||
         !accessible(reinterpret_cast<uint64_t>(l.c), span(l.m, l.n, l.ldc)))
       return kSimBadAccess;
+    if ((l.bias_row && !accessible(reinterpret_cast<uint64_t>(l.bias_row), l.m * 4ull)) ||
+        (l.bias_col && !accessible(reinterpret_cast<uint64_t>(l.bias_col), l.n * 4ull)))
+      return kSimBadAccess;
     for (int64_t j = 0; j < l.n; ++j) {
       for (int64_t i = 0; i < l.m; ++i) {
         float acc = 0.f;
@@ -247,7 +250,11 @@ public:
           acc += x * y;
         }
         float& out = l.c[i + j * l.ldc];
-        out = l.beta != 0.f ? l.alpha * acc + l.beta * out : l.alpha * acc;
+        float v = l.beta != 0.f ? l.alpha * acc + l.beta * out : l.alpha * acc;
+        if (l.bias_row) v += l.bias_row[i];
+        if (l.bias_col) v += l.bias_col[j];
+        if (l.relu && v < 0.f) v = 0.f;
+        out = v;
       }
     }
     std::lock_guard<std::mutex> lock(g_sim.mutex);

@@ -258,7 +258,47 @@ CanonProblem canonicalize(const GemmSpec& s) {
     p.a = operand(s.b, !eop_b);
     p.b = operand(s.a, !eop_a);
   }
+  const EpilogueSpec& ep = s.epilogue;
+  if (ep.bias_axis != XVRAM_AMD_BIAS_NONE) {
+    p.bias_allocation_id = ep.bias_allocation_id;
+    p.bias_base = ep.bias_offset_bytes;
+    // The caller's rows are C' columns when C was swapped.
+    p.bias_rows = (ep.bias_axis == XVRAM_AMD_BIAS_PER_ROW) != p.swapped;
+  }
+  p.relu = ep.activation == XVRAM_AMD_ACTIVATION_RELU;
   return p;
+}
+
+Error validate_epilogue(const GemmSpec& s) {
+  const EpilogueSpec& ep = s.epilogue;
+  const auto bad = [](const char* message) {
+    return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "gemm", "epilogue", message);
+  };
+  if (ep.activation != XVRAM_AMD_ACTIVATION_NONE && ep.activation != XVRAM_AMD_ACTIVATION_RELU)
+    return bad("unknown activation");
+  if (ep.bias_axis == XVRAM_AMD_BIAS_NONE) {
+    if (ep.bias_allocation_id != 0) return bad("a bias allocation needs a bias axis");
+    return {};
+  }
+  if (ep.bias_axis != XVRAM_AMD_BIAS_PER_ROW && ep.bias_axis != XVRAM_AMD_BIAS_PER_COLUMN)
+    return bad("unknown bias axis");
+  if (ep.bias_allocation_id == 0) return bad("bias axis given without a bias allocation");
+  if (ep.bias_offset_bytes % 4 != 0) return bad("bias offset must be 4-byte aligned");
+  uint64_t m, n, k;
+  problem_dims(s, m, n, k);
+  const uint64_t length = ep.bias_axis == XVRAM_AMD_BIAS_PER_ROW ? m : n;
+  uint64_t bytes = 0, end = 0;
+  if (!checked_mul(length, 4, bytes) || !checked_add(ep.bias_offset_bytes, bytes, end) ||
+      end > ep.bias_allocation_bytes)
+    return bad("bias vector exceeds its allocation");
+  if (ep.bias_allocation_id == s.c.allocation_id) {
+    // Conservative: the bias must lie outside C's whole storage extent.
+    const uint64_t c_lines = s.c.layout == XVRAM_MATRIX_COLUMN_MAJOR ? s.c.columns : s.c.rows;
+    const uint64_t c_begin = s.c.offset_bytes;
+    const uint64_t c_end = c_begin + (c_lines * s.c.leading_dimension) * 4;
+    if (ep.bias_offset_bytes < c_end && c_begin < end) return bad("bias overlaps C");
+  }
+  return {};
 }
 
 // Panel planning. Tiles are sized so that each A, B and C panel fits one
@@ -266,11 +306,17 @@ CanonProblem canonicalize(const GemmSpec& s) {
 // loop while A and B panels stream through the remaining frames, and the block
 // shape minimises the scheduled H2D traffic
 //   ceil(tiles_m/block_m)*|B| + ceil(tiles_n/block_n)*|A| (+|C| if beta != 0).
-Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t frame_count,
+Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_frames,
                      uint32_t prefetch_distance, uint64_t max_launch_flops, GemmPlanData& out) {
   out = GemmPlanData{};
   CanonProblem p = canonicalize(spec);
   out.problem = p;
+  // A bias vector stays pinned in one frame for the whole operation.
+  const bool bias = p.bias_allocation_id != 0;
+  if (bias && p.bias_length() * 4 > frame_bytes)
+    return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "gemm", "make_plan",
+                      "working_set_too_large: the bias vector exceeds one cache frame");
+  const uint64_t frame_count = total_frames - (bias && total_frames > 0 ? 1 : 0);
   if (frame_count < 3)
     return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "gemm", "make_plan",
                       "working_set_too_large: fewer than three cache frames");
@@ -460,6 +506,25 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
   size_t next = 0;
   const size_t total = plan.launches.size();
 
+  // The bias vector, when there is one, is one panel pinned for the whole
+  // operation; tile launches index it at their first C' row or column.
+  Frame* bias = nullptr;
+  if (p.bias_allocation_id != 0) {
+    PanelKey key;
+    key.allocation_id = p.bias_allocation_id;
+    key.offset = p.bias_base;
+    key.width = p.bias_length() * 4;
+    key.height = 1;
+    key.pitch = key.width;
+    Error e = rt.acquire(key, round_up(key.width, 16), true, bias);
+    if (!e) e = rt.wait_ready(*bias, rt.compute_stream());
+    if (e) {
+      if (bias) (void)rt.release_after(*bias, rt.compute_stream(), false);
+      (void)rt.finish_operation(operation_id);
+      return e;
+    }
+  }
+
   const auto acquire_launch = [&](size_t idx) -> Error {
     const TileLaunch& l = plan.launches[idx];
     const LaunchGeom g = launch_geom(plan, l);
@@ -528,6 +593,14 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     k.a_kcontig = p.a.transposed;
     k.b_ncontig = p.b.transposed;
     k.padded = true;
+    if (l.last_panel && p.has_epilogue()) {
+      if (bias) {
+        const float* v = reinterpret_cast<const float*>(bias->address);
+        if (p.bias_rows) k.bias_row = v + g.i0;
+        else k.bias_col = v + g.j0;
+      }
+      k.relu = p.relu;
+    }
     TraceInterval iv;
     iv.kind = 'k';
     if (Error e = rt.record_kernel(iv.start, iv.stop)) {
@@ -565,6 +638,7 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
       }
     }
   }
+  if (bias && !result) result = rt.release_after(*bias, rt.compute_stream(), false);
   if (result) {
     // Unpin what was acquired ahead, drop partial C panels, drain the device.
     rt.discard_dirty();

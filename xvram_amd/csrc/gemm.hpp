@@ -28,6 +28,20 @@ struct MatrixSpec {
   uint32_t data_type = XVRAM_DATA_FP32;
 };
 
+// Optional fused epilogue, an extension of this build with no reference
+// counterpart (the reference's tiled linear is bias-free,
+// python/xvram/torch_native.py:1920-1921):
+//   C = act(alpha * op(A) * op(B) + beta * C + bias)
+// with an FP32 bias vector over the rows (length m) or the columns (length n)
+// of the caller's C, and act = identity or ReLU.
+struct EpilogueSpec {
+  uint64_t bias_allocation_id = 0; // 0 = no bias
+  uint64_t bias_allocation_bytes = 0;
+  uint64_t bias_offset_bytes = 0;
+  uint32_t bias_axis = 0;  // XVRAM_AMD_BIAS_PER_ROW / _PER_COLUMN of the caller's C
+  uint32_t activation = 0; // XVRAM_AMD_ACTIVATION_NONE / _RELU
+};
+
 struct GemmSpec {
   MatrixSpec a, b, c;
   uint32_t operation_a = XVRAM_MATRIX_OP_N;
@@ -36,6 +50,7 @@ struct GemmSpec {
   double alpha = 1.0;
   double beta = 0.0;
   uint64_t tile_m_hint = 0, tile_n_hint = 0, tile_k_hint = 0;
+  EpilogueSpec epilogue;
 };
 
 // Problem error classes in the reference's enumerator order
@@ -82,7 +97,19 @@ struct CanonProblem {
   CanonOperand a, b, c;
   float alpha = 1.f, beta = 0.f;
   bool swapped = false; // C was row-major: C' = C^T, A' = B, B' = A
+  // Epilogue in canonical terms: the bias runs along C' rows (length m) when
+  // bias_rows, else along C' columns (length n).
+  uint64_t bias_allocation_id = 0;
+  uint64_t bias_base = 0;
+  bool bias_rows = false;
+  bool relu = false;
+  bool has_epilogue() const { return bias_allocation_id != 0 || relu; }
+  uint64_t bias_length() const { return bias_rows ? m : n; }
 };
+
+// Checks an epilogue against the problem (extension rules: FP32 bias inside
+// its allocation, 4-byte aligned, not overlapping C; known axis/activation).
+Error validate_epilogue(const GemmSpec& spec);
 
 CanonProblem canonicalize(const GemmSpec& spec);
 

@@ -286,13 +286,15 @@ Error Session::release(AllocationRecord& a) {
 Error Session::create_gemm_plan(const GemmSpec& spec_in, std::shared_ptr<AllocationRecord> a,
                                 std::shared_ptr<AllocationRecord> b,
                                 std::shared_ptr<AllocationRecord> c, uint64_t deadline_ms,
-                                std::shared_ptr<GemmPlanRecord>& out) {
-  if (!a || !b || !c || a->released || b->released || c->released)
+                                std::shared_ptr<GemmPlanRecord>& out,
+                                std::shared_ptr<AllocationRecord> bias) {
+  if (!a || !b || !c || a->released || b->released || c->released ||
+      (bias && bias->released))
     return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "gemm", "create_plan",
                       "GEMM allocation is invalid or released");
   std::shared_ptr<GemmPlanRecord> record;
   Error e = invoke_sync([&]() -> Error {
-    if (a->released || b->released || c->released)
+    if (a->released || b->released || c->released || (bias && bias->released))
       return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "gemm", "create_plan",
                         "GEMM allocation was released before planning");
     GemmSpec spec = spec_in;
@@ -302,6 +304,8 @@ Error Session::create_gemm_plan(const GemmSpec& spec_in, std::shared_ptr<Allocat
     spec.b.allocation_bytes = b->bytes;
     spec.c.allocation_id = c->id;
     spec.c.allocation_bytes = c->bytes;
+    spec.epilogue.bias_allocation_id = bias ? bias->id : 0;
+    spec.epilogue.bias_allocation_bytes = bias ? bias->bytes : 0;
     char who = 0;
     const ProblemError pe = validate_problem(spec, &who);
     if (pe != ProblemError::none) {
@@ -309,6 +313,7 @@ Error Session::create_gemm_plan(const GemmSpec& spec_in, std::shared_ptr<Allocat
       if (who) msg += std::string(" (") + who + ")";
       return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "gemm", "make_plan", msg);
     }
+    if (Error ee = validate_epilogue(spec)) return ee;
     if (spec.a.data_type != XVRAM_DATA_FP32)
       return make_error(XVRAM_STATUS_UNSUPPORTED, "gemm", "make_plan",
                         "only FP32 GEMM is implemented on this device path");
@@ -318,6 +323,7 @@ Error Session::create_gemm_plan(const GemmSpec& spec_in, std::shared_ptr<Allocat
     record->a = a;
     record->b = b;
     record->c = c;
+    record->bias = bias;
     record->deadline_ms = deadline_ms;
     const double cap = static_cast<double>(runtime_.config().max_transaction_ms) *
                        kGuardPlanningFlopsPerMs;
@@ -335,7 +341,8 @@ Error Session::submit_gemm(const std::shared_ptr<GemmPlanRecord>& plan,
   return enqueue(
       [this, plan](Operation& op) -> Error {
         if (Error d = op.deadline_error("gemm", "pre_launch_deadline")) return d;
-        if (plan->a->released || plan->b->released || plan->c->released)
+        if (plan->a->released || plan->b->released || plan->c->released ||
+            (plan->bias && plan->bias->released))
           return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "gemm", "execute",
                             "a GEMM allocation was released");
         GemmHooks hooks;

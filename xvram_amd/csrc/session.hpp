@@ -65,6 +65,7 @@ struct GemmPlanRecord {
   GemmSpec spec;
   GemmPlanData plan;
   std::shared_ptr<AllocationRecord> a, b, c;
+  std::shared_ptr<AllocationRecord> bias; // fused-epilogue bias vector, if any
   uint64_t deadline_ms = 0;
 };
 
@@ -84,7 +85,8 @@ public:
 
   Error create_gemm_plan(const GemmSpec& spec, std::shared_ptr<AllocationRecord> a,
                          std::shared_ptr<AllocationRecord> b, std::shared_ptr<AllocationRecord> c,
-                         uint64_t deadline_ms, std::shared_ptr<GemmPlanRecord>& out);
+                         uint64_t deadline_ms, std::shared_ptr<GemmPlanRecord>& out,
+                         std::shared_ptr<AllocationRecord> bias = nullptr);
   Error submit_gemm(const std::shared_ptr<GemmPlanRecord>& plan, std::shared_ptr<Operation>& out);
 
   // One access of a transaction or prefetch, with the record kept alive until

@@ -5,7 +5,9 @@
 //   a_kcontig == true : A(i,p) = a[p + i*lda]   (op T)
 //   b_ncontig == false: B(p,j) = b[p + j*ldb]   (op N)
 //   b_ncontig == true : B(p,j) = b[j + p*ldb]   (op T)
-// beta == 0 means C is not read. The kernel requires 16-byte aligned bases,
+// beta == 0 means C is not read. Optional epilogue, applied after the beta
+// term: + bias_row[i] (per row of C), + bias_col[j] (per column), then ReLU
+// (negative values become 0; NaN is kept). The kernel requires 16-byte aligned bases,
 // leading dimensions that are multiples of 4 floats and `padded` = true (every
 // line may be read as whole 16-byte vectors up to its leading dimension), which
 // frame-packed panels always satisfy; anything else returns hipErrorInvalidValue.
@@ -25,6 +27,9 @@ struct SgemmLaunch {
   bool a_kcontig = false;
   bool b_ncontig = false;
   bool padded = false;
+  const float* bias_row = nullptr;
+  const float* bias_col = nullptr;
+  bool relu = false;
 };
 
 // Enqueues the launch on `stream` (a hipStream_t); returns a hipError_t.

@@ -9,6 +9,8 @@
 // computed with full-precision FP32 matrix instructions
 // (v_mfma_f32_32x32x2_f32; no xf32 / reduced-precision path). beta == 0 means
 // C is never read, so stale or NaN contents of a write-only C panel never leak.
+// An optional fused epilogue adds a per-row or per-column bias and applies
+// ReLU after the beta term (the host requests it on a tile's last K panel).
 //
 // Operand forms (canonical column-major, decided by the host planner):
 //   A is m x k: A_KCONTIG=false -> a[i + p*lda] (op N), true -> a[p + i*lda] (op T)
@@ -74,6 +76,9 @@ struct Params {
   int m, n, k;
   float alpha, beta;
   int tiles_m, tiles_n;
+  const float* bias_row; // per-row bias (nullptr = none)
+  const float* bias_col; // per-column bias (nullptr = none)
+  int relu;
 };
 
 __device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
@@ -301,11 +306,19 @@ __global__ __launch_bounds__(kThreads, 2) void sgemm_mfma_kernel(Params p) {
   // MFMA row 8*(v/4) + 4*lhalf + v%4 and MFMA column lrow, i.e. tile row
   // wm + 4*(that) + i and tile column wn + 2*lrow + j.
   const bool read_c = p.beta != 0.f;
+  const bool extra = p.bias_row != nullptr || p.bias_col != nullptr || p.relu != 0;
+  // Bias and activation after the beta term; ReLU keeps NaN (v < 0 is false).
+  const auto finish = [&](float v, int r, float bias_c) {
+    if (p.bias_row != nullptr) v += p.bias_row[r];
+    v += bias_c;
+    return (p.relu != 0 && v < 0.f) ? 0.f : v;
+  };
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int col = n0 + wn + 2 * lrow + j;
     if (col >= p.n) continue;
     float* cline = p.c + (int64_t)col * p.ldc;
+    const float bias_c = p.bias_col != nullptr ? p.bias_col[col] : 0.f;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int mrow = 8 * (v >> 2) + 4 * lhalf + (v & 3);
@@ -327,13 +340,20 @@ __global__ __launch_bounds__(kThreads, 2) void sgemm_mfma_kernel(Params p) {
           r.z = p.alpha * out[2];
           r.w = p.alpha * out[3];
         }
+        if (extra) {
+          r.x = finish(r.x, row, bias_c);
+          r.y = finish(r.y, row + 1, bias_c);
+          r.z = finish(r.z, row + 2, bias_c);
+          r.w = finish(r.w, row + 3, bias_c);
+        }
         *dst = r;
       } else {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           if (row + t < p.m) {
             const float val = p.alpha * out[t];
-            cline[row + t] = read_c ? val + p.beta * cline[row + t] : val;
+            const float sum = read_c ? val + p.beta * cline[row + t] : val;
+            cline[row + t] = extra ? finish(sum, row + t, bias_c) : sum;
           }
         }
       }
@@ -375,6 +395,9 @@ int launch_sgemm(const SgemmLaunch& launch, void* stream) {
   p.beta = launch.beta;
   p.tiles_m = (launch.m + kTileM - 1) / kTileM;
   p.tiles_n = (launch.n + kTileN - 1) / kTileN;
+  p.bias_row = launch.bias_row;
+  p.bias_col = launch.bias_col;
+  p.relu = launch.relu ? 1 : 0;
   auto* s = static_cast<hipStream_t>(stream);
   hipError_t err;
   if (!launch.a_kcontig && !launch.b_ncontig) err = launch_variant<false, false>(p, s);
