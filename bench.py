@@ -44,11 +44,14 @@ WORKLOADS = {
                        "16 GiB VRAM budget (3x)"),
     "c4_32768_nt_2g": (32768, 32768, 32768, OP_N, OP_T, 2 * GiB, 64 * MiB,
                        "FP32 SGEMM N/T 32768^3, 3 x 4 GiB operands, 2 GiB VRAM budget"),
-    "resident_8192_nn": (8192, 8192, 8192, OP_N, OP_N, 0, 256 * MiB,
-                         "FP32 SGEMM N/N 8192^3, fully resident (one launch)"),
-    "resident_16384_nt": (16384, 16384, 16384, OP_N, OP_T, 0, 1024 * MiB,
-                          "FP32 SGEMM N/T 16384^3, fully resident (one launch)"),
 }
+# Config 3, the resident sweep: N/N and N/T at 4096^3, 8192^3, 16384^3, one launch
+# each (frames large enough for whole operands, budget unrestricted).
+for _s, _frame in ((4096, 64 * MiB), (8192, 256 * MiB), (16384, 1024 * MiB)):
+    for _ob, _name in ((OP_N, "nn"), (OP_T, "nt")):
+        WORKLOADS[f"resident_{_s}_{_name}"] = (
+            _s, _s, _s, OP_N, _ob, 0, _frame,
+            f"FP32 SGEMM N/{'NT'[_ob]} {_s}^3, fully resident (one launch)")
 DEFAULT = "ns65536_nt_16g"
 # Config 5: 8 x [Y = ReLU(X W^T + b)], X 256 x 16384 ~ N(0,1), W 16384 x 16384 and
 # b ~ N(0, 1/16384), 2 GiB budget of 64 MiB frames; one step = one 8-layer forward.
