@@ -51,6 +51,26 @@ typedef struct xvram_amd_epilogue_v1 {
   uint64_t reserved[2];
 } xvram_amd_epilogue_v1;
 
+/* What a device reports about itself (no session needed). */
+typedef struct xvram_amd_device_info_v1 {
+  uint32_t struct_size;
+  int32_t ordinal;
+  char name[256];
+  char arch[64];       /* e.g. "gfx950:sramecc+:xnack-" */
+  char pci_bus_id[32]; /* "dddd:bb:dd.f", empty when unknown */
+  uint64_t total_memory_bytes;
+  uint64_t free_memory_bytes;
+  uint64_t granularity_minimum_bytes;
+  uint64_t granularity_recommended_bytes;
+  uint32_t compute_major;
+  uint32_t compute_minor;
+  uint32_t multiprocessor_count;
+  uint32_t vmm_supported;
+  int32_t driver_version;
+  int32_t runtime_version;
+  uint64_t reserved[4];
+} xvram_amd_device_info_v1;
+
 typedef struct xvram_amd_ext_v1 {
   uint32_t struct_size;
   uint32_t ext_version;
@@ -61,7 +81,9 @@ typedef struct xvram_amd_ext_v1 {
                                                       const xvram_gemm_desc_v1* desc,
                                                       const xvram_amd_epilogue_v1* epilogue,
                                                       xvram_gemm_plan* out_plan);
-  uint64_t reserved[4];
+  /* Fills `out` (struct_size >= v1, preserved) for device `ordinal`. */
+  xvram_status(XVRAM_CALL* device_get_info)(int32_t ordinal, xvram_amd_device_info_v1* out);
+  uint64_t reserved[3];
 } xvram_amd_ext_v1;
 
 XVRAM_API xvram_status XVRAM_CALL xvram_amd_get_ext(uint32_t requested_version,

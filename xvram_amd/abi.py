@@ -272,14 +272,80 @@ class EpilogueV1(Structure):
                 ("activation", c_uint32), ("reserved", c_uint64 * 2)]
 
 
+class DeviceInfoV1(Structure):
+    _fields_ = [("struct_size", c_uint32), ("ordinal", c_int32), ("name", c_char * 256),
+                ("arch", c_char * 64), ("pci_bus_id", c_char * 32),
+                ("total_memory_bytes", c_uint64), ("free_memory_bytes", c_uint64),
+                ("granularity_minimum_bytes", c_uint64),
+                ("granularity_recommended_bytes", c_uint64), ("compute_major", c_uint32),
+                ("compute_minor", c_uint32), ("multiprocessor_count", c_uint32),
+                ("vmm_supported", c_uint32), ("driver_version", c_int32),
+                ("runtime_version", c_int32), ("reserved", c_uint64 * 4)]
+
+
 class ExtV1(Structure):
     _fields_ = [("struct_size", c_uint32), ("ext_version", c_uint32),
                 ("gemm_plan_create_epilogue",
                  _F(c_uint32, _H, POINTER(GemmDesc), POINTER(EpilogueV1), POINTER(_H))),
-                ("reserved", c_uint64 * 4)]
+                ("device_get_info", _F(c_uint32, c_int32, POINTER(DeviceInfoV1))),
+                ("reserved", c_uint64 * 3)]
 
 
 def epilogue_init() -> EpilogueV1:
     e = EpilogueV1()
     e.struct_size = ctypes.sizeof(EpilogueV1)
     return e
+
+
+# ---- ABI v2 (include/xvram/xvram_v2.h) ------------------------------------------------
+
+ABI_VERSION_2 = 2
+COMPRESSION_DISABLED, COMPRESSION_ADAPTIVE, COMPRESSION_CAPACITY = 0, 1, 2
+COMPRESSION_CODEC_AUTO, COMPRESSION_CODEC_LZ4 = 0, 1
+
+
+class SessionConfigV2(Structure):
+    _fields_ = [("struct_size", c_uint32), ("flags", c_uint32), ("v1", SessionConfig),
+                ("compression_mode", c_uint32), ("compression_codec", c_uint32),
+                ("host_store_cap_bytes", c_uint64), ("host_headroom_bytes", c_uint64),
+                ("compression_workspace_cap_bytes", c_uint64), ("codec_slots", c_uint32),
+                ("codec_workers", c_uint32), ("reserved", c_uint64 * 8)]
+
+
+_TELEMETRY_V2_U64 = [
+    "logical_bytes", "host_stored_bytes", "host_stored_peak_bytes", "host_raw_bytes",
+    "host_compressed_bytes", "host_implicit_zero_bytes", "host_invalid_bytes",
+    "logical_h2d_bytes", "pcie_h2d_bytes", "logical_d2h_bytes", "pcie_d2h_bytes",
+    "raw_path_decisions", "cpu_lz4_gpu_decode_decisions", "gpu_lz4_decisions",
+    "never_compress_decisions", "raw_fallbacks", "cpu_codec_fallbacks", "gpu_codec_fallbacks",
+    "compression_attempts", "compression_commits", "decompression_attempts",
+    "decompression_commits", "generations_created", "generations_committed",
+    "generations_discarded", "codec_workspace_bytes", "codec_workspace_peak_bytes",
+    "codec_slot_bytes", "codec_slot_peak_bytes", "spill_reserved_bytes",
+    "spill_reserved_peak_bytes", "cpu_encode_nanoseconds", "cpu_decode_nanoseconds",
+    "gpu_encode_nanoseconds", "gpu_decode_nanoseconds", "verification_nanoseconds"]
+
+
+class SessionTelemetryV2(Structure):
+    _fields_ = ([("struct_size", c_uint32), ("flags", c_uint32), ("v1", SessionTelemetry)]
+                + [(n, c_uint64) for n in _TELEMETRY_V2_U64] + [("reserved", c_uint64 * 8)])
+
+
+class ApiV2(Structure):
+    _fields_ = [("v1", ApiV1),
+                ("session_create_v2", _F(c_uint32, POINTER(SessionConfigV2), POINTER(_H))),
+                ("session_get_telemetry_v2", _F(c_uint32, _H, POINTER(SessionTelemetryV2))),
+                ("reserved", c_uint64 * 14)]
+
+
+def session_config_v2_init() -> SessionConfigV2:
+    """XVRAM_SESSION_CONFIG_V2_INIT (note: it requests ADAPTIVE compression)."""
+    c = SessionConfigV2()
+    c.struct_size = ctypes.sizeof(SessionConfigV2)
+    c.v1 = session_config_init()
+    c.compression_mode = COMPRESSION_ADAPTIVE
+    c.compression_codec = COMPRESSION_CODEC_AUTO
+    c.compression_workspace_cap_bytes = 268435456
+    c.codec_slots = 2
+    c.codec_workers = 2
+    return c

@@ -1,7 +1,9 @@
 """Builds the native libraries in-tree.
 
   lib/libxvram.so          the product: C++20 host runtime + gfx950 HIP kernel,
-                           exporting only ``xvram_get_api@@XVRAM_0.1``;
+                           exporting ``xvram_get_api@@XVRAM_0.1`` and the
+                           extension table ``xvram_amd_get_ext@@XVRAM_AMD_EXT_1``;
+  lib/build_info.json      compiler, HIP and source versions of that build;
   lib/libxvram_synth.so    seeded synthetic operands for the benchmark;
   lib/libxvram_hostsim.so  the same host runtime over a host-memory device
                            simulation, for CPU-only tests (never used on the
@@ -11,7 +13,9 @@ Run ``python -m xvram_amd.build`` (or ``__graft_entry__.build()``).
 """
 from __future__ import annotations
 
+import json
 import os
+import re
 import subprocess
 import sys
 from concurrent.futures import ThreadPoolExecutor
@@ -47,6 +51,32 @@ def _compile_host(src, obj, extra):
     return obj
 
 
+def _first_line(cmd):
+    try:
+        out = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                             timeout=60).stdout
+        return out.strip().splitlines()[0] if out.strip() else "unknown"
+    except (OSError, subprocess.SubprocessError):
+        return "unknown"
+
+
+def build_info() -> dict:
+    """Versions recorded next to the libraries (read by reports)."""
+    hip_version = 0
+    try:
+        text = open(os.path.join(ROCM, "include", "hip", "hip_version.h")).read()
+        parts = {k: int(v) for k, v in re.findall(r"#define HIP_VERSION_(MAJOR|MINOR|PATCH) (\d+)", text)}
+        hip_version = parts["MAJOR"] * 10000000 + parts["MINOR"] * 100000 + parts["PATCH"]
+    except (OSError, KeyError):
+        pass
+    commit = _first_line(["git", "-C", ROOT, "rev-parse", "HEAD"])
+    if not re.fullmatch(r"[0-9a-f]{40}", commit):
+        commit = "unknown"
+    return {"version": "0.1.0", "git_commit": commit, "build_type": "Release",
+            "compiler": f"{_first_line([HIPCC, '--version'])}; {_first_line(['g++', '--version'])}",
+            "hip_version": hip_version, "offload_arch": ARCH}
+
+
 def build(hostsim: bool = True, product: bool = True, verbose: bool = True) -> None:
     os.makedirs(OBJ, exist_ok=True)
     os.makedirs(LIB, exist_ok=True)
@@ -76,6 +106,8 @@ def build(hostsim: bool = True, product: bool = True, verbose: bool = True) -> N
               f"-Wl,--version-script={os.path.join(CSRC, 'exports.map')}", "-Wl,--no-undefined",
               f"-L{ROCM}/lib", "-lamdhip64", "-lpthread"])
         os.replace(out + ".tmp", out)
+        with open(os.path.join(LIB, "build_info.json"), "w") as f:
+            json.dump(build_info(), f, indent=1)
         if verbose:
             print(f"built {out}")
     synth = os.path.join(LIB, "libxvram_synth.so")

@@ -280,6 +280,58 @@ xvram_status XVRAM_CALL session_create_entry(const xvram_session_config_v1* conf
   });
 }
 
+// src/sdk/api.cpp:209-233.
+Error validate_session_config_v2(const xvram_session_config_v2* c) {
+  if (!has_v1_size(c))
+    return incompatible("session_create_v2", "session config is null or smaller than v2");
+  if (c->flags != 0 || !all_zero(c->reserved, 8))
+    return invalid("session_create_v2", "unknown flags or non-zero reserved field");
+  if (Error e = validate_session_config(&c->v1)) return e;
+  if (c->compression_mode != XVRAM_COMPRESSION_DISABLED &&
+      c->compression_mode != XVRAM_COMPRESSION_ADAPTIVE &&
+      c->compression_mode != XVRAM_COMPRESSION_CAPACITY)
+    return invalid("session_create_v2", "invalid compression mode");
+  if (c->compression_codec != XVRAM_COMPRESSION_CODEC_AUTO &&
+      c->compression_codec != XVRAM_COMPRESSION_CODEC_LZ4)
+    return invalid("session_create_v2", "invalid compression codec");
+  if (c->compression_workspace_cap_bytes == 0 || c->codec_slots < 2 || c->codec_slots > 8 ||
+      c->codec_workers == 0 || c->codec_workers > 8)
+    return invalid("session_create_v2", "invalid compression workspace, slots, or workers");
+  return {};
+}
+
+// src/sdk/api.cpp:399-447 and sdk/runtime.cpp:1393-1397: a DISABLED session is
+// exactly a v1 session; compression modes are not provided on this device path.
+xvram_status XVRAM_CALL session_create_v2_entry(const xvram_session_config_v2* config,
+                                                xvram_session* out) noexcept {
+  if (out == nullptr) return XVRAM_STATUS_INVALID_ARGUMENT;
+  *out = nullptr;
+  const xvram_status checked = boundary({}, "session_create_v2", [&]() -> Error {
+    if (Error e = validate_session_config_v2(config)) return e;
+    if (config->compression_mode != XVRAM_COMPRESSION_DISABLED)
+      return make_error(XVRAM_STATUS_UNSUPPORTED, "session", "session_create_v2",
+                        "host compression is not provided on this device path; use "
+                        "XVRAM_COMPRESSION_DISABLED");
+    return {};
+  });
+  if (checked != XVRAM_STATUS_SUCCESS) return checked;
+  return session_create_entry(&config->v1, out);
+}
+
+xvram_status XVRAM_CALL session_get_telemetry_v2_entry(xvram_session s,
+                                                       xvram_session_telemetry_v2* out) noexcept {
+  if (s == nullptr || !s->state || !has_v1_size(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  return boundary(s->state, "session_get_telemetry_v2", [&]() -> Error {
+    const uint32_t caller = out->struct_size;
+    xvram_session_telemetry_v2 local{};
+    local.struct_size = sizeof(local);
+    if (Error e = s->state->backend->telemetry_v2(local)) return e;
+    local.struct_size = caller;
+    *out = local;
+    return {};
+  });
+}
+
 xvram_status XVRAM_CALL session_get_error_entry(xvram_session s, xvram_error_info_v1* out) noexcept {
   if (s == nullptr || !s->state || !has_v1_size(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
   return boundary(s->state, "session_get_error", [&]() -> Error {
@@ -753,12 +805,61 @@ const xvram_api_v1& api_v1() noexcept {
   return api;
 }
 
+// src/sdk/api.cpp:1002-1013: the v1 table first (its struct_size and
+// abi_version describing the v2 table), then the two v2 entries.
+const xvram_api_v2& api_v2() {
+  static const xvram_api_v2 api = [] {
+    xvram_api_v2 v{};
+    v.v1 = api_v1();
+    v.v1.struct_size = sizeof(v);
+    v.v1.abi_version = XVRAM_ABI_VERSION_2;
+    v.session_create_v2 = &session_create_v2_entry;
+    v.session_get_telemetry_v2 = &session_get_telemetry_v2_entry;
+    return v;
+  }();
+  return api;
+}
+
+xvram_status XVRAM_CALL device_get_info_entry(int32_t ordinal,
+                                              xvram_amd_device_info_v1* out) noexcept {
+  if (!has_v1_size(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  try {
+    DeviceInfo info;
+    if (int rc = describe_device(ordinal, info)) {
+      return rc == 101 /* hipErrorInvalidDevice */ ? XVRAM_STATUS_INVALID_ARGUMENT
+                                                   : XVRAM_STATUS_CUDA_ERROR;
+    }
+    const uint32_t caller = out->struct_size;
+    xvram_amd_device_info_v1 local{};
+    local.struct_size = caller;
+    local.ordinal = ordinal;
+    copy_text(local.name, info.name);
+    copy_text(local.arch, info.arch);
+    copy_text(local.pci_bus_id, info.pci_bus_id);
+    local.total_memory_bytes = info.total_memory;
+    local.free_memory_bytes = info.free_memory;
+    local.granularity_minimum_bytes = info.granularity_minimum;
+    local.granularity_recommended_bytes = info.granularity_recommended;
+    local.compute_major = static_cast<uint32_t>(info.compute_major);
+    local.compute_minor = static_cast<uint32_t>(info.compute_minor);
+    local.multiprocessor_count = static_cast<uint32_t>(info.multiprocessors);
+    local.vmm_supported = info.vmm_supported ? 1u : 0u;
+    local.driver_version = info.driver_version;
+    local.runtime_version = info.runtime_version;
+    *out = local;
+    return XVRAM_STATUS_SUCCESS;
+  } catch (...) {
+    return exception_error("device_get_info").status;
+  }
+}
+
 const xvram_amd_ext_v1& ext_v1() {
   static const xvram_amd_ext_v1 ext = [] {
     xvram_amd_ext_v1 v{};
     v.struct_size = sizeof(v);
     v.ext_version = XVRAM_AMD_EXT_VERSION_1;
     v.gemm_plan_create_epilogue = &gemm_plan_create_epilogue_entry;
+    v.device_get_info = &device_get_info_entry;
     return v;
   }();
   return ext;
@@ -785,6 +886,12 @@ extern "C" XVRAM_API xvram_status XVRAM_CALL xvram_get_api(uint32_t requested_ab
     if (out_api == nullptr || caller_api_size < sizeof(xvram_api_v1))
       return XVRAM_STATUS_INVALID_ARGUMENT;
     std::memcpy(out_api, &xvram::api_v1(), sizeof(xvram_api_v1));
+    return XVRAM_STATUS_SUCCESS;
+  }
+  if (requested_abi_version == XVRAM_ABI_VERSION_2) {
+    if (out_api == nullptr || caller_api_size < sizeof(xvram_api_v2))
+      return XVRAM_STATUS_INVALID_ARGUMENT;
+    std::memcpy(out_api, &xvram::api_v2(), sizeof(xvram_api_v2));
     return XVRAM_STATUS_SUCCESS;
   }
   return XVRAM_STATUS_INCOMPATIBLE_ABI;

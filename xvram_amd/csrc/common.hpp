@@ -3,6 +3,7 @@
 
 #include <xvram/xvram.h>
 #include <xvram/xvram_amd_ext.h>
+#include <xvram/xvram_v2.h>
 
 #include <chrono>
 #include <cstdint>

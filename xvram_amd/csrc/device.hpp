@@ -14,6 +14,7 @@
 
 #include <cstdint>
 #include <memory>
+#include <string>
 
 #include "sgemm_launch.hpp"
 
@@ -21,6 +22,23 @@ namespace xvram {
 
 using Stream = void*;
 using Event = void*;
+
+// What a device reports about itself (for reports and diagnostics).
+struct DeviceInfo {
+  std::string name;
+  std::string arch;       // e.g. "gfx950:sramecc+:xnack-"
+  std::string pci_bus_id; // "dddd:bb:dd.f"
+  uint64_t total_memory = 0;
+  uint64_t free_memory = 0;
+  uint64_t granularity_minimum = 0;
+  uint64_t granularity_recommended = 0;
+  int compute_major = 0;
+  int compute_minor = 0;
+  int multiprocessors = 0;
+  bool vmm_supported = false;
+  int driver_version = 0;
+  int runtime_version = 0;
+};
 
 class Device {
 public:
@@ -70,5 +88,8 @@ public:
 
 // Defined by exactly one of device_hip.cpp / device_hostsim.cpp.
 std::unique_ptr<Device> make_device();
+// Describes device `ordinal` without disturbing the calling thread's current
+// device; returns 0 or the native error code.
+int describe_device(int ordinal, DeviceInfo& out);
 
 } // namespace xvram

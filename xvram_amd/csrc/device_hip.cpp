@@ -8,6 +8,8 @@
 // hipMemcpy2DAsync (strided panels instead of linear chunks).
 #include <hip/hip_runtime_api.h>
 
+#include <cstdio>
+
 #include "device.hpp"
 
 namespace xvram {
@@ -159,5 +161,45 @@ private:
 } // namespace
 
 std::unique_ptr<Device> make_device() { return std::make_unique<HipDevice>(); }
+
+int describe_device(int ordinal, DeviceInfo& out) {
+  int count = 0;
+  if (hipError_t e = hipGetDeviceCount(&count); e != hipSuccess) return e;
+  if (ordinal < 0 || ordinal >= count) return hipErrorInvalidDevice;
+  hipDeviceProp_t p{};
+  if (hipError_t e = hipGetDeviceProperties(&p, ordinal); e != hipSuccess) return e;
+  out.name = p.name;
+  out.arch = p.gcnArchName;
+  char bus[32];
+  std::snprintf(bus, sizeof(bus), "%04x:%02x:%02x.0", p.pciDomainID, p.pciBusID, p.pciDeviceID);
+  out.pci_bus_id = bus;
+  out.total_memory = p.totalGlobalMem;
+  out.compute_major = p.major;
+  out.compute_minor = p.minor;
+  out.multiprocessors = p.multiProcessorCount;
+  int vmm = 0;
+  if (hipDeviceGetAttribute(&vmm, hipDeviceAttributeVirtualMemoryManagementSupported, ordinal) ==
+      hipSuccess)
+    out.vmm_supported = vmm != 0;
+  hipMemAllocationProp prop{};
+  prop.type = hipMemAllocationTypePinned;
+  prop.location.type = hipMemLocationTypeDevice;
+  prop.location.id = ordinal;
+  size_t g = 0;
+  if (hipMemGetAllocationGranularity(&g, &prop, hipMemAllocationGranularityMinimum) == hipSuccess)
+    out.granularity_minimum = g;
+  if (hipMemGetAllocationGranularity(&g, &prop, hipMemAllocationGranularityRecommended) ==
+      hipSuccess)
+    out.granularity_recommended = g;
+  (void)hipDriverGetVersion(&out.driver_version);
+  (void)hipRuntimeGetVersion(&out.runtime_version);
+  int current = 0;
+  if (hipGetDevice(&current) == hipSuccess && hipSetDevice(ordinal) == hipSuccess) {
+    size_t f = 0, t = 0;
+    if (hipMemGetInfo(&f, &t) == hipSuccess) out.free_memory = f;
+    (void)hipSetDevice(current);
+  }
+  return hipSuccess;
+}
 
 } // namespace xvram

@@ -311,6 +311,19 @@ private:
 
 std::unique_ptr<Device> make_device() { return std::make_unique<HostSimDevice>(); }
 
+int describe_device(int ordinal, DeviceInfo& out) {
+  if (ordinal != 0) return 101; // hipErrorInvalidDevice
+  std::lock_guard<std::mutex> lock(g_sim.mutex);
+  out.name = "xvram host simulation";
+  out.arch = "hostsim";
+  out.pci_bus_id.clear();
+  out.total_memory = g_sim.total_bytes;
+  out.free_memory = g_sim.free_bytes;
+  out.granularity_minimum = out.granularity_recommended = 4096;
+  out.vmm_supported = true;
+  return 0;
+}
+
 } // namespace xvram
 
 // Test-only controls exported by libxvram_hostsim.so.

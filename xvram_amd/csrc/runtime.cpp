@@ -278,6 +278,7 @@ Error Runtime::allocate(uint64_t bytes, uint64_t alignment, uint32_t priority,
   a.priority = priority;
   a.host = static_cast<char*>(host);
   pinned_bytes_ += bytes;
+  pinned_peak_bytes_ = std::max(pinned_peak_bytes_, pinned_bytes_);
   auto [it, inserted] = allocations_.emplace(a.id, a);
   (void)inserted;
   out = &it->second;
@@ -981,7 +982,9 @@ Error Runtime::finish_operation(uint64_t operation_id) {
     f.ready_pending = false;
     if (first) continue;
     // Every stream has drained: all fills landed and every retire event of
-    // this operation has completed.
+    // this operation has completed (the host has now observed it: an event
+    // boundary for each frame that still had one outstanding).
+    if (f.retire_pending) ++t_.event_boundaries;
     f.retire_pending = false;
     f.completed = f.generation;
     if (f.state == EntryState::h2d_in_flight) move(f, EntryState::resident_clean);

@@ -255,6 +255,9 @@ public:
 
   // Telemetry snapshot in public form.
   void telemetry(xvram_session_telemetry_v1& out) const;
+  // Host-store figures of the v2 telemetry: every byte is stored raw.
+  uint64_t logical_bytes() const { return pinned_bytes_; }
+  uint64_t host_stored_peak_bytes() const { return pinned_peak_bytes_; }
 
   Error device_failure(int code, std::string_view stage, std::string_view operation);
   Error poison(std::string_view stage, std::string_view operation, std::string_view message);
@@ -319,7 +322,8 @@ private:
 
   std::map<uint64_t, HostAllocation> allocations_;
   uint64_t next_allocation_id_ = 1;
-  uint64_t pinned_bytes_ = 0;
+  uint64_t pinned_bytes_ = 0;      // sum of live allocation sizes (all raw host bytes)
+  uint64_t pinned_peak_bytes_ = 0;
 
   // Write-backs still in flight in this operation: a later refill of the same
   // entry waits for them.

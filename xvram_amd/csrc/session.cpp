@@ -154,6 +154,24 @@ void Session::refresh_telemetry() {
   runtime_.telemetry(t);
   std::lock_guard<std::mutex> lock(telemetry_mutex_);
   telemetry_ = t;
+  logical_bytes_ = runtime_.logical_bytes();
+  host_stored_peak_bytes_ = runtime_.host_stored_peak_bytes();
+}
+
+// The v2 view (reference sdk/runtime.cpp:572-620) of a session without host
+// compression: the host store holds every logical byte raw, and the logical
+// and PCIe traffic counters equal the v1 byte counters.
+Error Session::telemetry_v2(xvram_session_telemetry_v2& out) const {
+  std::lock_guard<std::mutex> lock(telemetry_mutex_);
+  out.v1 = telemetry_;
+  out.v1.struct_size = sizeof(out.v1);
+  out.logical_bytes = logical_bytes_;
+  out.host_stored_bytes = logical_bytes_;
+  out.host_stored_peak_bytes = host_stored_peak_bytes_;
+  out.host_raw_bytes = logical_bytes_;
+  out.logical_h2d_bytes = out.pcie_h2d_bytes = telemetry_.bytes_h2d;
+  out.logical_d2h_bytes = out.pcie_d2h_bytes = telemetry_.bytes_d2h;
+  return {};
 }
 
 void Session::worker_main() {

@@ -104,6 +104,7 @@ public:
                            void* user_data, std::shared_ptr<Operation>& out);
 
   Error telemetry(xvram_session_telemetry_v1& out) const;
+  Error telemetry_v2(xvram_session_telemetry_v2& out) const;
   Error drain(uint64_t timeout_ms);
   Error close(uint64_t timeout_ms);
 
@@ -145,6 +146,8 @@ private:
 
   mutable std::mutex telemetry_mutex_;
   xvram_session_telemetry_v1 telemetry_{};
+  uint64_t logical_bytes_ = 0;
+  uint64_t host_stored_peak_bytes_ = 0;
 };
 
 } // namespace xvram
