@@ -8,9 +8,13 @@
 //   - ref_validate_problem -> src/gemm/planner.cpp:785-859
 //   - ref_legal_transition -> src/residency/core.cpp:304-332
 //   - ref_normalize        -> src/residency/core.cpp:128-276
+//   - ref_policy_run       -> src/residency/policy.cpp:88-187
 #include "gemm/planner.hpp"
 #include "gemm_bench/pattern.hpp"
 #include "residency/core.hpp"
+#include "residency/policy.hpp"
+
+#include <memory>
 
 #include <cstdint>
 #include <cstdio>
@@ -121,6 +125,56 @@ int ref_normalize(const uint64_t* allocs, uint64_t n_allocs, const uint64_t* ran
   }
   *n_out_ranges = plan.normalized_ranges.size();
   *n_out_chunks = plan.chunks.size();
+  return 0;
+}
+
+// The command program of the library's hostsim hook, run against the
+// reference's ClockPolicy (kind 0) or LruPolicy (kind 1); ids are chunk
+// indices of allocation 1.
+int ref_policy_run(int kind, const uint64_t* program, uint64_t commands, uint64_t* results) {
+  using namespace xvram::residency;
+  std::unique_ptr<VictimPolicy> policy;
+  if (kind == 1) policy = std::make_unique<LruPolicy>();
+  else policy = std::make_unique<ClockPolicy>();
+  std::vector<VictimCandidate> candidates;
+  const auto key = [](uint64_t id) { return ChunkKey{AllocationId{1}, id}; };
+  for (uint64_t i = 0; i < commands; ++i) {
+    const uint64_t* c = program + 7 * i;
+    results[i] = 0;
+    switch (c[0]) {
+    case 0: policy->insert(key(c[1]), c[2], c[3] != 0, c[4] != 0); break;
+    case 1: policy->touch(key(c[1]), c[2], c[3] != 0); break;
+    case 2: results[i] = policy->erase(key(c[1])) ? 1 : 0; break;
+    case 3: {
+      VictimCandidate v{key(c[1]), static_cast<ChunkState>(c[2])};
+      v.hot = c[3] != 0;
+      v.pin_count = static_cast<std::uint32_t>(c[4]);
+      v.in_flight = c[5] != 0;
+      v.in_current_working_set = c[6] != 0;
+      bool replaced = false;
+      for (auto& existing : candidates)
+        if (existing.key == v.key) {
+          existing = v;
+          replaced = true;
+        }
+      if (!replaced) candidates.push_back(v);
+      break;
+    }
+    case 4:
+      for (size_t k = 0; k < candidates.size(); ++k)
+        if (candidates[k].key == key(c[1])) {
+          candidates.erase(candidates.begin() + static_cast<std::ptrdiff_t>(k));
+          break;
+        }
+      break;
+    case 5: {
+      const auto victim = policy->select_victim(candidates);
+      results[i] = victim ? victim->chunk_index : ~0ull;
+      break;
+    }
+    default: return -1;
+    }
+  }
   return 0;
 }
 }

@@ -410,3 +410,58 @@ extern "C" __attribute__((visibility("default"))) int xvram_hostsim_normalize(
   *n_out_chunks = chunks.size();
   return 0;
 }
+
+// Runs a command program against a fresh victim policy (kind: 0 CLOCK, 1 LRU).
+// Each command is 7 words {op, a, b, c, d, e, f}; one result word per command:
+//   op 0 insert(id=a, sequence=b, speculative=c, one_touch=d)           -> 0
+//   op 1 touch(id=a, sequence=b, one_touch=c)                           -> 0
+//   op 2 erase(id=a)                                                    -> 1 if erased
+//   op 3 set candidate id=a: state=b, hot=c, pins=d, in_flight=e, in_working_set=f -> 0
+//   op 4 drop candidate id=a                                            -> 0
+//   op 5 select_victim(current candidates)                              -> id or ~0
+extern "C" __attribute__((visibility("default"))) int xvram_hostsim_policy_run(
+    int kind, const uint64_t* program, uint64_t commands, uint64_t* results) {
+  std::unique_ptr<xvram::EvictionPolicy> policy =
+      xvram::make_policy(kind == 1 ? XVRAM_CACHE_POLICY_LRU : XVRAM_CACHE_POLICY_CLOCK);
+  std::vector<xvram::VictimCandidate> candidates;
+  for (uint64_t i = 0; i < commands; ++i) {
+    const uint64_t* c = program + 7 * i;
+    results[i] = 0;
+    switch (c[0]) {
+    case 0: policy->insert(c[1], c[2], c[3] != 0, c[4] != 0); break;
+    case 1: policy->touch(c[1], c[2], c[3] != 0); break;
+    case 2: results[i] = policy->erase(c[1]) ? 1 : 0; break;
+    case 3: {
+      xvram::VictimCandidate v;
+      v.id = c[1];
+      v.state = static_cast<xvram::EntryState>(c[2]);
+      v.hot = c[3] != 0;
+      v.pins = static_cast<uint32_t>(c[4]);
+      v.in_flight = c[5] != 0;
+      v.in_working_set = c[6] != 0;
+      bool replaced = false;
+      for (auto& existing : candidates)
+        if (existing.id == v.id) {
+          existing = v;
+          replaced = true;
+        }
+      if (!replaced) candidates.push_back(v);
+      break;
+    }
+    case 4:
+      for (size_t k = 0; k < candidates.size(); ++k)
+        if (candidates[k].id == c[1]) {
+          candidates.erase(candidates.begin() + static_cast<std::ptrdiff_t>(k));
+          break;
+        }
+      break;
+    case 5: {
+      const auto victim = policy->select_victim(candidates);
+      results[i] = victim ? *victim : ~0ull;
+      break;
+    }
+    default: return -1;
+    }
+  }
+  return 0;
+}

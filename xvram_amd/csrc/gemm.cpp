@@ -526,6 +526,8 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
   }
 
   const auto acquire_launch = [&](size_t idx) -> Error {
+    // Sample the live budget (rate-limited) before each launch's panels.
+    if (Error e = rt.refresh_budget(3, 0, false)) return e;
     const TileLaunch& l = plan.launches[idx];
     const LaunchGeom g = launch_geom(plan, l);
     Acquired acq;

@@ -133,6 +133,10 @@ Error Runtime::setup() {
                       "cache target leaves fewer than two frames");
   target_bytes_ = target;
   capacity_ = (target - config_.workspace_reserve_bytes) / frame_bytes_;
+  max_capacity_ = capacity_;
+  configured_cap_ = config_.cache_target_bytes != 0 ? config_.cache_target_bytes : total_bytes;
+  last_budget_sample_ = Clock::now();
+  policy_ = make_policy(config_.cache_policy);
   t_.cache_target_bytes = target_bytes_;
   t_.cache_target_minimum_bytes = target_bytes_;
   t_.cache_target_maximum_bytes = target_bytes_;
@@ -347,12 +351,22 @@ Error Runtime::map_frame_at(Frame& f, uint64_t address) {
   }
   if (!f.handle) {
     uint64_t handle = 0;
-    if (int rc = device_->mem_create(frame_bytes_, &handle)) {
-      if (rc == 2)
-        return make_error(XVRAM_STATUS_DEVICE_OUT_OF_MEMORY, "cache", "mem_create",
-                          "physical frame allocation failed");
-      return device_failure(rc, "cache", "mem_create");
+    int rc = device_->mem_create(frame_bytes_, &handle);
+    if (rc == 2 /* out of memory */) {
+      // Someone else took device memory: resample the budget once (which may
+      // shrink the pool) and retry if this frame is still inside it
+      // (reference create_handle, runtime.cpp:3184-3211).
+      ++t_.target_oom_retries;
+      if (Error e = refresh_budget(0, workspace_bytes_, true)) return e;
+      if (f.index >= capacity_)
+        return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "cache", "mem_create_retry",
+                          "live budget shrink removed the frame selected for allocation");
+      rc = device_->mem_create(frame_bytes_, &handle);
     }
+    if (rc == 2)
+      return make_error(XVRAM_STATUS_DEVICE_OUT_OF_MEMORY, "cache", "mem_create",
+                        "physical frame allocation failed");
+    if (rc) return device_failure(rc, "cache", "mem_create");
     f.handle = handle;
     ++t_.physical_handles_created;
   }
@@ -423,6 +437,7 @@ Error Runtime::wait_retired(Frame& f) {
 Error Runtime::evict_key(Frame& f, bool was_dirty) {
   if (!f.keyed) return {};
   index_.erase(f.key);
+  policy_->erase(f.index);
   f.keyed = false;
   f.dirty = false;
   f.ready_pending = false;
@@ -441,16 +456,29 @@ Error Runtime::evict_key(Frame& f, bool was_dirty) {
   return {};
 }
 
-// Frame choice (reference acquire_frame, runtime.cpp:3470-3529): the free
-// frame idle longest, else a not-yet-created frame, else the least-recently-
-// used unpinned entry — clean entries before dirty ones (a dirty victim is
-// written back first). The choice depends only on the schedule, never on how
-// far the device has progressed, so the accounting of a run is reproducible.
+bool Runtime::allocation_hot(uint64_t allocation_id) {
+  const HostAllocation* a = find(allocation_id);
+  return a && a->priority == XVRAM_ALLOCATION_HOT;
+}
+
+bool Runtime::allocation_streaming(uint64_t allocation_id) {
+  const HostAllocation* a = find(allocation_id);
+  return a && a->priority == XVRAM_ALLOCATION_STREAMING;
+}
+
+// Frame choice (reference acquire_frame, runtime.cpp:3470-3529): a free frame
+// (the one idle longest), else a not-yet-created frame, else the victim the
+// session's policy names among unpinned resident entries (a dirty victim is
+// written back first). Only frames inside the live capacity are considered.
+// The choice depends only on the schedule, never on how far the device has
+// progressed, so the accounting of a run is reproducible.
 Error Runtime::select_frame(Frame*& out) {
   Frame* free_frame = nullptr;
   Frame* uncreated = nullptr;
-  Frame* victim = nullptr;
-  for (Frame& f : frames_) {
+  std::vector<VictimCandidate> candidates;
+  candidates.reserve(capacity_);
+  for (uint64_t i = 0; i < capacity_; ++i) {
+    Frame& f = frames_[i];
     if (!f.handle) {
       if (!uncreated) uncreated = &f;
       continue;
@@ -460,27 +488,27 @@ Error Runtime::select_frame(Frame*& out) {
       if (!free_frame || f.last_use < free_frame->last_use) free_frame = &f;
       continue;
     }
-    if (!victim) {
-      victim = &f;
-    } else {
-      const bool better = (victim->dirty && !f.dirty) ||
-                          (victim->dirty == f.dirty && f.last_use < victim->last_use);
-      if (better) victim = &f;
-    }
+    VictimCandidate c;
+    c.id = f.index;
+    c.state = f.state;
+    c.hot = allocation_hot(f.key.allocation_id);
+    candidates.push_back(c);
   }
   Frame* chosen = free_frame ? free_frame : uncreated;
-  if (!chosen && victim) {
-    if (victim->dirty) {
-      if (Error e = writeback_and_evict(*victim)) return e;
+  if (!chosen) {
+    const std::optional<uint64_t> victim = policy_->select_victim(candidates);
+    if (!victim)
+      return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "cache", "select_frame",
+                        "every cache frame is pinned by the current working set");
+    Frame& v = frames_[*victim];
+    if (v.dirty) {
+      if (Error e = writeback_and_evict(v)) return e;
     } else {
-      if (Error e = evict_key(*victim, false)) return e;
+      if (Error e = evict_key(v, false)) return e;
       ++t_.clean_evictions;
     }
-    chosen = victim;
+    chosen = &v;
   }
-  if (!chosen)
-    return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "cache", "select_frame",
-                      "every cache frame is pinned by the current working set");
   if (Error e = wait_retired(*chosen)) return e;
   if (chosen->used_before) ++t_.handle_reuses;
   chosen->used_before = true;
@@ -509,6 +537,8 @@ Error Runtime::fill_entry(Frame& f, const PanelKey& key, uint64_t packed_pitch, 
   f.dirty = false;
   f.last_use = ++tick_;
   index_[key] = f.index;
+  policy_->insert(f.index, ++policy_sequence_, prefetching_,
+                  allocation_streaming(key.allocation_id));
   t_.resident_bytes += frame_bytes_;
   t_.resident_bytes_peak = std::max(t_.resident_bytes_peak, t_.resident_bytes);
   check_generation(f);
@@ -554,6 +584,8 @@ Error Runtime::acquire(const PanelKey& key, uint64_t packed_pitch, bool needs_da
       ++f.pins;
       f.last_use = ++tick_;
       ++t_.cache_hits;
+      if (!prefetching_)
+        policy_->touch(f.index, ++policy_sequence_, allocation_streaming(key.allocation_id));
       out = &f;
       return {};
     }
@@ -830,12 +862,15 @@ Error Runtime::acquire_chunk(ChunkUse& use) {
     ++f.pins;
     f.last_use = ++tick_;
     ++t_.cache_hits;
+    if (!prefetching_)
+      policy_->touch(f.index, ++policy_sequence_, allocation_streaming(key.allocation_id));
     use.frame = &f;
     return {};
   }
   const uint64_t address = a->va + key.offset;
   Frame* f = nullptr;
-  for (Frame& g : frames_) {
+  for (uint64_t i = 0; i < capacity_; ++i) {
+    Frame& g = frames_[i];
     // The frame that last held this chunk may still be mapped at its address.
     if (g.mapped_at == address && !g.keyed && g.pins == 0) {
       if (Error e = wait_retired(g)) return e;
@@ -863,6 +898,7 @@ Error Runtime::run_transaction(const std::vector<AccessSpan>& ranges, uint64_t w
   std::vector<ChunkUse> chunks;
   std::vector<AccessSpan> normalized;
   Error result = plan_chunks(ranges, chunks, normalized, "normalize_accesses");
+  if (!result) result = refresh_budget(chunks.size(), workspace_bytes, false);
   if (!result && chunks.size() > capacity_)
     result = make_error(XVRAM_STATUS_BUDGET_PRESSURE, "transaction", "working_set",
                         "declared working set exceeds the cache target");
@@ -933,16 +969,112 @@ Error Runtime::run_prefetch(const std::vector<AccessSpan>& ranges, uint64_t oper
   std::vector<ChunkUse> chunks;
   std::vector<AccessSpan> normalized;
   Error result = plan_chunks(ranges, chunks, normalized, "prefetch");
+  if (!result) result = refresh_budget(chunks.size(), 0, false);
   if (!result && chunks.size() > capacity_)
     result = make_error(XVRAM_STATUS_BUDGET_PRESSURE, "transaction", "prefetch",
                         "prefetch working set exceeds the cache target");
+  prefetching_ = true; // fills are speculative until a transaction uses them
   for (size_t i = 0; !result && i < chunks.size(); ++i) {
     chunks[i].needs_data = true; // a prefetched chunk must hold valid data
     if (Error e = acquire_chunk(chunks[i])) result = e;
     else result = release_after(*chunks[i].frame, h2d_, false);
   }
+  prefetching_ = false;
   Error finish = finish_operation(operation_id);
   return result ? result : finish;
+}
+
+// ---- live budget -------------------------------------------------------------------
+
+// Gives a frame's physical memory back: its entry is written back (dirty) or
+// dropped, its mapping removed and its handle released.
+Error Runtime::release_frame(Frame& f) {
+  if (f.keyed) {
+    if (f.dirty) {
+      if (Error e = writeback_and_evict(f)) return e;
+    } else {
+      if (Error e = evict_key(f, false)) return e;
+      ++t_.clean_evictions;
+    }
+  }
+  if (Error e = unmap_frame(f)) return e; // waits for the frame's last consumer
+  if (f.handle) {
+    if (int rc = device_->mem_release(f.handle)) return device_failure(rc, "budget", "mem_release");
+    f.handle = 0;
+    ++t_.physical_handles_released;
+  }
+  if (f.state == EntryState::evicting) move(f, EntryState::host_clean);
+  f.used_before = false;
+  return {};
+}
+
+Error Runtime::refresh_budget(uint64_t required_frames, uint64_t required_workspace, bool force) {
+  const Clock::time_point now = Clock::now();
+  if (!force && config_.budget_poll_ms > 0 &&
+      now - last_budget_sample_ < std::chrono::milliseconds(config_.budget_poll_ms))
+    return {};
+  last_budget_sample_ = now;
+  uint64_t free_bytes = 0, total_bytes = 0;
+  if (int rc = device_->mem_info(&free_bytes, &total_bytes))
+    return device_failure(rc, "budget", "mem_info");
+  ++t_.budget_sample_count;
+  t_.cuda_free_bytes_end = free_bytes;
+  t_.cuda_free_bytes_minimum = std::min(t_.cuda_free_bytes_minimum, free_bytes);
+
+  // Memory this session could hand back counts as available to it.
+  uint64_t created = 0;
+  for (const Frame& f : frames_)
+    if (f.handle) ++created;
+  const uint64_t managed = created * frame_bytes_ + workspace_bytes_;
+  const uint64_t reclaimable =
+      free_bytes > UINT64_MAX - managed ? UINT64_MAX : free_bytes + managed;
+  const uint64_t after_headroom = reclaimable > config_.device_headroom_bytes
+                                      ? reclaimable - config_.device_headroom_bytes
+                                      : 0;
+  uint64_t target = std::min(configured_cap_, after_headroom);
+  target -= target % frame_bytes_;
+  const uint64_t reserve = config_.workspace_reserve_bytes;
+  uint64_t frames = target > reserve ? (target - reserve) / frame_bytes_ : 0;
+  frames = std::min(frames, max_capacity_);
+
+  if (frames < capacity_) {
+    // Shrink now: every tail frame must be idle (checked before anything changes).
+    for (uint64_t i = frames; i < capacity_; ++i)
+      if (frames_[i].pins > 0)
+        return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "budget", "shrink_preflight",
+                          "an active working-set frame defers the live target shrink");
+    for (uint64_t i = frames; i < capacity_; ++i)
+      if (Error e = release_frame(frames_[i])) return e;
+    capacity_ = frames;
+    target_bytes_ = target;
+    t_.cache_target_bytes = target;
+    t_.cache_target_minimum_bytes = std::min(t_.cache_target_minimum_bytes, target);
+    ++t_.budget_shrinks;
+    growth_samples_ = 0;
+  }
+  if (t_.resident_bytes + workspace_bytes_ > target)
+    return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "budget", "managed_device_accounting",
+                      "managed residency and workspace exceed the live safe device target");
+  uint64_t required = 0;
+  if (!checked_mul(required_frames, frame_bytes_, required) ||
+      !checked_add(required, required_workspace, required) || target < required ||
+      target <= reserve || frames < required_frames)
+    return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "budget", "working_set",
+                      "live device budget fell below the next working set");
+  if (frames > capacity_) {
+    // Grow slowly: two frames after ten consecutive samples with room for them.
+    if (++growth_samples_ >= 10 && frames >= capacity_ + 2) {
+      capacity_ = std::min(frames, capacity_ + 2);
+      target_bytes_ = std::min(target, capacity_ * frame_bytes_ + reserve);
+      t_.cache_target_bytes = target_bytes_;
+      t_.cache_target_maximum_bytes = std::max(t_.cache_target_maximum_bytes, target_bytes_);
+      ++t_.budget_grows;
+      growth_samples_ = 0;
+    }
+  } else {
+    growth_samples_ = 0;
+  }
+  return {};
 }
 
 // ---- operation bracketing ------------------------------------------------------

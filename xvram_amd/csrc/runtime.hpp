@@ -33,6 +33,8 @@
 
 #include "common.hpp"
 #include "device.hpp"
+#include "entry_state.hpp"
+#include "policy.hpp"
 
 namespace xvram {
 
@@ -45,6 +47,7 @@ struct RuntimeConfig {
   uint32_t prefetch_distance = 2;
   uint32_t cache_policy = XVRAM_CACHE_POLICY_CLOCK;
   uint64_t max_transaction_ms = 250;
+  uint64_t budget_poll_ms = 100;
 };
 
 struct HostAllocation {
@@ -90,26 +93,6 @@ struct PanelKey {
 // (exact for rectangles of equal pitch, conservative otherwise).
 bool keys_overlap(const PanelKey& a, const PanelKey& b);
 
-// Entry states and their legal transitions: the reference's chunk state
-// machine (src/residency/core.hpp:102-113, core.cpp:304-332) applied to every
-// cache entry (panel or chunk), plus one edge of this design:
-// resident_dirty -> evicting, the discard of a failed operation's unwritten
-// output (the host copy stays authoritative; the reference poisons instead).
-// An illegal move is counted in telemetry (unsafe_transitions), never taken
-// silently.
-enum class EntryState : uint32_t {
-  host_clean,
-  prefetch_queued,
-  mapping,
-  h2d_in_flight,
-  resident_clean,
-  resident_dirty,
-  writeback_queued,
-  d2h_in_flight,
-  evicting,
-  poisoned,
-};
-bool is_legal_transition(EntryState from, EntryState to);
 
 struct Frame {
   uint64_t index = 0;
@@ -244,6 +227,13 @@ public:
   // ---- operation bracketing ----
   // Marks the start of an operation: every stream is ordered after it.
   Error begin_operation();
+  // Live budget (reference refresh_budget, runtime.cpp:3213-3468): samples
+  // hipMemGetInfo at most every budget_poll_ms (always when forced), shrinks
+  // the frame pool at once when the safe target falls (writing back and
+  // releasing the tail frames; BUDGET_PRESSURE if one of them is in use), grows
+  // it by two frames after ten consecutive samples with room for two more, and
+  // fails with BUDGET_PRESSURE when the next working set no longer fits.
+  Error refresh_budget(uint64_t required_frames, uint64_t required_workspace, bool force);
   // Waits for every stream; folds kernel/copy intervals into telemetry, applies
   // the duration guard, writes the optional trace line.
   Error finish_operation(uint64_t operation_id);
@@ -281,6 +271,9 @@ private:
   Error map_frame_at(Frame& frame, uint64_t address);
   Error unmap_frame(Frame& frame);
   Error select_frame(Frame*& out);
+  bool allocation_hot(uint64_t allocation_id);
+  bool allocation_streaming(uint64_t allocation_id);
+  Error release_frame(Frame& frame);
   Error fill_entry(Frame& f, const PanelKey& key, uint64_t packed_pitch, bool needs_data);
   Error wait_retired(Frame& frame);
   Error evict_key(Frame& frame, bool was_dirty);
@@ -301,8 +294,15 @@ private:
 
   uint64_t granularity_ = 0;
   uint64_t frame_bytes_ = 0;
-  uint64_t capacity_ = 0;
+  uint64_t capacity_ = 0;       // frames usable now (live budget)
+  uint64_t max_capacity_ = 0;   // frames reserved at setup (the arena)
+  uint64_t configured_cap_ = 0; // cache_target_bytes, or total device memory when 0
   uint64_t target_bytes_ = 0;
+  Clock::time_point last_budget_sample_{};
+  uint32_t growth_samples_ = 0;
+  std::unique_ptr<EvictionPolicy> policy_;
+  uint64_t policy_sequence_ = 0;
+  bool prefetching_ = false;
   uint64_t arena_ = 0;
   uint64_t arena_bytes_ = 0;
   std::vector<Frame> frames_;

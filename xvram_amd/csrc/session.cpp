@@ -119,6 +119,7 @@ RuntimeConfig runtime_config(const xvram_session_config_v1& c) {
   r.prefetch_distance = c.prefetch_distance;
   r.cache_policy = c.cache_policy;
   r.max_transaction_ms = c.max_transaction_ms == 0 ? 250 : c.max_transaction_ms;
+  r.budget_poll_ms = c.budget_poll_ms;
   return r;
 }
 
