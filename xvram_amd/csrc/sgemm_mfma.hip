@@ -271,6 +271,10 @@ __global__ __launch_bounds__(kThreads, 2) void sgemm_mfma_kernel(Params p) {
     for (; st + 1 < full_stages; ++st) {
       const int buf = st & 1;
       load_full<AK, BN>(pa + (st + 1) * a_step, pb + (st + 1) * b_step, p.lda, p.ldb, s);
+      // Keep the next stage's global loads here, a whole stage of MFMAs ahead
+      // of their use (the scheduler would otherwise sink them next to the LDS
+      // stores to shorten register live ranges, exposing their latency).
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int q = 0; q < kSteps - 1; ++q) {
         read_frag(buf, 2 * (q + 1), (q + 1) & 1);
