@@ -31,6 +31,7 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
 HOST_SOURCES = ["api.cpp", "session.cpp", "runtime.cpp", "gemm.cpp", "policy.cpp"]
+HIP_SOURCES = ["sgemm_mfma.hip", "sgemm_wide.hip"]
 COMMON_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-fvisibility=hidden", "-DXVRAM_BUILDING_LIBRARY",
                 f"-I{INCLUDE}", f"-I{CSRC}", "-Wall", "-Wextra", "-Wno-unused-parameter"]
 # Packed-FP32 instructions are disabled for every HIP compile.
@@ -88,9 +89,9 @@ def build(hostsim: bool = True, product: bool = True, verbose: bool = True) -> N
                 jobs.append(pool.submit(_compile_host, src,
                                         os.path.join(OBJ, "hip_" + src.replace(".cpp", ".o")),
                                         hip_flags))
-            jobs.append(pool.submit(_run, [HIPCC, *HIP_FLAGS, "-c",
-                                           os.path.join(CSRC, "sgemm_mfma.hip"), "-o",
-                                           os.path.join(OBJ, "sgemm_mfma.o")]))
+            for src in HIP_SOURCES:
+                jobs.append(pool.submit(_run, [HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src),
+                                               "-o", os.path.join(OBJ, src.replace(".hip", ".o"))]))
         if hostsim:
             for src in HOST_SOURCES + ["device_hostsim.cpp"]:
                 jobs.append(pool.submit(_compile_host, src,
@@ -100,7 +101,8 @@ def build(hostsim: bool = True, product: bool = True, verbose: bool = True) -> N
             j.result()
     if product:
         objs = [os.path.join(OBJ, "hip_" + s.replace(".cpp", ".o"))
-                for s in HOST_SOURCES + ["device_hip.cpp"]] + [os.path.join(OBJ, "sgemm_mfma.o")]
+                for s in HOST_SOURCES + ["device_hip.cpp"]] + [
+                    os.path.join(OBJ, s.replace(".hip", ".o")) for s in HIP_SOURCES]
         out = os.path.join(LIB, "libxvram.so")
         _run([HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", out + ".tmp", *objs,
               f"-Wl,--version-script={os.path.join(CSRC, 'exports.map')}", "-Wl,--no-undefined",

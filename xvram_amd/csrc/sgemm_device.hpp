@@ -1,0 +1,132 @@
+// sgemm_device.hpp — device-side pieces shared by the tile kernels
+// (sgemm_mfma.hip: 256 x 128 tiles, two workgroups per CU; sgemm_wide.hip:
+// 256 x 256 tiles, one workgroup per CU). Compiled only by hipcc.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace xvram::kernels::device {
+
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+// One launch, canonical column-major form (see sgemm_launch.hpp).
+struct Params {
+  const float* a;
+  const float* b;
+  float* c;
+  int64_t lda, ldb, ldc;
+  int m, n, k;
+  float alpha, beta;
+  int tiles_m, tiles_n;
+  const float* bias_row; // per-row bias (nullptr = none)
+  const float* bias_col; // per-column bias (nullptr = none)
+  int relu;
+};
+
+__device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+
+// Four consecutive elements of a line starting at `first`; elements at or
+// beyond `limit` (and the whole vector when !line_ok) read as 0.
+__device__ __forceinline__ float4 load4(const float* __restrict__ line, int first, int limit,
+                                        bool line_ok) {
+  if (!line_ok || first >= limit) return zero4();
+  float4 v = *reinterpret_cast<const float4*>(line + first);
+  if (first + 4 > limit) {
+    const int left = limit - first;
+    if (left < 4) v.w = 0.f;
+    if (left < 3) v.z = 0.f;
+    if (left < 2) v.y = 0.f;
+  }
+  return v;
+}
+
+// Linear workgroup id -> (tile_m, tile_n): undo the round-robin XCD dispatch
+// so XCD x owns ids [x*per, (x+1)*per), then walk tiles in kGroupM-row groups
+// (column-major inside a group).
+template <int kGroupM>
+__device__ __forceinline__ void tile_coords(const Params& p, int& tm, int& tn) {
+  const int total = p.tiles_m * p.tiles_n;
+  int id = blockIdx.x;
+  constexpr int kXcds = 8;
+  if ((total % kXcds) == 0) {
+    const int per = total / kXcds;
+    id = (id % kXcds) * per + id / kXcds;
+  }
+  const int span = kGroupM * p.tiles_n;
+  const int group = id / span;
+  const int first_m = group * kGroupM;
+  const int rows = min(p.tiles_m - first_m, kGroupM);
+  const int in_group = id - group * span;
+  tm = first_m + in_group % rows;
+  tn = in_group / rows;
+}
+
+// Writes one wave's accumulators: acc[i][j] holds MFMA block (row block i,
+// column block j) of v_mfma_f32_32x32x2f32; element v of this lane sits at
+// MFMA row 8*(v/4) + 4*lhalf + v%4 and MFMA column lrow, i.e. tile row
+// row0 + 4*(that) + i and tile column col0 + kNJ*lrow + j (row blocks and
+// column blocks interleaved so one float4 covers four consecutive rows).
+// C = alpha*acc + beta*C (C not read when beta == 0), then + bias_row[i] +
+// bias_col[j], then ReLU (NaN kept: v < 0 is false). Only in-range elements
+// are touched.
+template <int kNJ>
+__device__ __forceinline__ void store_c_tile(const Params& p, const float16_t (&acc)[4][kNJ],
+                                             int row0, int col0, int lrow, int lhalf) {
+  const bool read_c = p.beta != 0.f;
+  const bool extra = p.bias_row != nullptr || p.bias_col != nullptr || p.relu != 0;
+  const auto finish = [&](float v, int r, float bias_c) {
+    if (p.bias_row != nullptr) v += p.bias_row[r];
+    v += bias_c;
+    return (p.relu != 0 && v < 0.f) ? 0.f : v;
+  };
+#pragma unroll
+  for (int j = 0; j < kNJ; ++j) {
+    const int col = col0 + kNJ * lrow + j;
+    if (col >= p.n) continue;
+    float* cline = p.c + (int64_t)col * p.ldc;
+    const float bias_c = p.bias_col != nullptr ? p.bias_col[col] : 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int mrow = 8 * (v >> 2) + 4 * lhalf + (v & 3);
+      const int row = row0 + 4 * mrow;
+      if (row >= p.m) continue;
+      const float out[4] = {acc[0][j][v], acc[1][j][v], acc[2][j][v], acc[3][j][v]};
+      if (row + 4 <= p.m) {
+        float4* dst = reinterpret_cast<float4*>(cline + row);
+        float4 r;
+        if (read_c) {
+          const float4 old = *dst;
+          r.x = p.alpha * out[0] + p.beta * old.x;
+          r.y = p.alpha * out[1] + p.beta * old.y;
+          r.z = p.alpha * out[2] + p.beta * old.z;
+          r.w = p.alpha * out[3] + p.beta * old.w;
+        } else {
+          r.x = p.alpha * out[0];
+          r.y = p.alpha * out[1];
+          r.z = p.alpha * out[2];
+          r.w = p.alpha * out[3];
+        }
+        if (extra) {
+          r.x = finish(r.x, row, bias_c);
+          r.y = finish(r.y, row + 1, bias_c);
+          r.z = finish(r.z, row + 2, bias_c);
+          r.w = finish(r.w, row + 3, bias_c);
+        }
+        *dst = r;
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if (row + t < p.m) {
+            const float val = p.alpha * out[t];
+            const float sum = read_c ? val + p.beta * cline[row + t] : val;
+            cline[row + t] = extra ? finish(sum, row + t, bias_c) : sum;
+          }
+        }
+      }
+    }
+  }
+}
+
+} // namespace xvram::kernels::device

@@ -34,7 +34,5 @@ struct SgemmLaunch {
 
 // Enqueues the launch on `stream` (a hipStream_t); returns a hipError_t.
 int launch_sgemm(const SgemmLaunch& launch, void* stream);
-int sgemm_tile_m();
-int sgemm_tile_n();
 
 } // namespace xvram::kernels

@@ -48,10 +48,18 @@
 
 #include <cstdint>
 
+#include "sgemm_device.hpp"
 #include "sgemm_launch.hpp"
 
 namespace xvram::kernels {
+
+int wide_tile();
+hipError_t launch_wide(const device::Params& p, bool a_kcontig, bool b_ncontig,
+                       hipStream_t stream);
+
 namespace {
+
+using namespace device;
 
 constexpr int kThreads = 256;
 constexpr int kTileM = 256;
@@ -65,38 +73,6 @@ constexpr int kPitchN = kTileN + 4;
 constexpr int kGroupM = 8;
 constexpr int kALoads = kTileM * kStageK / 4 / kThreads; // float4 per thread per stage
 constexpr int kBLoads = kTileN * kStageK / 4 / kThreads;
-
-typedef float float16_t __attribute__((ext_vector_type(16)));
-
-struct Params {
-  const float* a;
-  const float* b;
-  float* c;
-  int64_t lda, ldb, ldc;
-  int m, n, k;
-  float alpha, beta;
-  int tiles_m, tiles_n;
-  const float* bias_row; // per-row bias (nullptr = none)
-  const float* bias_col; // per-column bias (nullptr = none)
-  int relu;
-};
-
-__device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
-
-// Four consecutive elements of a line starting at `first`; elements at or
-// beyond `limit` (and the whole vector when !line_ok) read as 0.
-__device__ __forceinline__ float4 load4(const float* __restrict__ line, int first, int limit,
-                                        bool line_ok) {
-  if (!line_ok || first >= limit) return zero4();
-  float4 v = *reinterpret_cast<const float4*>(line + first);
-  if (first + 4 > limit) {
-    const int left = limit - first;
-    if (left < 4) v.w = 0.f;
-    if (left < 3) v.z = 0.f;
-    if (left < 2) v.y = 0.f;
-  }
-  return v;
-}
 
 struct Stage {
   float4 a[kALoads];
@@ -187,33 +163,13 @@ __device__ __forceinline__ void store_stage(float* __restrict__ la, float* __res
   }
 }
 
-// Linear workgroup id -> (tile_m, tile_n): undo the round-robin XCD dispatch
-// so XCD x owns ids [x*per, (x+1)*per), then walk tiles in GROUP_M-row groups
-// (column-major inside a group).
-__device__ __forceinline__ void tile_coords(const Params& p, int& tm, int& tn) {
-  const int total = p.tiles_m * p.tiles_n;
-  int id = blockIdx.x;
-  constexpr int kXcds = 8;
-  if ((total % kXcds) == 0) {
-    const int per = total / kXcds;
-    id = (id % kXcds) * per + id / kXcds;
-  }
-  const int span = kGroupM * p.tiles_n;
-  const int group = id / span;
-  const int first_m = group * kGroupM;
-  const int rows = min(p.tiles_m - first_m, kGroupM);
-  const int in_group = id - group * span;
-  tm = first_m + in_group % rows;
-  tn = in_group / rows;
-}
-
 template <bool AK, bool BN>
 __global__ __launch_bounds__(kThreads, 2) void sgemm_mfma_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float lds_a[2][kStageK * kPitchA];
   __shared__ __attribute__((aligned(16))) float lds_b[2][kStageK * kPitchN];
 
   int tile_m, tile_n;
-  tile_coords(p, tile_m, tile_n);
+  tile_coords<kGroupM>(p, tile_m, tile_n);
   const int m0 = tile_m * kTileM;
   const int n0 = tile_n * kTileN;
   const int tid = threadIdx.x;
@@ -306,63 +262,7 @@ __global__ __launch_bounds__(kThreads, 2) void sgemm_mfma_kernel(Params p) {
     mfmas((kSteps - 1) & 1);
   }
 
-  // Epilogue. Accumulator element v of block (i, j) for this lane sits at
-  // MFMA row 8*(v/4) + 4*lhalf + v%4 and MFMA column lrow, i.e. tile row
-  // wm + 4*(that) + i and tile column wn + 2*lrow + j.
-  const bool read_c = p.beta != 0.f;
-  const bool extra = p.bias_row != nullptr || p.bias_col != nullptr || p.relu != 0;
-  // Bias and activation after the beta term; ReLU keeps NaN (v < 0 is false).
-  const auto finish = [&](float v, int r, float bias_c) {
-    if (p.bias_row != nullptr) v += p.bias_row[r];
-    v += bias_c;
-    return (p.relu != 0 && v < 0.f) ? 0.f : v;
-  };
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int col = n0 + wn + 2 * lrow + j;
-    if (col >= p.n) continue;
-    float* cline = p.c + (int64_t)col * p.ldc;
-    const float bias_c = p.bias_col != nullptr ? p.bias_col[col] : 0.f;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int mrow = 8 * (v >> 2) + 4 * lhalf + (v & 3);
-      const int row = m0 + wm + 4 * mrow;
-      if (row >= p.m) continue;
-      const float out[4] = {acc[0][j][v], acc[1][j][v], acc[2][j][v], acc[3][j][v]};
-      if (row + 4 <= p.m) {
-        float4* dst = reinterpret_cast<float4*>(cline + row);
-        float4 r;
-        if (read_c) {
-          const float4 old = *dst;
-          r.x = p.alpha * out[0] + p.beta * old.x;
-          r.y = p.alpha * out[1] + p.beta * old.y;
-          r.z = p.alpha * out[2] + p.beta * old.z;
-          r.w = p.alpha * out[3] + p.beta * old.w;
-        } else {
-          r.x = p.alpha * out[0];
-          r.y = p.alpha * out[1];
-          r.z = p.alpha * out[2];
-          r.w = p.alpha * out[3];
-        }
-        if (extra) {
-          r.x = finish(r.x, row, bias_c);
-          r.y = finish(r.y, row + 1, bias_c);
-          r.z = finish(r.z, row + 2, bias_c);
-          r.w = finish(r.w, row + 3, bias_c);
-        }
-        *dst = r;
-      } else {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          if (row + t < p.m) {
-            const float val = p.alpha * out[t];
-            const float sum = read_c ? val + p.beta * cline[row + t] : val;
-            cline[row + t] = extra ? finish(sum, row + t, bias_c) : sum;
-          }
-        }
-      }
-    }
-  }
+  store_c_tile<2>(p, acc, m0 + wm, n0 + wn, lrow, lhalf);
 }
 
 template <bool AK, bool BN>
@@ -374,8 +274,20 @@ hipError_t launch_variant(const Params& p, hipStream_t stream) {
 
 } // namespace
 
-int sgemm_tile_m() { return kTileM; }
-int sgemm_tile_n() { return kTileN; }
+// A launch with at least this many 256 x 256 tiles (one per CU of the chip)
+// runs the 256 x 256 kernel; smaller ones keep two 256 x 128 tiles per CU.
+constexpr int64_t kWideMinTiles = 256;
+
+// The 256 x 256 kernel addresses each operand panel with 32-bit buffer
+// offsets, so every panel must span less than 2^31 bytes.
+bool wide_fits(const SgemmLaunch& l) {
+  constexpr int64_t kLimit = int64_t(1) << 31;
+  const int64_t t = wide_tile();
+  const int64_t tiles = ((l.m + t - 1) / t) * ((l.n + t - 1) / t);
+  const int64_t a_bytes = (l.a_kcontig ? (int64_t)l.m : (int64_t)l.k) * l.lda * 4;
+  const int64_t b_bytes = (l.b_ncontig ? (int64_t)l.k : (int64_t)l.n) * l.ldb * 4;
+  return tiles >= kWideMinTiles && a_bytes < kLimit && b_bytes < kLimit;
+}
 
 int launch_sgemm(const SgemmLaunch& launch, void* stream) {
   const bool aligned =
@@ -397,12 +309,17 @@ int launch_sgemm(const SgemmLaunch& launch, void* stream) {
   p.k = launch.k;
   p.alpha = launch.alpha;
   p.beta = launch.beta;
-  p.tiles_m = (launch.m + kTileM - 1) / kTileM;
-  p.tiles_n = (launch.n + kTileN - 1) / kTileN;
   p.bias_row = launch.bias_row;
   p.bias_col = launch.bias_col;
   p.relu = launch.relu ? 1 : 0;
   auto* s = static_cast<hipStream_t>(stream);
+  if (wide_fits(launch)) {
+    p.tiles_m = (launch.m + wide_tile() - 1) / wide_tile();
+    p.tiles_n = (launch.n + wide_tile() - 1) / wide_tile();
+    return static_cast<int>(launch_wide(p, launch.a_kcontig, launch.b_ncontig, s));
+  }
+  p.tiles_m = (launch.m + kTileM - 1) / kTileM;
+  p.tiles_n = (launch.n + kTileN - 1) / kTileN;
   hipError_t err;
   if (!launch.a_kcontig && !launch.b_ncontig) err = launch_variant<false, false>(p, s);
   else if (!launch.a_kcontig && launch.b_ncontig) err = launch_variant<false, true>(p, s);

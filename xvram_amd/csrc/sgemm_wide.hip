@@ -1,0 +1,368 @@
+// sgemm_wide.hip — the 256 x 256 tile kernel used for large launches on gfx950.
+//
+// Same contract as the 256 x 128 kernel in sgemm_mfma.hip (which dispatches
+// here): C = alpha * op(A) * op(B) + beta * C with FP32 matrix instructions
+// (v_mfma_f32_32x32x2_f32), the optional bias / ReLU epilogue, exact zeros for
+// out-of-range rows, columns and k in both operands, and only in-range C
+// elements stored. Organised for one workgroup per CU:
+//
+//   * workgroup = 4 waves; wave w owns a 128 x 128 sub-tile = 4 x 4 MFMA blocks
+//     whose 256 accumulator registers live in AGPRs. Row blocks and column
+//     blocks are interleaved (MFMA row r of row block i is wave row 4r+i, MFMA
+//     column c of column block j is wave column 4c+j), so one ds_read_b128
+//     feeds four blocks of each operand;
+//   * K advances in stages of 16 through three LDS buffers: stage s+2 is loaded
+//     while stage s is multiplied. An operand whose tile extent is contiguous
+//     in memory (m for op-N A, n for op-T B) is loaded straight into LDS
+//     (buffer_load_dwordx4 ... lds: one 256-float k-row per wave instruction,
+//     rows unpadded); a k-contiguous operand goes through registers and
+//     transposing LDS stores into rows padded by 4 floats (distinct banks);
+//   * every load of the steady state uses a buffer descriptor over the tile's
+//     operand panel: the per-lane offsets are fixed and the stage advance is a
+//     scalar offset, so the loop issues no 64-bit vector address arithmetic
+//     (which measurably delays MFMA issue on this chip). The descriptor's
+//     record count also makes any read past the panel return zeros;
+//   * the stage's eight loads are spread over the first MFMAs of the stage
+//     rather than issued as a burst; the single barrier per stage sits before
+//     the second half of the last k-pair, whose MFMAs cover the next stage's
+//     first fragment reads;
+//   * edge tiles and the last stages run a register-staged loop with
+//     predicated loads; workgroup ids are remapped per XCD as in the 256 x 128
+//     kernel.
+//
+// The host uses this kernel only when every operand panel spans less than
+// 2^31 bytes from a tile's base (32-bit buffer offsets) and the launch has at
+// least one tile per CU.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <type_traits>
+#include <utility>
+
+#include "sgemm_device.hpp"
+
+namespace xvram::kernels {
+namespace {
+
+using namespace device;
+
+constexpr int kThreads = 256;
+constexpr int kTile = 256;     // rows and columns of C per workgroup
+constexpr int kStageK = 16;
+constexpr int kWave = 128;     // rows and columns of C per wave
+constexpr int kGroupM = 8;
+constexpr int kLoads = kTile * kStageK / 4 / kThreads; // float4 per thread per operand per stage
+constexpr int kLoadStep = 3;   // MFMAs between consecutive loads at the start of a stage
+constexpr int kPairs = kStageK / 4;
+static_assert(kLoads == 4 && kLoadStep * 2 * kLoads <= 32, "loads fit in the first k-pair");
+
+// LDS row pitch in floats: unpadded for rows written whole (direct loads and
+// float4 stores of extent-contiguous operands), padded for transposing stores.
+template <bool KC> constexpr int kPitch = KC ? kTile + 4 : kTile;
+
+template <int N> using Int = std::integral_constant<int, N>;
+
+struct Half {
+  float4 v[kLoads];
+};
+
+// Thread -> element map of one operand's stage (f = tid + r*256):
+//   extent-contiguous (KC = false): k-row f/64, elements (f%64)*4..+3
+//   k-contiguous      (KC = true) : element f/4, k (f%4)*4..+3
+template <bool KC>
+__device__ __forceinline__ void load_edge(const float* base, int64_t ld, int e0, int extent, int k0,
+                                          int k, int tid, Half& h) {
+#pragma unroll
+  for (int r = 0; r < kLoads; ++r) {
+    const int f = tid + r * kThreads;
+    if constexpr (!KC) {
+      const int kk = f / (kTile / 4), ee = (f % (kTile / 4)) * 4, kg = k0 + kk;
+      h.v[r] = load4(base + (int64_t)kg * ld + e0, ee, extent - e0, kg < k);
+    } else {
+      const int ee = f / (kStageK / 4), kk = (f % (kStageK / 4)) * 4, eg = e0 + ee;
+      h.v[r] = load4(base + (int64_t)eg * ld + k0, kk, k - k0, eg < extent);
+    }
+  }
+}
+
+// Interior stage; `p` points at this thread's first element of the stage.
+template <bool KC>
+__device__ __forceinline__ void load_full(const float* __restrict__ p, int64_t ld, Half& h) {
+#pragma unroll
+  for (int r = 0; r < kLoads; ++r) {
+    const int64_t off = KC ? (int64_t)(r * (kThreads / (kStageK / 4))) * ld
+                           : (int64_t)(r * (kThreads / (kTile / 4))) * ld;
+    h.v[r] = *reinterpret_cast<const float4*>(p + off);
+  }
+}
+
+template <bool KC>
+__device__ __forceinline__ void store_half(float* __restrict__ l, int tid, const Half& h) {
+  constexpr int P = kPitch<KC>;
+#pragma unroll
+  for (int r = 0; r < kLoads; ++r) {
+    const int f = tid + r * kThreads;
+    if constexpr (!KC) {
+      const int kk = f / (kTile / 4), ee = (f % (kTile / 4)) * 4;
+      *reinterpret_cast<float4*>(l + kk * P + ee) = h.v[r];
+    } else {
+      const int ee = f / (kStageK / 4), kk = (f % (kStageK / 4)) * 4;
+      l[(kk + 0) * P + ee] = h.v[r].x;
+      l[(kk + 1) * P + ee] = h.v[r].y;
+      l[(kk + 2) * P + ee] = h.v[r].z;
+      l[(kk + 3) * P + ee] = h.v[r].w;
+    }
+  }
+}
+
+// Raw buffer descriptor (no stride, 32-bit data format word) over `bytes`
+// bytes from `base`; reads at or past `bytes` return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t panel_rsrc(const float* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+// One wave-wide direct load: lane l's 16 bytes at rsrc.base + soff + voff land
+// at LDS byte address lds_base + kOff + 16*l (lds_base wave-uniform). Counted
+// by vmcnt only: the caller waits before the barrier that publishes the data.
+template <int kOff>
+__device__ __forceinline__ void load_lds16(uint32_t lds_base, uint32_t voff,
+                                           __amdgpu_buffer_rsrc_t rsrc, uint32_t soff) {
+  asm volatile("s_add_u32 m0, %0, %4\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff), "i"(kOff)
+               : "memory", "m0", "scc");
+}
+
+__device__ __forceinline__ float4 load_reg16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff,
+                                             uint32_t soff) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, soff, 0));
+}
+
+__device__ __forceinline__ uint32_t lds_byte_addr(const float* p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
+}
+
+template <bool AK, bool BN>
+__global__ __launch_bounds__(kThreads, 1) void sgemm_wide_kernel(Params p) {
+  constexpr bool kDirectA = !AK; // m-contiguous A: straight into LDS
+  constexpr bool kDirectB = BN;  // n-contiguous B: straight into LDS
+  constexpr int kPA = kPitch<AK>;
+  constexpr int kPB = kPitch<!BN>;
+  constexpr int kBufA = kStageK * kPA;
+  constexpr int kBuf = kBufA + kStageK * kPB;
+  constexpr int kDirect = (kDirectA ? kLoads : 0) + (kDirectB ? kLoads : 0);
+  __shared__ __attribute__((aligned(16))) float lds[3 * kBuf];
+
+  // The MFMAs take their accumulators in AGPRs (256 per lane), leaving the
+  // architectural VGPRs to fragments, staging and addresses.
+  asm volatile("; accumulators in AGPRs" ::: "a0");
+
+  int tile_m, tile_n;
+  tile_coords<kGroupM>(p, tile_m, tile_n);
+  const int m0 = tile_m * kTile;
+  const int n0 = tile_n * kTile;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = (wave & 1) * kWave;
+  const int wn = (wave >> 1) * kWave;
+  const int lrow = lane & 31;  // MFMA row (A) / column (B) of this lane
+  const int lhalf = lane >> 5; // which of the MFMA's two k values
+
+  float16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int stages = (p.k + kStageK - 1) / kStageK;
+  const int full_stages = p.k / kStageK;
+  const bool interior = m0 + kTile <= p.m && n0 + kTile <= p.n;
+  const float* pa = AK ? p.a + (int64_t)(m0 + tid / (kStageK / 4)) * p.lda + (tid % (kStageK / 4)) * 4
+                       : p.a + (int64_t)(tid / (kTile / 4)) * p.lda + m0 + (tid % (kTile / 4)) * 4;
+  const float* pb = BN ? p.b + (int64_t)(tid / (kTile / 4)) * p.ldb + n0 + (tid % (kTile / 4)) * 4
+                       : p.b + (int64_t)(n0 + tid / (kStageK / 4)) * p.ldb + (tid % (kStageK / 4)) * 4;
+  const int64_t a_step = AK ? kStageK : (int64_t)kStageK * p.lda;
+  const int64_t b_step = BN ? (int64_t)kStageK * p.ldb : kStageK;
+
+  auto lds_a = [&](int buf) { return lds + buf * kBuf; };
+  auto lds_b = [&](int buf) { return lds + buf * kBuf + kBufA; };
+
+  Half ha, hb;
+  auto load_any = [&](int stg) {
+    load_edge<AK>(p.a, p.lda, m0, p.m, stg * kStageK, p.k, tid, ha);
+    load_edge<!BN>(p.b, p.ldb, n0, p.n, stg * kStageK, p.k, tid, hb);
+  };
+  auto store_any = [&](int buf) {
+    store_half<AK>(lds_a(buf), tid, ha);
+    store_half<!BN>(lds_b(buf), tid, hb);
+  };
+
+  load_any(0);
+  store_any(0);
+  if (stages > 1) {
+    load_any(1);
+    store_any(1);
+  }
+  __syncthreads();
+
+  float4 fa[2][2], fb[2][2];
+  // Fragments of the k-pair (kk, kk+2) into `slot`.
+  auto read_pair = [&](const float* la, const float* lb, int kk, int slot) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int krow = kk + 2 * t + lhalf;
+      fa[slot][t] = *reinterpret_cast<const float4*>(la + wm + 4 * lrow + krow * kPA);
+      fb[slot][t] = *reinterpret_cast<const float4*>(lb + wn + 4 * lrow + krow * kPB);
+    }
+  };
+  // MFMAs number from..to-1 of a k-pair: x = 16*t + 4*i + j.
+  auto mfma_range = [&](int slot, int from, int to) {
+#pragma unroll
+    for (int x = 0; x < 32; ++x) {
+      if (x < from || x >= to) continue;
+      const int t = x / 16, i = (x % 16) / 4, j = x % 4;
+      const float4 a = fa[slot][t], b = fb[slot][t];
+      const float ao = i == 0 ? a.x : i == 1 ? a.y : i == 2 ? a.z : a.w;
+      const float bo = j == 0 ? b.x : j == 1 ? b.y : j == 2 ? b.z : b.w;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(ao, bo, acc[i][j], 0, 0, 0);
+    }
+  };
+  read_pair(lds_a(0), lds_b(0), 0, 0);
+  int st = 0;
+
+  if (interior) {
+    // Buffer descriptors over this tile's panels. A(i, k) sits at byte
+    // 4*((i-m0)*lda + k) (op T) or 4*(k*lda + i-m0) (op N) from a + m0*lda or
+    // a + m0; B likewise from b + n0 (op T) or b + n0*ldb (op N).
+    const float* a_base = AK ? p.a + (int64_t)m0 * p.lda : p.a + m0;
+    const float* b_base = BN ? p.b + n0 : p.b + (int64_t)n0 * p.ldb;
+    const int64_t a_bytes = AK ? (int64_t)(p.m - m0) * p.lda * 4 : ((int64_t)p.k * p.lda - m0) * 4;
+    const int64_t b_bytes = BN ? ((int64_t)p.k * p.ldb - n0) * 4 : (int64_t)(p.n - n0) * p.ldb * 4;
+    const __amdgpu_buffer_rsrc_t rs_a = panel_rsrc(a_base, (uint32_t)a_bytes);
+    const __amdgpu_buffer_rsrc_t rs_b = panel_rsrc(b_base, (uint32_t)b_bytes);
+    // Per-lane byte offsets of load r in stage 0, and the byte advance per stage.
+    uint32_t vo_a[kLoads], vo_b[kLoads];
+#pragma unroll
+    for (int r = 0; r < kLoads; ++r) {
+      vo_a[r] = kDirectA ? (uint32_t)(((int64_t)(wave + 4 * r) * p.lda + lane * 4) * 4)
+                         : (uint32_t)(((int64_t)(tid / 4 + 64 * r) * p.lda + (tid % 4) * 4) * 4);
+      vo_b[r] = kDirectB ? (uint32_t)(((int64_t)(wave + 4 * r) * p.ldb + lane * 4) * 4)
+                         : (uint32_t)(((int64_t)(tid / 4 + 64 * r) * p.ldb + (tid % 4) * 4) * 4);
+    }
+    const uint32_t a_stage_bytes = (uint32_t)(kDirectA ? kStageK * p.lda * 4 : kStageK * 4);
+    const uint32_t b_stage_bytes = (uint32_t)(kDirectB ? kStageK * p.ldb * 4 : kStageK * 4);
+    // LDS byte address of this wave's first direct-load row in buffer 0.
+    const uint32_t lds_a_wave = lds_byte_addr(lds + wave * kPA);
+    const uint32_t lds_b_wave = lds_byte_addr(lds + kBufA + wave * kPB);
+
+    // Load r (A for r < kLoads, else B) of stage `stg` into buffer `far`.
+    auto issue = [&]<int far, int r>(int stg, Int<far>, Int<r>) {
+      if constexpr (r < kLoads) {
+        const uint32_t so = __builtin_amdgcn_readfirstlane(a_stage_bytes * (uint32_t)stg);
+        if constexpr (kDirectA)
+          load_lds16<(far * kBuf + r * 4 * kPA) * 4>(lds_a_wave, vo_a[r], rs_a, so);
+        else
+          ha.v[r] = load_reg16(rs_a, vo_a[r], so);
+      } else {
+        const uint32_t so = __builtin_amdgcn_readfirstlane(b_stage_bytes * (uint32_t)stg);
+        if constexpr (kDirectB)
+          load_lds16<(far * kBuf + (r - kLoads) * 4 * kPB) * 4>(lds_b_wave, vo_b[r - kLoads],
+                                                                          rs_b, so);
+        else
+          hb.v[r - kLoads] = load_reg16(rs_b, vo_b[r - kLoads], so);
+      }
+    };
+    // One stage: multiply stage stg from buffer cur while stage stg+2 loads
+    // into buffer far; end with stage stg+1's first fragments read from nxt.
+    auto body = [&]<int cur, int nxt, int far>(int stg, Int<cur>, Int<nxt>, Int<far> far_t) {
+      auto one_mfma = [&]<int Q, int X>(Int<Q>, Int<X>) {
+        constexpr int g = Q * 32 + X;
+        if constexpr (g % kLoadStep == 0 && g / kLoadStep < 2 * kLoads) {
+          __builtin_amdgcn_sched_barrier(0);
+          issue(stg + 2, far_t, Int<g / kLoadStep>{});
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        mfma_range(Q & 1, X, X + 1);
+      };
+      auto pair = [&]<int Q>(Int<Q> q) {
+        read_pair(lds_a(cur), lds_b(cur), 4 * (Q + 1), (Q + 1) & 1);
+        __builtin_amdgcn_sched_barrier(0);
+        [&]<int... X>(std::integer_sequence<int, X...>) {
+          (one_mfma(q, Int<X>{}), ...);
+        }(std::make_integer_sequence<int, 32>{});
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      [&]<int... Q>(std::integer_sequence<int, Q...>) {
+        (pair(Int<Q>{}), ...);
+      }(std::make_integer_sequence<int, kPairs - 1>{});
+      if constexpr (!kDirectA) store_half<true>(lds_a(far), tid, ha);
+      if constexpr (!kDirectB) store_half<true>(lds_b(far), tid, hb);
+      mfma_range((kPairs - 1) & 1, 0, 16);
+      __builtin_amdgcn_sched_barrier(0);
+      // Stage stg+1's direct loads were issued a stage earlier than this
+      // stage's kDirect ones; loads complete in order.
+      if constexpr (kDirect == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      else if constexpr (kDirect == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      __syncthreads();
+      read_pair(lds_a(nxt), lds_b(nxt), 0, 0);
+      mfma_range((kPairs - 1) & 1, 16, 32);
+    };
+    // Stages 0 and 1 are in LDS; each body needs stages stg..stg+2 full.
+    for (; st + 4 < full_stages; st += 3) {
+      body(st, Int<0>{}, Int<1>{}, Int<2>{});
+      body(st + 1, Int<1>{}, Int<2>{}, Int<0>{});
+      body(st + 2, Int<2>{}, Int<0>{}, Int<1>{});
+    }
+  }
+
+  // Remaining stages (every stage of an edge tile): stage st+2 is staged
+  // through registers while st runs; stage st+1 is in LDS or in flight.
+  for (; st < stages; ++st) {
+    const int cur = st % 3, nxt = (st + 1) % 3, far = (st + 2) % 3;
+    const bool more2 = st + 2 < stages;
+    if (more2) {
+      if (interior && st + 2 < full_stages) {
+        load_full<AK>(pa + (st + 2) * a_step, p.lda, ha);
+        load_full<!BN>(pb + (st + 2) * b_step, p.ldb, hb);
+      } else {
+        load_any(st + 2);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kPairs - 1; ++q) {
+      read_pair(lds_a(cur), lds_b(cur), 4 * (q + 1), (q + 1) & 1);
+      mfma_range(q & 1, 0, 32);
+    }
+    if (more2) store_any(far);
+    if constexpr (kDirect > 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (st + 1 < stages) read_pair(lds_a(nxt), lds_b(nxt), 0, 0);
+    mfma_range((kPairs - 1) & 1, 0, 32);
+  }
+
+  store_c_tile<4>(p, acc, m0 + wm, n0 + wn, lrow, lhalf);
+}
+
+} // namespace
+
+int wide_tile() { return kTile; }
+
+// Launches the 256 x 256 kernel for `p` (tiles_m / tiles_n already in 256s).
+hipError_t launch_wide(const Params& p, bool a_kcontig, bool b_ncontig, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
+  if (!a_kcontig && !b_ncontig)
+    hipLaunchKernelGGL((sgemm_wide_kernel<false, false>), grid, dim3(kThreads), 0, stream, p);
+  else if (!a_kcontig && b_ncontig)
+    hipLaunchKernelGGL((sgemm_wide_kernel<false, true>), grid, dim3(kThreads), 0, stream, p);
+  else if (a_kcontig && !b_ncontig)
+    hipLaunchKernelGGL((sgemm_wide_kernel<true, false>), grid, dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((sgemm_wide_kernel<true, true>), grid, dim3(kThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+} // namespace xvram::kernels
