@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import glob
 import json
 import os
 import sys
@@ -520,10 +521,11 @@ def main() -> int:
                "sample": f"C[0:{sr}, 0:{cols}] of the same {m}x{n}x{k} product with full K "
                          f"(FP64 accumulation over FP32 inputs, {cpu_s:.1f} s on {threads} threads)"}
 
-    # HBM traffic per launch from the committed rocprofv3 --pmc summary, if any.
+    # HBM traffic per launch from the committed rocprofv3 --pmc summary of this
+    # workload's tile kernel (profiles/traffic_<kernel>_<workload>.txt), if any.
     traffic = None
-    traffic_file = os.path.join(ROOT, "profiles", f"traffic_sgemm_mfma_{args.workload}.txt")
-    if os.path.exists(traffic_file):
+    for traffic_file in sorted(glob.glob(os.path.join(ROOT, "profiles",
+                                                      f"traffic_*_{args.workload}.txt"))):
         for line in open(traffic_file):
             if line.startswith("traffic_bytes_per_launch:"):
                 traffic = int(float(line.split(":", 1)[1]))
