@@ -402,6 +402,7 @@ void Runtime::check_generation(const Frame& f) {
 Error Runtime::record_retire(Frame& f, Stream stream) {
   if (int rc = device_->event_record(f.retire, stream)) return device_failure(rc, "cache", "record");
   f.retire_pending = true;
+  f.retire_seq = ++retire_records_;
   ++f.generation;
   return {};
 }
@@ -470,8 +471,13 @@ bool Runtime::allocation_streaming(uint64_t allocation_id) {
 // (the one idle longest), else a not-yet-created frame, else the victim the
 // session's policy names among unpinned resident entries (a dirty victim is
 // written back first). Only frames inside the live capacity are considered.
-// The choice depends only on the schedule, never on how far the device has
-// progressed, so the accounting of a run is reproducible.
+// A free frame whose last consumer is still pending (typically a C tile whose
+// write-back was just queued) would make the host wait for that consumer while
+// launches it could already enqueue sit idle; a clean entry whose last
+// consumer was recorded earlier in the schedule is evicted instead when the
+// policy names one. The choice depends only on the schedule (the order of
+// retire records), never on how far the device has progressed, so the
+// accounting of a run is reproducible.
 Error Runtime::select_frame(Frame*& out) {
   Frame* free_frame = nullptr;
   Frame* uncreated = nullptr;
@@ -495,6 +501,22 @@ Error Runtime::select_frame(Frame*& out) {
     candidates.push_back(c);
   }
   Frame* chosen = free_frame ? free_frame : uncreated;
+  if (free_frame && free_frame->retire_pending) {
+    std::vector<VictimCandidate> older;
+    for (const VictimCandidate& c : candidates) {
+      const Frame& f = frames_[c.id];
+      if (!f.dirty && (!f.retire_pending || f.retire_seq < free_frame->retire_seq))
+        older.push_back(c);
+    }
+    if (!older.empty()) {
+      if (const std::optional<uint64_t> victim = policy_->select_victim(older)) {
+        Frame& v = frames_[*victim];
+        if (Error e = evict_key(v, false)) return e;
+        ++t_.clean_evictions;
+        chosen = &v;
+      }
+    }
+  }
   if (!chosen) {
     const std::optional<uint64_t> victim = policy_->select_victim(candidates);
     if (!victim)

@@ -110,6 +110,7 @@ struct Frame {
   bool ready_pending = false;
   Event retire = nullptr; // recorded after the last consumer (kernel or write-back)
   bool retire_pending = false;
+  uint64_t retire_seq = 0; // schedule order of the last retire record
   bool used_before = false;
   EntryState state = EntryState::host_clean;
   // Event generations (reference core.cpp begin/complete_event_generation):
@@ -308,6 +309,7 @@ private:
   std::vector<Frame> frames_;
   std::map<PanelKey, uint64_t> index_; // key -> frame index
   uint64_t tick_ = 0;
+  uint64_t retire_records_ = 0; // retire events recorded so far (schedule order)
 
   uint64_t workspace_va_ = 0;
   uint64_t workspace_bytes_ = 0;
