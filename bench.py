@@ -305,6 +305,9 @@ def run_chain(args, xv, lib, synth, link) -> int:
         log(f"step {i}: {times[-1]:.3f}s = {flops / times[-1] / 1e12:.1f} TFLOP/s")
     tele1 = session.telemetry()
     ops = [json.loads(line) for line in open(trace_path).readlines()[before:]]
+    if args.trace_out:
+        with open(args.trace_out, "w") as out:
+            out.writelines(json.dumps(op) + "\n" for op in ops)
     stats = analyse(ops)
     step_s = sum(times) / len(times)
 

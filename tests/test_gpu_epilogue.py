@@ -77,13 +77,15 @@ def test_epilogue_ragged_out_of_core(lib, oracle_mod, c_layout, axis):
     assert bad == 0
 
 
-def test_inference_chain_streams_weights(lib, oracle_mod):
-    """Config 5 at reduced width: 8 x [Y = ReLU(X W^T + b)], X 256 x 4096,
-    W 4096 x 4096 ~ N(0, 1/4096), b ~ N(0, 1/4096), X ~ N(0, 1); 64 MiB of
-    weights per layer through a 192 MiB budget of 16 MiB frames."""
-    layers, batch, width = 8, 256, 4096
+def run_chain(lib, oracle_mod, prefetch_distance=2, layers=8, batch=256, width=4096):
+    """Config 5 at reduced width: layers x [Y = ReLU(X W^T + b)], X batch x width,
+    W width x width ~ N(0, 1/width), b ~ N(0, 1/width), X ~ N(0, 1); 64 MiB of
+    weights per layer through a 192 MiB budget of 16 MiB frames. The layers are
+    queued back to back, so each one's tail can carry the next one's first
+    weight fills (prefetch_distance 0 turns that off)."""
     std = 1.0 / np.sqrt(width)
-    s = xv.Session(lib, chunk_size_bytes=16 * MiB, cache_target_bytes=12 * 16 * MiB)
+    s = xv.Session(lib, chunk_size_bytes=16 * MiB, cache_target_bytes=12 * 16 * MiB,
+                   prefetch_distance=prefetch_distance)
     try:
         acts = [s.allocation(batch * width * 4) for _ in range(layers + 1)]
         x0 = oracle_mod.fill_normal(batch * width, 700, 1.0).reshape(batch, width)
@@ -114,6 +116,12 @@ def test_inference_chain_streams_weights(lib, oracle_mod):
             p.release()
     finally:
         balanced_close(s)
+    return x0, ys, weights, biases, t0, t1
+
+
+def test_inference_chain_streams_weights(lib, oracle_mod):
+    layers, width = 8, 4096
+    x0, ys, weights, biases, t0, t1 = run_chain(lib, oracle_mod, layers=layers, width=width)
     # All weights streamed (8 x 64 MiB), activations in and out once per layer.
     assert t1.bytes_h2d - t0.bytes_h2d >= layers * width * width * 4
     # Per layer, from the FP32 input the GPU actually used.
@@ -132,3 +140,18 @@ def test_inference_chain_streams_weights(lib, oracle_mod):
     rel = np.abs(ys[-1] - y).max() / np.abs(y).max()
     print(f"chain: max |Y - Y_fp64| / max |Y_fp64| = {rel:.3e}", flush=True)
     assert rel < 1e-4
+
+
+def test_chain_carried_fills_match(lib, oracle_mod):
+    """Fills carried across queued operations (the default) change where and
+    when weight panels are loaded, never what a kernel reads: every layer's
+    output is bit-identical to the run without carrying, and no extra bytes
+    cross the link."""
+    _, carried, _, _, c0, c1 = run_chain(lib, oracle_mod, prefetch_distance=2)
+    _, plain, _, _, p0, p1 = run_chain(lib, oracle_mod, prefetch_distance=0)
+    for l, (a, b) in enumerate(zip(carried, plain)):
+        assert np.array_equal(a, b), l
+    assert c1.bytes_h2d - c0.bytes_h2d == p1.bytes_h2d - p0.bytes_h2d
+    assert c1.cache_misses - c0.cache_misses == p1.cache_misses - p0.cache_misses
+    print(f"carried hits {c1.cache_hits - c0.cache_hits} vs {p1.cache_hits - p0.cache_hits}",
+          flush=True)

@@ -641,6 +641,7 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     }
   }
   if (bias && !result) result = rt.release_after(*bias, rt.compute_stream(), false);
+  if (!result && hooks.tail) result = hooks.tail();
   if (result) {
     // Unpin what was acquired ahead, drop partial C panels, drain the device.
     rt.discard_dirty();
@@ -648,6 +649,39 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     return result;
   }
   return rt.finish_operation(operation_id);
+}
+
+Error carry_gemm_head(Runtime& rt, const GemmPlanData& plan, uint64_t launches) {
+  const CanonProblem& p = plan.problem;
+  const auto carry = [&](const PanelKey& key, uint64_t pitch, bool& stop) -> Error {
+    bool issued = false;
+    Error e = rt.carry_fill(key, pitch, issued);
+    if (e && e.status == XVRAM_STATUS_BUDGET_PRESSURE) {
+      stop = true; // every frame is pinned: nothing more can be carried
+      return {};
+    }
+    return e;
+  };
+  bool stop = false;
+  if (p.bias_allocation_id != 0) {
+    PanelKey key;
+    key.allocation_id = p.bias_allocation_id;
+    key.offset = p.bias_base;
+    key.width = p.bias_length() * 4;
+    key.height = 1;
+    key.pitch = key.width;
+    if (Error e = carry(key, round_up(key.width, 16), stop)) return e;
+  }
+  const uint64_t n = std::min<uint64_t>(launches, plan.launches.size());
+  for (uint64_t idx = 0; idx < n && !stop; ++idx) {
+    const LaunchGeom g = launch_geom(plan, plan.launches[idx]);
+    const PanelGeom ag = a_geom(p.a, g.i0, g.h, g.p0, g.w);
+    const PanelGeom bg = b_geom(p.b, g.p0, g.w, g.j0, g.g);
+    if (Error e = carry(panel_key(p.a, ag), packed_ld(ag) * 4, stop)) return e;
+    if (stop) break;
+    if (Error e = carry(panel_key(p.b, bg), packed_ld(bg) * 4, stop)) return e;
+  }
+  return {};
 }
 
 } // namespace xvram

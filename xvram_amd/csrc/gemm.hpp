@@ -145,9 +145,18 @@ struct GemmHooks {
   // execution there.
   std::function<Error(const char* boundary)> boundary;
   std::function<void(uint64_t completed, uint64_t total)> progress;
+  // Called once after the last launch is enqueued, while it still runs: the
+  // place to start fills for the operation queued next (carry_gemm_head).
+  std::function<Error()> tail;
 };
 
 Error execute_gemm(Runtime& runtime, const GemmPlanData& plan, uint64_t operation_id,
                    const GemmHooks& hooks);
+
+// Starts, behind the running operation (Runtime::carry_fill), the fills of
+// the bias and of the A and B panels of the first `launches` launches of
+// `plan`: the panels its executor acquires before its first enqueue. Stops
+// quietly when no frame is free of pins; device errors are returned.
+Error carry_gemm_head(Runtime& runtime, const GemmPlanData& plan, uint64_t launches);
 
 } // namespace xvram

@@ -155,6 +155,7 @@ Error Runtime::setup() {
   if (int rc = device_->stream_create(&h2d_)) return device_failure(rc, "setup", "stream");
   if (int rc = device_->stream_create(&d2h_)) return device_failure(rc, "setup", "stream");
   if (int rc = device_->event_create(&op_start_)) return device_failure(rc, "setup", "event");
+  if (int rc = device_->event_create(&carry_fence_)) return device_failure(rc, "setup", "event");
   t_.flags = XVRAM_TELEMETRY_NO_PHYSICAL_ALIASES | XVRAM_TELEMETRY_STABLE_VIRTUAL_ADDRESSES;
   setup_done_ = true;
   return {};
@@ -215,10 +216,15 @@ Error Runtime::close() {
   arena_ = 0;
   for (Event e : event_pool_) device_->event_destroy(e);
   for (Event e : events_in_use_) device_->event_destroy(e);
+  for (Event e : carried_events_) device_->event_destroy(e);
   event_pool_.clear();
   events_in_use_.clear();
+  carried_events_.clear();
+  carried_trace_.clear();
   pending_writebacks_.clear();
   if (op_start_) device_->event_destroy(op_start_);
+  if (carry_fence_) device_->event_destroy(carry_fence_);
+  op_start_ = carry_fence_ = nullptr;
   for (Stream s : {h2d_, compute_, d2h_})
     if (s) device_->stream_destroy(s);
   compute_ = h2d_ = d2h_ = nullptr;
@@ -627,6 +633,31 @@ Error Runtime::acquire(const PanelKey& key, uint64_t packed_pitch, bool needs_da
   if (Error e = fill_entry(*f, key, packed_pitch, needs_data)) return e;
   out = f;
   return {};
+}
+
+// The carried entry is inserted like any executor fill (not as a speculative
+// prefetch): the next operation pins it before anything else, so the victim
+// policy must not rank it below older entries.
+Error Runtime::carry_fill(const PanelKey& key, uint64_t packed_pitch, bool& issued) {
+  issued = false;
+  if (poisoned_) return make_error(XVRAM_STATUS_POISONED, "cache", "carry", "session is poisoned");
+  if (index_.count(key)) return {};
+  for (const auto& [written, done] : pending_writebacks_)
+    if (keys_overlap(written, key)) return {};
+  for (const Frame& f : frames_)
+    if (f.keyed && f.dirty && keys_overlap(f.key, key)) return {};
+  if (!carry_active_) {
+    if (int rc = device_->event_record(carry_fence_, h2d_)) return device_failure(rc, "cache", "record");
+    carry_active_ = true;
+    carry_trace_mark_ = trace_.size();
+    carry_event_mark_ = events_in_use_.size();
+  }
+  Frame* f = nullptr;
+  if (Error e = acquire(key, packed_pitch, true, f)) return e;
+  f->carry_serial = op_serial_;
+  issued = true;
+  // Retired by its own copy: evicting or unmapping the frame waits for the fill.
+  return release_after(*f, h2d_, false);
 }
 
 // Orders `stream` after the fill; from then on the entry's bytes are resident
@@ -1109,7 +1140,13 @@ Error Runtime::begin_operation() {
                       "the transaction duration guard");
   kernels_in_operation_ = 0;
   transactions_in_operation_ = 0;
-  trace_.clear();
+  ++op_serial_;
+  carry_active_ = false;
+  // Fills the previous operation carried over belong to this one's trace.
+  trace_ = std::move(carried_trace_);
+  carried_trace_.clear();
+  events_in_use_.insert(events_in_use_.end(), carried_events_.begin(), carried_events_.end());
+  carried_events_.clear();
   if (int rc = device_->event_record(op_start_, compute_)) return device_failure(rc, "operation", "record");
   for (Stream s : {h2d_, d2h_})
     if (int rc = device_->stream_wait_event(s, op_start_)) return device_failure(rc, "operation", "wait");
@@ -1127,12 +1164,19 @@ Error Runtime::record_kernel(Event& start, Event& stop) {
 // max_transaction_ms blocks further launches and fails with a timeout).
 Error Runtime::finish_operation(uint64_t operation_id) {
   Error first;
-  for (Stream s : {h2d_, compute_, d2h_}) {
+  for (Stream s : {compute_, d2h_}) {
     if (int rc = device_->stream_sync(s)) {
       if (!first) first = device_failure(rc, "operation", "stream_sync");
     }
   }
+  // This operation's own fills end at the carry fence; carried fills run on.
+  if (int rc = carry_active_ ? device_->event_sync(carry_fence_) : device_->stream_sync(h2d_)) {
+    if (!first) first = device_failure(rc, "operation", "stream_sync");
+  }
+  const bool carrying = carry_active_ && !first;
   for (Frame& f : frames_) {
+    if (carrying && f.carry_serial == op_serial_) continue; // still filling for the next one
+    f.carry_serial = 0;
     f.ready_pending = false;
     if (first) continue;
     // Every stream has drained: all fills landed and every retire event of
@@ -1152,10 +1196,12 @@ Error Runtime::finish_operation(uint64_t operation_id) {
     if (out) std::fprintf(out, "{\"operation_id\": %llu", static_cast<unsigned long long>(operation_id));
     const char* names[4] = {"kernels", "h2d", "d2h", "transactions"};
     const char kinds[4] = {'k', 'h', 'd', 't'};
+    const size_t own = carrying ? carry_trace_mark_ : trace_.size();
     for (int c = 0; c < 4; ++c) {
       if (out) std::fprintf(out, ", \"%s\": [", names[c]);
       bool comma = false;
-      for (const TraceInterval& iv : trace_) {
+      for (size_t i = 0; i < own; ++i) {
+        const TraceInterval& iv = trace_[i];
         if (iv.kind != kinds[c]) continue;
         float s = 0.f, e = 0.f;
         if (device_->event_elapsed_ms(&s, op_start_, iv.start) != 0) s = 0.f;
@@ -1184,10 +1230,25 @@ Error Runtime::finish_operation(uint64_t operation_id) {
     t_.transactions_completed += kernels_in_operation_ + transactions_in_operation_;
     t_.algorithm_selections += kernels_in_operation_;
   }
+  // Carried fills are traced with the next operation; their events stay live.
+  carried_trace_.clear();
+  carried_events_.clear();
+  size_t own_events = events_in_use_.size();
+  if (carrying) {
+    carried_trace_.assign(trace_.begin() + static_cast<std::ptrdiff_t>(carry_trace_mark_),
+                          trace_.end());
+    carried_events_.assign(events_in_use_.begin() + static_cast<std::ptrdiff_t>(carry_event_mark_),
+                           events_in_use_.end());
+    own_events = carry_event_mark_;
+  }
+  carry_active_ = false;
   trace_.clear();
   kernels_in_operation_ = 0;
   transactions_in_operation_ = 0;
-  for (Event e : events_in_use_) event_pool_.push_back(e);
+  for (size_t i = 0; i < events_in_use_.size(); ++i) {
+    // After a failure carried events are returned too: nothing reads them again.
+    if (i < own_events || !carrying) event_pool_.push_back(events_in_use_[i]);
+  }
   events_in_use_.clear();
   uint64_t free_bytes = 0, total_bytes = 0;
   if (!first && device_->mem_info(&free_bytes, &total_bytes) == 0) {

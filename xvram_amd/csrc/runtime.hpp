@@ -118,6 +118,9 @@ struct Frame {
   // host has seen finish. A frame is remapped or refilled only when equal.
   uint64_t generation = 0;
   uint64_t completed = 0;
+  // Serial of the operation that started this frame's fill for the operation
+  // after it (Runtime::carry_fill); 0 when the frame holds no carried fill.
+  uint64_t carry_serial = 0;
 };
 
 // Per-operation intervals for the optional trace file (XVRAM_TRACE_FILE).
@@ -236,8 +239,18 @@ public:
   // fails with BUDGET_PRESSURE when the next working set no longer fits.
   Error refresh_budget(uint64_t required_frames, uint64_t required_workspace, bool force);
   // Waits for every stream; folds kernel/copy intervals into telemetry, applies
-  // the duration guard, writes the optional trace line.
+  // the duration guard, writes the optional trace line. Fills carried to the
+  // next operation (carry_fill) are not waited for: the H2D stream is waited
+  // on only up to the carry fence.
   Error finish_operation(uint64_t operation_id);
+
+  // Cross-operation fill: while the current operation's last launches run,
+  // starts the H2D fill of a panel the next queued operation will read, behind
+  // a fence that marks the end of the current operation's own fills. The entry
+  // is left clean and unpinned, with its ready and retire events pending, for
+  // the next operation to find. Panels already cached, or overlapping a dirty
+  // entry or a write-back still in flight, are skipped (issued = false).
+  Error carry_fill(const PanelKey& key, uint64_t packed_pitch, bool& issued);
 
   // Kernel bookkeeping used by the executor.
   Error record_kernel(Event& start, Event& stop);
@@ -321,6 +334,18 @@ private:
   Event op_start_ = nullptr;
   std::vector<Event> event_pool_;
   std::vector<Event> events_in_use_;
+  uint64_t op_serial_ = 0; // operations begun so far
+
+  // Fills carried past the current operation (carry_fill): the fence on the
+  // H2D stream before the first of them, and where their trace intervals and
+  // events start in trace_ / events_in_use_. At the end of the operation they
+  // move to carried_trace_ / carried_events_ and join the next operation.
+  bool carry_active_ = false;
+  Event carry_fence_ = nullptr;
+  size_t carry_trace_mark_ = 0;
+  size_t carry_event_mark_ = 0;
+  std::vector<TraceInterval> carried_trace_;
+  std::vector<Event> carried_events_;
 
   std::map<uint64_t, HostAllocation> allocations_;
   uint64_t next_allocation_id_ = 1;

@@ -234,7 +234,7 @@ void Session::worker_main() {
 }
 
 Error Session::enqueue(Action action, uint64_t units, uint64_t deadline_ms,
-                       std::shared_ptr<Operation>& out) {
+                       std::shared_ptr<Operation>& out, std::shared_ptr<GemmPlanRecord> gemm) {
   Deadline deadline;
   if (!Deadline::create(deadline_ms, Clock::now(), deadline))
     return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "deadline", "submit",
@@ -243,7 +243,7 @@ Error Session::enqueue(Action action, uint64_t units, uint64_t deadline_ms,
   {
     std::lock_guard<std::mutex> lock(queue_mutex_);
     if (closing_) return make_error(XVRAM_STATUS_CLOSED, "session", "submit", "session is closing");
-    queue_.push_back(WorkItem{op, std::move(action), false});
+    queue_.push_back(WorkItem{op, std::move(action), false, std::move(gemm)});
   }
   queue_cv_.notify_one();
   out = std::move(op);
@@ -369,9 +369,32 @@ Error Session::submit_gemm(const std::shared_ptr<GemmPlanRecord>& plan,
           return op.deadline_error("gemm", "tile_deadline");
         };
         hooks.progress = [&](uint64_t done, uint64_t) { op.advance(done); };
+        // Operations run one at a time, so the link would idle while this
+        // one's last launches and write-backs finish and the next one starts:
+        // start the next queued GEMM's first panel fills behind this one's
+        // work instead. prefetch_distance = 0 turns this off.
+        hooks.tail = [this]() -> Error {
+          if (config_.prefetch_distance == 0) return {};
+          const std::shared_ptr<GemmPlanRecord> next = next_queued_gemm();
+          if (!next) return {};
+          return carry_gemm_head(runtime_, next->plan, uint64_t{next->plan.lookahead} + 1);
+        };
         return execute_gemm(runtime_, plan->plan, op.id(), hooks);
       },
-      units, plan->deadline_ms, out);
+      units, plan->deadline_ms, out, plan);
+}
+
+std::shared_ptr<GemmPlanRecord> Session::next_queued_gemm() const {
+  std::shared_ptr<GemmPlanRecord> next;
+  {
+    std::lock_guard<std::mutex> lock(queue_mutex_);
+    if (queue_.empty()) return nullptr;
+    next = queue_.front().gemm;
+  }
+  if (!next || next->a->released || next->b->released || next->c->released ||
+      (next->bias && next->bias->released))
+    return nullptr;
+  return next;
 }
 
 namespace {

@@ -114,10 +114,15 @@ private:
     std::shared_ptr<Operation> operation;
     Action action;
     bool shutdown = false;
+    std::shared_ptr<GemmPlanRecord> gemm; // set for a GEMM execution
   };
 
   Error enqueue(Action action, uint64_t units, uint64_t deadline_ms,
-                std::shared_ptr<Operation>& out);
+                std::shared_ptr<Operation>& out,
+                std::shared_ptr<GemmPlanRecord> gemm = nullptr);
+  // The plan of the GEMM queued next, if the next queued item is one whose
+  // allocations are all live.
+  std::shared_ptr<GemmPlanRecord> next_queued_gemm() const;
   Error invoke_sync(std::function<Error()> action, uint64_t timeout_ms = XVRAM_TIMEOUT_INFINITE);
   void worker_main();
   void refresh_telemetry();
