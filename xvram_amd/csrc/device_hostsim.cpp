@@ -241,6 +241,8 @@ public:
     if ((l.bias_row && !accessible(reinterpret_cast<uint64_t>(l.bias_row), l.m * 4ull)) ||
         (l.bias_col && !accessible(reinterpret_cast<uint64_t>(l.bias_col), l.n * 4ull)))
       return kSimBadAccess;
+    // Events attached to the dispatch are stamped around the kernel itself.
+    if (l.start_event) recorded_[l.start_event] = std::chrono::steady_clock::now();
     for (int64_t j = 0; j < l.n; ++j) {
       for (int64_t i = 0; i < l.m; ++i) {
         float acc = 0.f;
@@ -257,6 +259,7 @@ public:
         out = v;
       }
     }
+    if (l.stop_event) recorded_[l.stop_event] = std::chrono::steady_clock::now();
     std::lock_guard<std::mutex> lock(g_sim.mutex);
     ++g_sim.kernel_launches;
     return 0;

@@ -494,8 +494,8 @@ LaunchGeom launch_geom(const GemmPlanData& plan, const TileLaunch& l) {
 // Pipelined execution. Panels of the next `lookahead` launches are acquired
 // (H2D copies queued on the copy stream) before each launch is enqueued on the
 // compute stream; the compute stream waits on the fill events of the launch's
-// three frames; every frame's retire event is recorded after its kernel; a C
-// tile is written back on the D2H stream as soon as its last K panel is
+// three frames; the launch's stop event, recorded by its dispatch, becomes the
+// retire event of those frames; a C tile is written back on the D2H stream as soon as its last K panel is
 // enqueued. The host blocks only when a frame it wants to refill still has an
 // unretired consumer.
 Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
@@ -603,29 +603,26 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
       }
       k.relu = p.relu;
     }
+    // The launch's timing events are recorded by its dispatch; the stop event
+    // is also the retire event of its three frames (each marker packet between
+    // kernels would otherwise cost the compute stream a few microseconds).
     TraceInterval iv;
     iv.kind = 'k';
     if (Error e = rt.record_kernel(iv.start, iv.stop)) {
       result = e;
       break;
     }
-    if (int rc = rt.device().event_record(iv.start, cs)) {
-      result = rt.device_failure(rc, "gemm", "record");
-      break;
-    }
+    k.start_event = iv.start;
+    k.stop_event = iv.stop;
     if (int rc = rt.device().launch_sgemm(k, cs)) {
       result = rt.device_failure(rc, "gemm", "launch_tile");
       break;
     }
-    if (int rc = rt.device().event_record(iv.stop, cs)) {
-      result = rt.device_failure(rc, "gemm", "record");
-      break;
-    }
     rt.trace_push(iv);
     rt.note_kernel_launched();
-    if (Error e = rt.release_after(*acq.a, cs, false)) { result = e; break; }
-    if (Error e = rt.release_after(*acq.b, cs, false)) { result = e; break; }
-    if (Error e = rt.release_after(*acq.c, cs, true)) { result = e; break; }
+    if (Error e = rt.release_after_event(*acq.a, iv.stop, false)) { result = e; break; }
+    if (Error e = rt.release_after_event(*acq.b, iv.stop, false)) { result = e; break; }
+    if (Error e = rt.release_after_event(*acq.c, iv.stop, true)) { result = e; break; }
     if (l.last_panel) {
       if (Error e = rt.writeback_and_evict(*acq.c)) {
         result = e;

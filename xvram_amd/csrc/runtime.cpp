@@ -202,7 +202,7 @@ Error Runtime::close() {
     }
     if (f.ready) device_->event_destroy(f.ready);
     if (f.retire) device_->event_destroy(f.retire);
-    f.ready = f.retire = nullptr;
+    f.ready = f.retire = f.retire_ref = nullptr;
   }
   if (workspace_va_) {
     note(device_->mem_unmap(workspace_va_, workspace_bytes_), "unmap");
@@ -407,10 +407,16 @@ void Runtime::check_generation(const Frame& f) {
 
 Error Runtime::record_retire(Frame& f, Stream stream) {
   if (int rc = device_->event_record(f.retire, stream)) return device_failure(rc, "cache", "record");
+  adopt_retire(f, f.retire);
+  return {};
+}
+
+// `done` becomes the frame's retire event: one more event generation.
+void Runtime::adopt_retire(Frame& f, Event done) {
+  f.retire_ref = done;
   f.retire_pending = true;
   f.retire_seq = ++retire_records_;
   ++f.generation;
-  return {};
 }
 
 Error Runtime::unmap_frame(Frame& f) {
@@ -429,9 +435,9 @@ Error Runtime::unmap_frame(Frame& f) {
 Error Runtime::wait_retired(Frame& f) {
   if (!f.retire_pending) return {};
   ++t_.event_boundaries;
-  const int q = device_->event_query(f.retire);
+  const int q = device_->event_query(f.retire_ref);
   if (q == 1) {
-    if (int rc = device_->event_sync(f.retire)) return device_failure(rc, "cache", "event_sync");
+    if (int rc = device_->event_sync(f.retire_ref)) return device_failure(rc, "cache", "event_sync");
   } else if (q != 0) {
     return device_failure(q, "cache", "event_query");
   }
@@ -673,6 +679,17 @@ Error Runtime::wait_ready(Frame& f, Stream stream) {
 Error Runtime::release_after(Frame& f, Stream stream, bool dirty) {
   if (f.pins <= 0) return make_error(XVRAM_STATUS_INTERNAL, "cache", "release", "frame is not pinned");
   if (Error e = record_retire(f, stream)) return e;
+  return unpin(f, dirty);
+}
+
+Error Runtime::release_after_event(Frame& f, Event done, bool dirty) {
+  if (f.pins <= 0) return make_error(XVRAM_STATUS_INTERNAL, "cache", "release", "frame is not pinned");
+  if (!done) return make_error(XVRAM_STATUS_INTERNAL, "cache", "release", "no retire event");
+  adopt_retire(f, done);
+  return unpin(f, dirty);
+}
+
+Error Runtime::unpin(Frame& f, bool dirty) {
   --f.pins;
   if (dirty && f.state != EntryState::resident_dirty) {
     if (f.state == EntryState::h2d_in_flight) move(f, EntryState::resident_clean);
@@ -705,7 +722,7 @@ Error Runtime::writeback_and_evict(Frame& f) {
   HostAllocation* a = find(f.key.allocation_id);
   if (!a) return make_error(XVRAM_STATUS_INTERNAL, "cache", "writeback", "entry owner is gone");
   if (f.retire_pending)
-    if (int rc = device_->stream_wait_event(d2h_, f.retire))
+    if (int rc = device_->stream_wait_event(d2h_, f.retire_ref))
       return device_failure(rc, "cache", "stream_wait");
   move(f, EntryState::writeback_queued);
   TraceInterval iv;

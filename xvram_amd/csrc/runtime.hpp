@@ -108,7 +108,10 @@ struct Frame {
   uint64_t last_use = 0;
   Event ready = nullptr; // recorded on the H2D stream after a fill
   bool ready_pending = false;
-  Event retire = nullptr; // recorded after the last consumer (kernel or write-back)
+  Event retire = nullptr; // this frame's own event for its last consumer
+  // The event that marks the last consumer: `retire`, or the stop event of the
+  // tile launch that consumed the frame (adopted, not recorded again).
+  Event retire_ref = nullptr;
   bool retire_pending = false;
   uint64_t retire_seq = 0; // schedule order of the last retire record
   bool used_before = false;
@@ -213,6 +216,10 @@ public:
   Error wait_ready(Frame& frame, Stream stream);
   // Unpins after the consumer enqueued on `stream`; records the retire event.
   Error release_after(Frame& frame, Stream stream, bool dirty);
+  // Unpins after a consumer whose completion `done` already marks (the stop
+  // event of a tile launch, recorded by its dispatch): no event is recorded.
+  // `done` must stay unrecorded until the operation ends.
+  Error release_after_event(Frame& frame, Event done, bool dirty);
   // Writes a dirty entry back to its host bytes (D2H stream, ordered after the
   // frame's last consumer), removes it from the cache and drops clean entries
   // that overlap the written bytes.
@@ -282,6 +289,8 @@ private:
   void move(Frame& frame, EntryState to);
   void check_generation(const Frame& frame);
   Error record_retire(Frame& frame, Stream stream);
+  void adopt_retire(Frame& frame, Event done);
+  Error unpin(Frame& frame, bool dirty);
   Error map_frame_at(Frame& frame, uint64_t address);
   Error unmap_frame(Frame& frame);
   Error select_frame(Frame*& out);

@@ -11,6 +11,11 @@
 // leading dimensions that are multiples of 4 floats and `padded` = true (every
 // line may be read as whole 16-byte vectors up to its leading dimension), which
 // frame-packed panels always satisfy; anything else returns hipErrorInvalidValue.
+//
+// start_event / stop_event (hipEvent_t, optional) are recorded by the dispatch
+// itself (hipExtLaunchKernelGGL): no separate marker packets run between
+// kernels, and stop_event completes when the kernel does, so it can serve as
+// the retire event of every panel the launch reads or writes.
 #pragma once
 
 #include <cstdint>
@@ -30,6 +35,8 @@ struct SgemmLaunch {
   const float* bias_row = nullptr;
   const float* bias_col = nullptr;
   bool relu = false;
+  void* start_event = nullptr;
+  void* stop_event = nullptr;
 };
 
 // Enqueues the launch on `stream` (a hipStream_t); returns a hipError_t.

@@ -44,6 +44,7 @@
 //   * workgroup ids are remapped so each XCD (8 per chip, dispatched
 //     round-robin) walks a contiguous range of tiles, grouped GROUP_M tile-rows
 //     at a time, keeping its A/B panels in its own L2.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -55,7 +56,7 @@ namespace xvram::kernels {
 
 int wide_tile();
 hipError_t launch_wide(const device::Params& p, bool a_kcontig, bool b_ncontig,
-                       hipStream_t stream);
+                       hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 
 namespace {
 
@@ -266,9 +267,10 @@ __global__ __launch_bounds__(kThreads, 2) void sgemm_mfma_kernel(Params p) {
 }
 
 template <bool AK, bool BN>
-hipError_t launch_variant(const Params& p, hipStream_t stream) {
+hipError_t launch_variant(const Params& p, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
   const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
-  hipLaunchKernelGGL((sgemm_mfma_kernel<AK, BN>), grid, dim3(kThreads), 0, stream, p);
+  hipExtLaunchKernelGGL((sgemm_mfma_kernel<AK, BN>), grid, dim3(kThreads), 0, stream, start, stop,
+                        0, p);
   return hipGetLastError();
 }
 
@@ -313,18 +315,20 @@ int launch_sgemm(const SgemmLaunch& launch, void* stream) {
   p.bias_col = launch.bias_col;
   p.relu = launch.relu ? 1 : 0;
   auto* s = static_cast<hipStream_t>(stream);
+  auto* e0 = static_cast<hipEvent_t>(launch.start_event);
+  auto* e1 = static_cast<hipEvent_t>(launch.stop_event);
   if (wide_fits(launch)) {
     p.tiles_m = (launch.m + wide_tile() - 1) / wide_tile();
     p.tiles_n = (launch.n + wide_tile() - 1) / wide_tile();
-    return static_cast<int>(launch_wide(p, launch.a_kcontig, launch.b_ncontig, s));
+    return static_cast<int>(launch_wide(p, launch.a_kcontig, launch.b_ncontig, s, e0, e1));
   }
   p.tiles_m = (launch.m + kTileM - 1) / kTileM;
   p.tiles_n = (launch.n + kTileN - 1) / kTileN;
   hipError_t err;
-  if (!launch.a_kcontig && !launch.b_ncontig) err = launch_variant<false, false>(p, s);
-  else if (!launch.a_kcontig && launch.b_ncontig) err = launch_variant<false, true>(p, s);
-  else if (launch.a_kcontig && !launch.b_ncontig) err = launch_variant<true, false>(p, s);
-  else err = launch_variant<true, true>(p, s);
+  if (!launch.a_kcontig && !launch.b_ncontig) err = launch_variant<false, false>(p, s, e0, e1);
+  else if (!launch.a_kcontig && launch.b_ncontig) err = launch_variant<false, true>(p, s, e0, e1);
+  else if (launch.a_kcontig && !launch.b_ncontig) err = launch_variant<true, false>(p, s, e0, e1);
+  else err = launch_variant<true, true>(p, s, e0, e1);
   return static_cast<int>(err);
 }
 

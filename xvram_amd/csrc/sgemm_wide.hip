@@ -33,6 +33,7 @@
 // The host uses this kernel only when every operand panel spans less than
 // 2^31 bytes from a tile's base (32-bit buffer offsets) and the launch has at
 // least one tile per CU.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -351,17 +352,20 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_wide_kernel(Params p) {
 
 int wide_tile() { return kTile; }
 
-// Launches the 256 x 256 kernel for `p` (tiles_m / tiles_n already in 256s).
-hipError_t launch_wide(const Params& p, bool a_kcontig, bool b_ncontig, hipStream_t stream) {
+// Launches the 256 x 256 kernel for `p` (tiles_m / tiles_n already in 256s);
+// start / stop (optional) are recorded by the dispatch itself.
+hipError_t launch_wide(const Params& p, bool a_kcontig, bool b_ncontig, hipStream_t stream,
+                       hipEvent_t start, hipEvent_t stop) {
   const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
+  const dim3 block(kThreads);
   if (!a_kcontig && !b_ncontig)
-    hipLaunchKernelGGL((sgemm_wide_kernel<false, false>), grid, dim3(kThreads), 0, stream, p);
+    hipExtLaunchKernelGGL((sgemm_wide_kernel<false, false>), grid, block, 0, stream, start, stop, 0, p);
   else if (!a_kcontig && b_ncontig)
-    hipLaunchKernelGGL((sgemm_wide_kernel<false, true>), grid, dim3(kThreads), 0, stream, p);
+    hipExtLaunchKernelGGL((sgemm_wide_kernel<false, true>), grid, block, 0, stream, start, stop, 0, p);
   else if (a_kcontig && !b_ncontig)
-    hipLaunchKernelGGL((sgemm_wide_kernel<true, false>), grid, dim3(kThreads), 0, stream, p);
+    hipExtLaunchKernelGGL((sgemm_wide_kernel<true, false>), grid, block, 0, stream, start, stop, 0, p);
   else
-    hipLaunchKernelGGL((sgemm_wide_kernel<true, true>), grid, dim3(kThreads), 0, stream, p);
+    hipExtLaunchKernelGGL((sgemm_wide_kernel<true, true>), grid, block, 0, stream, start, stop, 0, p);
   return hipGetLastError();
 }
 
