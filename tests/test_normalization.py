@@ -1,18 +1,17 @@
 """Access normalisation and the entry-state table of the runtime (pure host
 logic, exported by the hostsim library for tests), pinned by the reference's
-own known-answer tests (tests/unit/residency_core_tests.cpp:38-147) and, where
-the reference tree is mounted, by a differential test against the reference's
-compiled core.cpp (oracle/_ref)."""
+own known-answer tests (tests/unit/residency_core_tests.cpp:38-147), by the
+answers of the reference's compiled core.cpp recorded in
+tests/golden/reference_outputs.json, and, where the reference tree is mounted,
+by a differential test against that compiled code (oracle/_ref)."""
 import ctypes
-import random
 
-import numpy as np
 import pytest
 
+import generators
 import xvram_amd as xv
+from generators import R, RW, WO, normalize
 
-U64 = ctypes.c_uint64
-R, RW, WO = 0, 1, 2
 STATES = ["host_clean", "prefetch_queued", "mapping", "h2d_in_flight", "resident_clean",
           "resident_dirty", "writeback_queued", "d2h_in_flight", "evicting", "poisoned"]
 S = {name: i for i, name in enumerate(STATES)}
@@ -26,33 +25,8 @@ def sim():
     lib = xv.load(hostsim=True).dll
     lib.xvram_hostsim_legal_transition.argtypes = [ctypes.c_int, ctypes.c_int]
     lib.xvram_hostsim_legal_transition.restype = ctypes.c_int
-    _declare(lib.xvram_hostsim_normalize)
+    generators.declare_normalize(lib.xvram_hostsim_normalize)
     return lib
-
-
-def _declare(fn):
-    p = ctypes.POINTER(U64)
-    fn.argtypes = [p, U64, p, U64, U64, p, p, p, p, ctypes.c_char_p, U64]
-    fn.restype = ctypes.c_int
-
-
-def normalize(fn, allocs, ranges, chunk):
-    a = np.array([v for pair in allocs for v in pair] or [0], dtype=np.uint64)
-    r = np.array([v for q in ranges for v in q] or [0], dtype=np.uint64)
-    cap = 4 * len(ranges) + 64
-    out_r = np.zeros(4 * cap, np.uint64)
-    out_c = np.zeros(5 * 64 * cap, np.uint64)
-    n_r, n_c = U64(cap), U64(64 * cap)
-    err = ctypes.create_string_buffer(64)
-    ptr = lambda x: x.ctypes.data_as(ctypes.POINTER(U64))
-    rc = fn(ptr(a), len(allocs), ptr(r), len(ranges), chunk, ptr(out_r), ctypes.byref(n_r),
-            ptr(out_c), ctypes.byref(n_c), err, 64)
-    assert rc in (0, 1), rc
-    if rc == 1:
-        return err.value.decode()
-    rng = [tuple(int(v) for v in out_r[4 * i:4 * i + 4]) for i in range(n_r.value)]
-    chk = [tuple(int(v) for v in out_c[5 * i:5 * i + 5]) for i in range(n_c.value)]
-    return rng, chk
 
 
 def test_reference_access_plan_kats(sim):
@@ -89,58 +63,55 @@ def test_reference_state_machine_kats(sim):
     assert legal("host_clean", "mapping") and legal("mapping", "host_clean")
 
 
+def check_state_table(sim, table):
+    diff = set()
+    for a in range(len(STATES)):
+        for b in range(len(STATES)):
+            mine = sim.xvram_hostsim_legal_transition(a, b)
+            if mine != table[a][b]:
+                diff.add((a, b))
+                assert mine == 1 and table[a][b] == 0
+    assert diff == EXTRA_EDGES
+
+
+def test_state_table_matches_recorded_reference(sim):
+    check_state_table(sim, generators.reference_outputs("state_table"))
+
+
 def test_state_table_matches_reference(sim, oracle_mod):
     ref = oracle_mod.ref_lib()
     if ref is None:
         pytest.skip("reference tree not built into oracle/_ref")
     ref.ref_legal_transition.argtypes = [ctypes.c_int, ctypes.c_int]
-    diff = set()
-    for a in range(len(STATES)):
-        for b in range(len(STATES)):
-            mine = sim.xvram_hostsim_legal_transition(a, b)
-            theirs = ref.ref_legal_transition(a, b)
-            if mine != theirs:
-                diff.add((a, b))
-                assert mine == 1 and theirs == 0
-    assert diff == EXTRA_EDGES
+    table = [[ref.ref_legal_transition(a, b) for b in range(len(STATES))] for a in range(len(STATES))]
+    assert table == generators.reference_outputs("state_table")
+    check_state_table(sim, table)
 
 
-def random_case(rng: random.Random):
-    n_alloc = rng.randint(1, 3)
-    ids = rng.sample(range(1, 8), n_alloc)
-    allocs = [(i, rng.choice([1, 7, 8, 9, 20, 33, 64, 100])) for i in ids]
-    ranges = []
-    for _ in range(rng.randint(1, 6)):
-        aid, size = rng.choice(allocs)
-        roll = rng.random()
-        if roll < 0.03:
-            ranges.append((rng.choice([99, 0]), 0, 1, R))
-        elif roll < 0.06:
-            ranges.append((aid, rng.randrange(size), 0, R))
-        elif roll < 0.08:
-            ranges.append((aid, (1 << 64) - rng.randint(1, 3), rng.randint(4, 9), R))
-        elif roll < 0.11:
-            ranges.append((aid, rng.randrange(size), size, R))
-        elif roll < 0.13:
-            ranges.append((aid, 0, 1, rng.choice([3, 7])))
-        else:
-            off = rng.randrange(size)
-            ranges.append((aid, off, rng.randint(1, size - off), rng.choice([R, RW, WO])))
-    return allocs, ranges, rng.choice([1, 3, 4, 8, 16])
+NORMALIZATION_OUTCOMES = {"ok", "unknown_allocation", "zero_length", "range_overflow",
+                          "range_out_of_bounds", "invalid_access_mode"}
+
+
+def test_normalization_matches_recorded_reference(sim):
+    cases = generators.normalization_cases(1000, 2024)
+    want = generators.reference_outputs("normalization", cases)
+    outcomes = set()
+    for case, theirs in zip(cases, want):
+        mine = generators.as_json(normalize(sim.xvram_hostsim_normalize, *case))
+        assert mine == theirs, case
+        outcomes.add(mine if isinstance(mine, str) else "ok")
+    assert outcomes >= NORMALIZATION_OUTCOMES
 
 
 def test_normalization_matches_reference(sim, oracle_mod):
     ref = oracle_mod.ref_lib()
     if ref is None:
         pytest.skip("reference tree not built into oracle/_ref")
-    _declare(ref.ref_normalize)
-    rng = random.Random(2024)
+    generators.declare_normalize(ref.ref_normalize)
     outcomes = set()
-    for _ in range(4000):
-        allocs, ranges, chunk = random_case(rng)
+    for allocs, ranges, chunk in generators.normalization_cases(4000, 2024):
         mine = normalize(sim.xvram_hostsim_normalize, allocs, ranges, chunk)
         theirs = normalize(ref.ref_normalize, allocs, ranges, chunk)
         assert mine == theirs, (allocs, ranges, chunk)
         outcomes.add(mine if isinstance(mine, str) else "ok")
-    assert outcomes >= {"ok", "unknown_allocation", "zero_length", "range_overflow",
-                        "range_out_of_bounds", "invalid_access_mode"}
+    assert outcomes >= NORMALIZATION_OUTCOMES

@@ -1,8 +1,9 @@
 """Pins the CPU oracle before anything is checked against it.
 
 - pattern values, closed-form sums and expected C: the reference's own KATs
-  (tests/unit/gemm_pattern_tests.cpp:103-153) and, where the reference tree is
-  mounted, the reference's compiled pattern code itself (oracle/_ref);
+  (tests/unit/gemm_pattern_tests.cpp:103-153), the answers of the reference's
+  compiled pattern code recorded in tests/golden/reference_outputs.json, and,
+  where the reference tree is mounted, that compiled code itself (oracle/_ref);
 - the FP64 SGEMM: brute-force Python loops (bit-exact, same summation order),
   numpy float64 matmul, the analytic pattern (exact) for all N/T views, and the
   reference example's closed-form inputs (examples/preview-gemm/main.cpp:53-58);
@@ -18,6 +19,7 @@ import os
 import numpy as np
 import pytest
 
+import generators
 import oracle
 
 
@@ -48,16 +50,24 @@ def test_pattern_expected_brute_force():
         assert oracle.pattern_expected(row, col, k) == naive
 
 
+def test_pattern_against_recorded_reference():
+    """The reference's own pattern.cpp answers, recorded by tests/golden/make_golden.py."""
+    pts = generators.pattern_points(1000, 7)
+    want = generators.reference_outputs("pattern", pts)
+    for (row, col, k), (a, b, expected, p, q, pq) in zip(pts, want):
+        assert oracle.pattern_a(row, k) == a
+        assert oracle.pattern_b(k, col) == b
+        assert oracle.pattern_expected(row, col, k) == expected
+        assert oracle.pattern_sums(k) == (p, q, pq)
+
+
 def test_pattern_against_compiled_reference():
     ref = oracle.ref_lib()
     if ref is None:
         pytest.skip("reference pattern code not built here (oracle/_ref needs /root/reference)")
     out = ctypes.c_uint64()
     p, q, pq = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
-    rng = np.random.default_rng(7)
-    for row, col, k in zip(rng.integers(0, 10**6, 2000), rng.integers(0, 10**6, 2000),
-                           rng.integers(1, 10**7, 2000)):
-        row, col, k = int(row), int(col), int(k)
+    for row, col, k in generators.pattern_points(2000, 7):
         assert ref.ref_pattern_a(row, k) == oracle.pattern_a(row, k)
         assert ref.ref_pattern_b(k, col) == oracle.pattern_b(k, col)
         assert ref.ref_pattern_expected(row, col, k, ctypes.byref(out)) == 1

@@ -4,51 +4,32 @@ Policies (CLOCK, the default, and LRU) are driven through a command program
 exported by the hostsim library: pinned by the reference's own known answers
 (tests/unit/residency_core_tests.cpp:200-250) and, where the reference tree is
 mounted, by random programs run side by side against the reference's compiled
-policy.cpp (oracle/_ref). The live budget (shrink at once, grow by two frames
+policy.cpp (oracle/_ref), whose answers tests/golden/reference_outputs.json
+also records for checkouts without the reference tree. The live budget (shrink at once, grow by two frames
 after ten samples, one retry after an out-of-memory frame allocation;
 reference runtime.cpp:3184-3468) is exercised through hostsim sessions whose
 device memory the test changes underneath them."""
 import ctypes
-import random
 import time
 
 import numpy as np
 import pytest
 
+import generators
 import xvram_amd as xv
+from generators import CLEAN, DIRTY, DROP, ERASE, INSERT, NONE, SELECT, SET, TOUCH
 from xvram_amd import abi
 
 from gemm_cases import Problem, uniform
 
 KiB = 1 << 10
-U64 = ctypes.c_uint64
-INSERT, TOUCH, ERASE, SET, DROP, SELECT = range(6)
-CLEAN, DIRTY = 4, 5  # EntryState::resident_clean / resident_dirty
-H2D = 3              # EntryState::h2d_in_flight (not eligible)
-NONE = (1 << 64) - 1
-
-
-def declare(fn):
-    fn.argtypes = [ctypes.c_int, ctypes.POINTER(U64), U64, ctypes.POINTER(U64)]
-    fn.restype = ctypes.c_int
 
 
 @pytest.fixture(scope="module")
 def run():
     lib = xv.load(hostsim=True).dll
-    declare(lib.xvram_hostsim_policy_run)
-    return lambda kind, cmds: execute(lib.xvram_hostsim_policy_run, kind, cmds)
-
-
-def execute(fn, kind, cmds):
-    words = []
-    for c in cmds:
-        words += list(c) + [0] * (7 - len(c))
-    prog = np.array(words, dtype=np.uint64)
-    out = np.zeros(len(cmds), dtype=np.uint64)
-    assert fn(kind, prog.ctypes.data_as(ctypes.POINTER(U64)), len(cmds),
-              out.ctypes.data_as(ctypes.POINTER(U64))) == 0
-    return [int(v) for v in out]
+    generators.declare_policy(lib.xvram_hostsim_policy_run)
+    return lambda kind, cmds: generators.run_policy(lib.xvram_hostsim_policy_run, kind, cmds)
 
 
 def test_clock_kats(run):
@@ -82,26 +63,19 @@ def test_hot_entries_go_last(run, kind):
     assert out[4] == 2
 
 
-def random_program(rng: random.Random, length=120):
-    cmds, seq, ids = [], 0, list(range(1, 9))
-    for _ in range(length):
-        r = rng.random()
-        i = rng.choice(ids)
-        seq += rng.choice([0, 1, 1, 2])
-        if r < 0.25:
-            cmds.append((INSERT, i, seq, int(rng.random() < 0.3), int(rng.random() < 0.2)))
-        elif r < 0.45:
-            cmds.append((TOUCH, i, seq, int(rng.random() < 0.2)))
-        elif r < 0.5:
-            cmds.append((ERASE, i))
-        elif r < 0.75:
-            cmds.append((SET, i, rng.choice([CLEAN, CLEAN, DIRTY, H2D]), int(rng.random() < 0.2),
-                         int(rng.random() < 0.15), int(rng.random() < 0.1), int(rng.random() < 0.1)))
-        elif r < 0.8:
-            cmds.append((DROP, i))
-        else:
-            cmds.append((SELECT,))
-    return cmds
+def selections(programs, outputs):
+    return sum(1 for cmds, out in zip(programs, outputs)
+               for c, v in zip(cmds, out) if c[0] == SELECT and v != NONE)
+
+
+@pytest.mark.parametrize("kind", [0, 1], ids=["clock", "lru"])
+def test_policies_match_recorded_reference(run, kind):
+    programs = generators.policy_programs(kind, 150)
+    want = generators.reference_outputs(("policy_clock", "policy_lru")[kind], programs)
+    for cmds, theirs in zip(programs, want):
+        mine = [-1 if v == NONE else v for v in run(kind, cmds)]
+        assert mine == theirs, cmds
+    assert selections(programs, want) > 250
 
 
 @pytest.mark.parametrize("kind", [0, 1], ids=["clock", "lru"])
@@ -109,16 +83,15 @@ def test_policies_match_reference(run, oracle_mod, kind):
     ref = oracle_mod.ref_lib()
     if ref is None:
         pytest.skip("reference tree not built into oracle/_ref")
-    declare(ref.ref_policy_run)
-    rng = random.Random(77 + kind)
-    selections = 0
-    for _ in range(300):
-        cmds = random_program(rng)
+    generators.declare_policy(ref.ref_policy_run)
+    programs = generators.policy_programs(kind, 300)
+    outputs = []
+    for cmds in programs:
         mine = run(kind, cmds)
-        theirs = execute(ref.ref_policy_run, kind, cmds)
+        theirs = generators.run_policy(ref.ref_policy_run, kind, cmds)
         assert mine == theirs, cmds
-        selections += sum(1 for c, v in zip(cmds, mine) if c[0] == SELECT and v != NONE)
-    assert selections > 500
+        outputs.append(mine)
+    assert selections(programs, outputs) > 500
 
 
 # ---- live budget ------------------------------------------------------------------------

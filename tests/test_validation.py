@@ -1,12 +1,15 @@
 """Boundary validation: session/allocation/GEMM descriptors are rejected with
 the reference's statuses, and GEMM-problem validity matches the reference's own
-validate_problem (src/gemm/planner.cpp:785-859, compiled into oracle/_ref) on
-randomly generated descriptors. Runs over the host-simulation library."""
+validate_problem (src/gemm/planner.cpp:785-859) on randomly generated
+descriptors: against its answers recorded in tests/golden/reference_outputs.json
+and, where the reference tree is mounted, against the compiled function itself
+(oracle/_ref). Runs over the host-simulation library."""
 import ctypes
 
 import numpy as np
 import pytest
 
+import generators
 import oracle
 import xvram_amd as xv
 from xvram_amd import abi
@@ -169,87 +172,63 @@ def test_gemm_descriptor_rules(session):
     plan.release()
 
 
-class RefMatrix(ctypes.Structure):
-    _fields_ = [("allocation_id", ctypes.c_uint64), ("allocation_bytes", ctypes.c_uint64),
-                ("offset_bytes", ctypes.c_uint64), ("rows", ctypes.c_uint64),
-                ("columns", ctypes.c_uint64), ("leading_dimension", ctypes.c_uint64),
-                ("layout", ctypes.c_uint32), ("element_type", ctypes.c_uint32)]
-
-
-def test_problem_validation_matches_reference(session):
-    """Random GEMM descriptors: the library's verdict equals the reference
-    planner's validate_problem (error class included, via the message)."""
-    ref = oracle.ref_lib()
-    if ref is None:
-        pytest.skip("reference planner not built here (oracle/_ref needs /root/reference)")
-    ref.ref_validate_problem.argtypes = [ctypes.POINTER(RefMatrix)] * 3 + [
-        ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_double]
-    rng = np.random.default_rng(2024)
-    sizes = [4096, 8192, 20000]
-    allocs = [session.allocation(s) for s in sizes]
+def abi_verdicts(session, cases):
+    """gemm_plan_create of each case: (status, last error message)."""
+    allocs = [session.allocation(size) for size in generators.VALIDATION_SIZES]
     api = session.api
-    seen = set()
-    for _ in range(1500):
-        ids = rng.integers(0, 3, 3)
-        mats = []
-        descs = []
-        for slot in range(3):
-            al = int(ids[slot])
-            rows = int(rng.integers(1, 40))
-            cols = int(rng.integers(1, 40))
-            layout = int(rng.integers(0, 2))
-            dtype = int(rng.choice([0, 1, 2, 2, 2, 3]))
-            need = cols if layout == abi.ROW_MAJOR else rows
-            ld = int(need + rng.integers(-2, 4)) if rng.random() < 0.9 else int(rng.integers(1, 1 << 33))
-            ld = max(ld, 1)
-            offset = [0, 0, 64, 1000, 4096, 30000, (1 << 64) - 8][int(rng.integers(0, 7))]
-            descs.append(xv.matrix(allocs[al], rows, cols, ld, layout, offset, dtype))
-            mats.append(RefMatrix(al + 1, sizes[al], offset, rows, cols, ld, layout, dtype))
-        # make shapes consistent most of the time
-        op_a, op_b = int(rng.integers(0, 2)), int(rng.integers(0, 2))
-        if rng.random() < 0.7:
-            m = descs[0].columns if op_a else descs[0].rows
-            k = descs[0].rows if op_a else descs[0].columns
-            n = int(rng.integers(1, 40))
-            if op_b:
-                descs[1].rows, descs[1].columns = n, k
-            else:
-                descs[1].rows, descs[1].columns = k, n
-            descs[2].rows, descs[2].columns = m, n
-            for slot in (1, 2):
-                d = descs[slot]
-                need = d.columns if d.layout == abi.ROW_MAJOR else d.rows
-                if d.leading_dimension < need and rng.random() < 0.8:
-                    d.leading_dimension = need
-                mats[slot].rows, mats[slot].columns = d.rows, d.columns
-                mats[slot].leading_dimension = d.leading_dimension
-        compute = int(rng.integers(0, 4))
-        beta = float(rng.choice([0.0, 0.5]))
+    out = []
+    for c in cases:
         gd = abi.gemm_desc_init()
-        gd.a, gd.b, gd.c = descs
-        gd.operation_a, gd.operation_b = op_a, op_b
-        gd.compute_mode = compute
-        gd.beta = beta
+        gd.a, gd.b, gd.c = [xv.matrix(allocs[al], rows, cols, ld, layout, offset, dtype)
+                            for al, offset, rows, cols, ld, layout, dtype in c["mats"]]
+        gd.operation_a, gd.operation_b = c["op_a"], c["op_b"]
+        gd.compute_mode = c["compute"]
+        gd.beta = c["beta"]
         h = ctypes.c_void_p()
         st = api.gemm_plan_create(session.handle, ctypes.byref(gd), ctypes.byref(h))
-        # reference compute-mode mapping (src/sdk/runtime.cpp:119-135)
-        a_type = mats[0].element_type
-        if compute == abi.COMPUTE_AUTO:
-            rc = 2 if a_type == abi.DATA_FP64 else (0 if a_type in (0, 1) else 1)
-        else:
-            rc = {abi.COMPUTE_FP32_STRICT: 0, abi.COMPUTE_FP32_TF32: 1, abi.COMPUTE_FP64: 2}[compute]
-        want = ref.ref_validate_problem(ctypes.byref(mats[0]), ctypes.byref(mats[1]),
-                                        ctypes.byref(mats[2]), op_a, op_b, rc, beta)
+        msg = session.error().message.decode() if st != abi.SUCCESS else ""
+        if st == abi.SUCCESS:
+            api.gemm_plan_release(h)
+        out.append((st, msg))
+    return out
+
+
+def check_verdicts(cases, verdicts, wants):
+    """A reference verdict of 0 (valid) must plan (FP32) or be UNSUPPORTED
+    (other types); any other verdict is INVALID_ARGUMENT naming that class."""
+    seen = set()
+    for c, (st, msg), want in zip(cases, verdicts, wants):
         seen.add(want)
         if want == 0:
-            expected = abi.SUCCESS if a_type == abi.DATA_FP32 else abi.UNSUPPORTED
-            assert st == expected, (st, session.error().message)
-            if st == abi.SUCCESS:
-                api.gemm_plan_release(h)
+            expected = abi.SUCCESS if c["mats"][0][6] == abi.DATA_FP32 else abi.UNSUPPORTED
+            assert st == expected, (c, st, msg)
         else:
-            assert st == abi.INVALID_ARGUMENT
-            msg = session.error().message.decode()
-            assert f"invalid_problem: {PROBLEM_ERRORS[want]}" in msg, (msg, PROBLEM_ERRORS[want])
+            assert st == abi.INVALID_ARGUMENT, (c, st)
+            assert f"invalid_problem: {PROBLEM_ERRORS[want]}" in msg, (c, msg, PROBLEM_ERRORS[want])
     # every class reachable through the ABI (the ABI itself rejects zero
     # sizes and bad enums first, and one handle cannot have two sizes)
     assert seen >= {0, 7, 8, 9, 10, 11, 12, 13}, sorted(seen)
+
+
+def test_problem_validation_matches_recorded_reference(session):
+    cases = generators.validation_cases(1500, 2024)
+    wants = generators.reference_outputs("validation", cases)
+    check_verdicts(cases, abi_verdicts(session, cases), wants)
+
+
+def test_problem_validation_matches_reference(session):
+    """The same random descriptors through the compiled reference planner."""
+    ref = oracle.ref_lib()
+    if ref is None:
+        pytest.skip("reference planner not built here (oracle/_ref needs /root/reference)")
+    ref.ref_validate_problem.argtypes = [ctypes.POINTER(generators.RefMatrix)] * 3 + [
+        ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_double]
+    cases = generators.validation_cases(1500, 2024)
+    wants = []
+    for c in cases:
+        mats = [generators.ref_matrix(m) for m in c["mats"]]
+        rc = generators.reference_compute_mode(c["compute"], c["mats"][0][6])
+        wants.append(ref.ref_validate_problem(*(ctypes.byref(m) for m in mats), c["op_a"],
+                                              c["op_b"], rc, c["beta"]))
+    assert wants == generators.reference_outputs("validation", cases)
+    check_verdicts(cases, abi_verdicts(session, cases), wants)
