@@ -40,7 +40,10 @@ PCIE5_X16_THEORETICAL_GBPS = 63.0  # per direction
 OP_N, OP_T = 0, 1
 WORKLOADS = {
     # name: (m, n, k, op_a, op_b, budget, frame, description)
-    "ns65536_nt_16g": (65536, 65536, 65536, OP_N, OP_T, 16 * GiB, 256 * MiB,
+    # 512 MiB frames: 8192 x 8192 C tiles with 16384-deep K panels (each C tile
+    # passes through HBM 4 times instead of 8 with 256 MiB frames' 8192-deep
+    # panels); 31 frames still hide the larger A/B re-streaming under compute.
+    "ns65536_nt_16g": (65536, 65536, 65536, OP_N, OP_T, 16 * GiB, 512 * MiB,
                        "FP32 SGEMM N/T 65536^3, 3 x 16 GiB operands in pinned host RAM, "
                        "16 GiB VRAM budget (3x)"),
     "c4_32768_nt_2g": (32768, 32768, 32768, OP_N, OP_T, 2 * GiB, 64 * MiB,
@@ -419,6 +422,10 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--frame-mib", type=int, default=0,
+                    help="cache frame (chunk_size_bytes) in MiB instead of the workload's")
+    ap.add_argument("--tile-hints", default="0,0,0", metavar="M,N,K",
+                    help="tile_m/n/k hints of the GEMM plan (0 = the planner's choice)")
     ap.add_argument("--trace-out", default=None,
                     help="also keep the library's per-operation trace (JSON lines) here")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -448,6 +455,8 @@ def main() -> int:
         log(f"workload {args.workload}")
         return run_chain(args, xv, lib, synth, link)
     m, n, k, op_a, op_b, budget, frame, desc = WORKLOADS[args.workload]
+    if args.frame_mib:
+        frame = args.frame_mib * MiB
     log(f"workload {args.workload}: {desc}")
     cfg = dict(chunk_size_bytes=frame)
     if budget:
@@ -463,7 +472,8 @@ def main() -> int:
     fill_allocation(synth, b, b_rows * b_cols, 2)
     log(f"operands ready: {3 * m * n * 4 / GiB:.1f} GiB pinned host ({time.time() - t0:.1f}s)")
     plan = xv.GemmPlan(session, xv.matrix(a, a_rows, a_cols, a_rows),
-                       xv.matrix(b, b_rows, b_cols, b_rows), xv.matrix(c, m, n, m), op_a, op_b)
+                       xv.matrix(b, b_rows, b_cols, b_rows), xv.matrix(c, m, n, m), op_a, op_b,
+                       tile_hints=tuple(int(v) for v in args.tile_hints.split(",")))
     info = plan.info()
     log(f"plan: tiles {info.tile_m}x{info.tile_n}x{info.tile_k}, {info.tile_count} launches")
     for i in range(args.warmup):

@@ -334,8 +334,13 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
     tn = p.n;
     bk = p.k;
   } else {
-    uint64_t s = isqrt(F / 4);
-    s = s >= 256 ? s / 256 * 256 : std::max<uint64_t>(16, s / 16 * 16);
+    // Start from the largest power of two whose square panel fits a frame:
+    // such extents divide the usual problem sizes (no ragged last tile of a
+    // 65536 extent, as 11520 would leave), and the growth step below then
+    // spends the rest of the frame on a deeper K panel (fewer launches, and
+    // fewer passes of each C tile through HBM).
+    uint64_t s = 16;
+    while ((s * 2) * (s * 2) <= F / 4) s *= 2;
     tm = std::min(p.m, s);
     tn = std::min(p.n, s);
     bk = std::min(p.k, s);
