@@ -123,3 +123,55 @@ def test_carry_into_a_cancelled_operation(sim, oracle_mod):
         ref, absab = oracle_mod.sgemm_f64(np.asfortranarray(ws[l]), np.asfortranarray(out[l]))
         bad, _, _ = oracle_mod.check_bound(out[l + 1], ws[l].shape[1], ref, absab)
         assert bad == 0, l
+
+
+def test_carried_frames_can_be_evicted_by_a_later_operation(sim, oracle_mod):
+    """The GEMM a fill was carried for is cancelled; the next operation, a
+    transaction whose working set needs every frame, must be able to evict the
+    carried entries (their reuse waits for the fill, like any other frame's)."""
+    frames, frame = 14, 16 * KiB
+    s = xv.Session(sim, chunk_size_bytes=frame, cache_target_bytes=frames * frame,
+                   workspace_cap_bytes=0, device_headroom_bytes=0, prefetch_distance=2)
+    try:
+        m, n = 96, 40
+        x = s.allocation(m * n * 4)
+        x.write(np.asfortranarray(uniform(oracle_mod, m, n, 50)).T.copy())
+        ys = [s.allocation(m * n * 4) for _ in range(2)]
+        plans = []
+        for l in range(2):
+            w = s.allocation(m * m * 4)
+            w.write(np.asfortranarray(uniform(oracle_mod, m, m, 51 + l)).T.copy())
+            plans.append(xv.GemmPlan(s, xv.matrix(w, m, m, m), xv.matrix(x, m, n, m),
+                                     xv.matrix(ys[l], m, n, m)))
+        big = s.allocation(frames * frame)
+        big.write(np.arange(frames * frame // 4, dtype=np.float32))
+        gate = threading.Event()
+        scratch = s.allocation(4 * KiB)
+
+        def hold(_view):
+            gate.wait(30)
+
+        held = s.transaction([xv.access(scratch, 0, 4 * KiB)], hold)
+        first = plans[0].submit()
+        second = plans[1].submit()
+        seen = []
+        whole = s.transaction([xv.access(big, 0, frames * frame)],
+                              lambda view: seen.append(len(view.ranges)))
+        assert second.cancel() == abi.SUCCESS
+        gate.set()
+        results = []
+        for op in (held, first, second, whole):
+            st, info = op.wait()
+            assert st == abi.SUCCESS
+            results.append((info.result, op.error().message))
+            op.release()
+        assert [r for r, _ in results] == [abi.SUCCESS, abi.SUCCESS, abi.CANCELLED, abi.SUCCESS], \
+            results
+        assert seen == [1]
+        for p in plans:
+            p.release()
+    finally:
+        s.close()
+        t = s.telemetry()
+        assert t.mappings == t.unmaps and t.unsafe_transitions == 0 and t.unsafe_remaps == 0
+        s.release()

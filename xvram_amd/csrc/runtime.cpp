@@ -1157,6 +1157,14 @@ Error Runtime::begin_operation() {
                       "the transaction duration guard");
   kernels_in_operation_ = 0;
   transactions_in_operation_ = 0;
+  // Entries the previous operation carried over become ordinary clean
+  // entries: a consumer still waits for the fill (ready event) and a reuse of
+  // the frame still waits for the copy (retire event), so the policy may pick
+  // them as victims like any other (the operation they were carried for may
+  // have been cancelled, or need the frames for something else).
+  for (Frame& f : frames_)
+    if (f.carry_serial != 0 && f.keyed && f.state == EntryState::h2d_in_flight)
+      move(f, EntryState::resident_clean);
   ++op_serial_;
   carry_active_ = false;
   // Fills the previous operation carried over belong to this one's trace.
