@@ -14,13 +14,6 @@ namespace {
 
 uint64_t lcm64(uint64_t a, uint64_t b) { return a / std::gcd(a, b) * b; }
 
-// Combined access of two overlapping spans (the reference ORs mode bits:
-// anything that both reads and writes is read_write).
-uint32_t combine_modes(uint32_t a, uint32_t b) {
-  if (a == b) return a;
-  return XVRAM_ACCESS_READ_WRITE;
-}
-
 } // namespace
 
 bool is_legal_transition(EntryState from, EntryState to) {
@@ -839,26 +832,38 @@ const char* normalize_accesses(const std::vector<AllocationExtent>& allocations,
     if (r.offset >= size->second || end > size->second) return "range_out_of_bounds";
     by_alloc[r.allocation_id].push_back(&r);
   }
+  // Per allocation, a sweep over the range boundaries: between two
+  // consecutive boundaries the covering ranges are fixed, and their combined
+  // mode is the one mode they share, else read-write. Counting the active
+  // ranges per mode makes this O((B + R) log R) instead of testing every
+  // range against every elementary piece.
+  struct Boundary {
+    uint64_t at;
+    int delta; // +1 a range starts here, -1 one ends here
+    uint32_t mode;
+  };
+  std::vector<Boundary> bounds;
   for (const auto& [id, list] : by_alloc) {
-    std::vector<uint64_t> cuts;
-    cuts.reserve(2 * list.size());
+    bounds.clear();
+    bounds.reserve(2 * list.size());
     for (const AccessSpan* r : list) {
-      cuts.push_back(r->offset);
-      cuts.push_back(r->offset + r->length);
+      bounds.push_back(Boundary{r->offset, +1, r->mode});
+      bounds.push_back(Boundary{r->offset + r->length, -1, r->mode});
     }
-    std::sort(cuts.begin(), cuts.end());
-    cuts.erase(std::unique(cuts.begin(), cuts.end()), cuts.end());
-    for (size_t i = 0; i + 1 < cuts.size(); ++i) {
-      const uint64_t lo = cuts[i], hi = cuts[i + 1];
-      bool covered = false;
-      uint32_t mode = XVRAM_ACCESS_READ;
-      for (const AccessSpan* r : list) {
-        if (r->offset <= lo && hi <= r->offset + r->length) {
-          mode = covered ? combine_modes(mode, r->mode) : r->mode;
-          covered = true;
-        }
-      }
-      if (!covered) continue;
+    std::sort(bounds.begin(), bounds.end(),
+              [](const Boundary& a, const Boundary& b) { return a.at < b.at; });
+    uint64_t active[3] = {0, 0, 0}; // READ, READ_WRITE, WRITE_ONLY
+    for (size_t i = 0; i < bounds.size();) {
+      const uint64_t lo = bounds[i].at;
+      for (; i < bounds.size() && bounds[i].at == lo; ++i)
+        active[bounds[i].mode] += static_cast<uint64_t>(static_cast<int64_t>(bounds[i].delta));
+      if (i == bounds.size()) break;
+      const uint64_t hi = bounds[i].at;
+      const int kinds = (active[0] != 0) + (active[1] != 0) + (active[2] != 0);
+      if (kinds == 0) continue;
+      uint32_t mode = XVRAM_ACCESS_READ_WRITE;
+      if (kinds == 1) mode = active[0] ? XVRAM_ACCESS_READ : (active[1] ? XVRAM_ACCESS_READ_WRITE
+                                                                          : XVRAM_ACCESS_WRITE_ONLY);
       AccessSpan* last = normalized.empty() ? nullptr : &normalized.back();
       if (last && last->allocation_id == id && last->offset + last->length == lo &&
           last->mode == mode) {
