@@ -238,3 +238,30 @@ def test_product_generator_is_bit_identical():
     blk = np.empty(10 * 5, np.float32)
     synth.synth_fill_uniform_strided(blk.ctypes.data_as(fp), 10, 5, 8, 3 + 5 * 50, 1, 50)
     assert np.array_equal(blk.reshape(5, 10).T, full[3:13, 5:10])
+
+
+def test_product_pattern_fillers_match_the_oracle():
+    """The product-side pattern fillers (used to build full-size pattern
+    operands) against the oracle's restatement of pattern.cpp, for both
+    storage forms of each operand and a column window that does not start at 0."""
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "xvram_amd",
+                        "lib", "libxvram_synth.so")
+    synth = ctypes.CDLL(path)
+    fp = ctypes.POINTER(ctypes.c_float)
+    u64 = ctypes.c_uint64
+    for name in ("synth_fill_pattern_a", "synth_fill_pattern_b"):
+        getattr(synth, name).argtypes = [fp, u64, u64, u64, ctypes.c_int]
+    rows, cols, col0 = 37, 23, 1000
+    for transposed in (0, 1):
+        a = np.empty(rows * cols, np.float32)
+        synth.synth_fill_pattern_a(a.ctypes.data_as(fp), rows, cols, col0, transposed)
+        b = np.empty(rows * cols, np.float32)
+        synth.synth_fill_pattern_b(b.ctypes.data_as(fp), rows, cols, col0, transposed)
+        a, b = a.reshape(cols, rows).T, b.reshape(cols, rows).T  # stored (x, y - col0)
+        for x in range(rows):
+            for c in range(cols):
+                y = col0 + c
+                # stored N: A(i=x, k=y), B(k=x, j=y); stored T: A(i=y, k=x), B(k=y, j=x)
+                want_a = oracle.pattern_a(y, x) if transposed else oracle.pattern_a(x, y)
+                want_b = oracle.pattern_b(y, x) if transposed else oracle.pattern_b(x, y)
+                assert a[x, c] == want_a and b[x, c] == want_b, (transposed, x, y)

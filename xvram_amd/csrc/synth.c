@@ -53,3 +53,29 @@ void synth_fill_normal(float* out, uint64_t count, uint64_t seed, uint64_t first
     out[i] = (float)(sigma * sqrt(-2.0 * log(u1)) * cos(two_pi * u2));
   }
 }
+
+/* The analytic integer pattern of the reference's GEMM benchmark
+ * (src/gemm_bench/pattern.cpp:207-237): A(i,k) = 1 + i%3 + k%2 and
+ * B(k,j) = 1 + j%5 + k%3, whose product is exact in FP32 while 28*K < 2^24.
+ * These fill columns [col0, col0 + cols) of the operand as stored column-major
+ * with `rows` rows (out[x + c*rows] is stored element (x, col0 + c)); a
+ * transposed operand is stored as its transpose (op T). */
+void synth_fill_pattern_a(float* out, uint64_t rows, uint64_t cols, uint64_t col0, int transposed) {
+#pragma omp parallel for schedule(static)
+  for (int64_t c = 0; c < (int64_t)cols; ++c) {
+    const uint64_t y = col0 + (uint64_t)c;
+    float* col = out + (uint64_t)c * rows;
+    for (uint64_t x = 0; x < rows; ++x)
+      col[x] = transposed ? (float)(1 + y % 3 + x % 2) : (float)(1 + x % 3 + y % 2);
+  }
+}
+
+void synth_fill_pattern_b(float* out, uint64_t rows, uint64_t cols, uint64_t col0, int transposed) {
+#pragma omp parallel for schedule(static)
+  for (int64_t c = 0; c < (int64_t)cols; ++c) {
+    const uint64_t y = col0 + (uint64_t)c;
+    float* col = out + (uint64_t)c * rows;
+    for (uint64_t x = 0; x < rows; ++x)
+      col[x] = transposed ? (float)(1 + x % 5 + y % 3) : (float)(1 + y % 5 + x % 3);
+  }
+}
