@@ -476,7 +476,31 @@ struct Acquired {
   Frame* a = nullptr;
   Frame* b = nullptr;
   Frame* c = nullptr;
+  uint64_t slice = 0;                  // K depth of each slice; 0 = one launch
+  std::vector<Event> a_ready, b_ready; // per-slice fill events (empty: whole panel)
 };
+
+// The first launch of an operation waits for its whole A and B panels before
+// any compute can start (18.8 ms for 2 x 512 MiB at 57 GB/s). When they are
+// cache misses, each is filled by copies of K slices of at least this depth
+// (at most kFirstSlices of them) and the launch runs as one kernel per slice,
+// each waiting only for its own slices of A and B: compute starts after the
+// first slices land and runs under the rest of the fill.
+constexpr uint64_t kFirstSliceMin = 2048;
+constexpr uint64_t kFirstSlices = 8;
+
+// The K slices of a panel as copy pieces: K runs along its lines (op-N A,
+// op-T B) or within them (op-T A, op-N B).
+std::vector<PanelPiece> k_slices(const PanelGeom& g, bool k_within_lines, uint64_t slice) {
+  std::vector<PanelPiece> out;
+  const uint64_t depth = k_within_lines ? g.xn : g.yn;
+  for (uint64_t k0 = 0; k0 < depth; k0 += slice) {
+    const uint64_t d = std::min(slice, depth - k0);
+    if (k_within_lines) out.push_back(PanelPiece{0, g.yn, k0 * 4, d * 4});
+    else out.push_back(PanelPiece{k0, d, 0, g.xn * 4});
+  }
+  return out;
+}
 
 struct LaunchGeom {
   uint64_t i0, h, j0, g, p0, w;
@@ -541,17 +565,27 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     const PanelGeom bg = b_geom(p.b, g.p0, g.w, g.j0, g.g);
     const PanelGeom cg = c_geom(g.i0, g.h, g.j0, g.g);
     const bool c_needs_data = !l.first_panel || p.beta != 0.f;
+    if (idx == 0 && plan.launches.size() > 1 && g.w >= 2 * kFirstSliceMin)
+      acq.slice = std::max(kFirstSliceMin, round_up(ceil_div(g.w, kFirstSlices), 16));
     if (Error e = rt.acquire(panel_key(p.c, cg), packed_ld(cg) * 4, c_needs_data, acq.c)) return e;
-    if (Error e = rt.acquire(panel_key(p.a, ag), packed_ld(ag) * 4, true, acq.a)) {
+    // A hit (or an unsliced launch) leaves the per-slice event lists empty.
+    const auto operand = [&](const CanonOperand& op, const PanelGeom& pg, bool k_within,
+                             Frame*& out, std::vector<Event>& ready) -> Error {
+      if (!acq.slice) return rt.acquire(panel_key(op, pg), packed_ld(pg) * 4, true, out);
+      return rt.acquire_pieces(panel_key(op, pg), packed_ld(pg) * 4,
+                               k_slices(pg, k_within, acq.slice), out, ready);
+    };
+    if (Error e = operand(p.a, ag, p.a.transposed, acq.a, acq.a_ready)) {
       (void)rt.release_after(*acq.c, rt.compute_stream(), false);
       return e;
     }
-    if (Error e = rt.acquire(panel_key(p.b, bg), packed_ld(bg) * 4, true, acq.b)) {
+    if (Error e = operand(p.b, bg, !p.b.transposed, acq.b, acq.b_ready)) {
       (void)rt.release_after(*acq.c, rt.compute_stream(), false);
       (void)rt.release_after(*acq.a, rt.compute_stream(), false);
       return e;
     }
-    window.push_back(acq);
+    if (acq.a_ready.empty() && acq.b_ready.empty()) acq.slice = 0; // both cached
+    window.push_back(std::move(acq));
     return {};
   };
 
@@ -570,7 +604,7 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
       }
     }
     if (result) break;
-    Acquired acq = window.front();
+    Acquired acq = std::move(window.front());
     window.pop_front();
     const TileLaunch& l = plan.launches[idx];
     const LaunchGeom g = launch_geom(plan, l);
@@ -578,56 +612,86 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     const PanelGeom bg = b_geom(p.b, g.p0, g.w, g.j0, g.g);
     const PanelGeom cg = c_geom(g.i0, g.h, g.j0, g.g);
     Stream cs = rt.compute_stream();
-    for (Frame* f : {acq.a, acq.b, acq.c}) {
-      if (Error e = rt.wait_ready(*f, cs)) {
+    // Whole-panel fills are waited for up front; sliced ones slice by slice.
+    if (Error e = rt.wait_ready(*acq.c, cs)) { result = e; break; }
+    if (acq.a_ready.empty())
+      if (Error e = rt.wait_ready(*acq.a, cs)) { result = e; break; }
+    if (acq.b_ready.empty())
+      if (Error e = rt.wait_ready(*acq.b, cs)) { result = e; break; }
+    const uint64_t depth = acq.slice ? acq.slice : g.w;
+    const uint64_t slices = ceil_div(g.w, depth);
+    const int64_t lda = static_cast<int64_t>(packed_ld(ag));
+    const int64_t ldb = static_cast<int64_t>(packed_ld(bg));
+    Event done = nullptr;
+    for (uint64_t s = 0; s < slices && !result; ++s) {
+      const uint64_t k0 = s * depth;
+      if (!acq.a_ready.empty())
+        if (int rc = rt.device().stream_wait_event(cs, acq.a_ready[s])) {
+          result = rt.device_failure(rc, "gemm", "stream_wait");
+          break;
+        }
+      if (!acq.b_ready.empty())
+        if (int rc = rt.device().stream_wait_event(cs, acq.b_ready[s])) {
+          result = rt.device_failure(rc, "gemm", "stream_wait");
+          break;
+        }
+      // K slice s of a packed panel: whole lines (op-N A: A(i,p) = a[i + p*lda];
+      // op-T B: B(p,j) = b[j + p*ldb]) or a column range of every line.
+      const float* a = reinterpret_cast<const float*>(acq.a->address);
+      const float* b = reinterpret_cast<const float*>(acq.b->address);
+      kernels::SgemmLaunch k;
+      k.a = a + (p.a.transposed ? k0 : k0 * lda);
+      k.b = b + (p.b.transposed ? k0 * ldb : k0);
+      k.c = reinterpret_cast<float*>(acq.c->address);
+      k.lda = lda;
+      k.ldb = ldb;
+      k.ldc = static_cast<int64_t>(packed_ld(cg));
+      k.m = static_cast<int>(g.h);
+      k.n = static_cast<int>(g.g);
+      k.k = static_cast<int>(std::min(depth, g.w - k0));
+      k.alpha = p.alpha;
+      k.beta = (s == 0 && l.first_panel) ? p.beta : 1.f;
+      k.a_kcontig = p.a.transposed;
+      k.b_ncontig = p.b.transposed;
+      k.padded = true;
+      if (l.last_panel && s + 1 == slices && p.has_epilogue()) {
+        if (bias) {
+          const float* v = reinterpret_cast<const float*>(bias->address);
+          if (p.bias_rows) k.bias_row = v + g.i0;
+          else k.bias_col = v + g.j0;
+        }
+        k.relu = p.relu;
+      }
+      // The launch's timing events are recorded by its dispatch; the last
+      // slice's stop event is also the retire event of the three frames (each
+      // marker packet between kernels would otherwise cost the compute stream
+      // a few microseconds).
+      TraceInterval iv;
+      iv.kind = 'k';
+      if (Error e = rt.record_kernel(iv.start, iv.stop)) {
         result = e;
         break;
       }
+      k.start_event = iv.start;
+      k.stop_event = iv.stop;
+      if (int rc = rt.device().launch_sgemm(k, cs)) {
+        result = rt.device_failure(rc, "gemm", "launch_tile");
+        break;
+      }
+      rt.trace_push(iv);
+      done = iv.stop;
     }
     if (result) break;
-    kernels::SgemmLaunch k;
-    k.a = reinterpret_cast<const float*>(acq.a->address);
-    k.b = reinterpret_cast<const float*>(acq.b->address);
-    k.c = reinterpret_cast<float*>(acq.c->address);
-    k.lda = static_cast<int64_t>(packed_ld(ag));
-    k.ldb = static_cast<int64_t>(packed_ld(bg));
-    k.ldc = static_cast<int64_t>(packed_ld(cg));
-    k.m = static_cast<int>(g.h);
-    k.n = static_cast<int>(g.g);
-    k.k = static_cast<int>(g.w);
-    k.alpha = p.alpha;
-    k.beta = l.first_panel ? p.beta : 1.f;
-    k.a_kcontig = p.a.transposed;
-    k.b_ncontig = p.b.transposed;
-    k.padded = true;
-    if (l.last_panel && p.has_epilogue()) {
-      if (bias) {
-        const float* v = reinterpret_cast<const float*>(bias->address);
-        if (p.bias_rows) k.bias_row = v + g.i0;
-        else k.bias_col = v + g.j0;
-      }
-      k.relu = p.relu;
-    }
-    // The launch's timing events are recorded by its dispatch; the stop event
-    // is also the retire event of its three frames (each marker packet between
-    // kernels would otherwise cost the compute stream a few microseconds).
-    TraceInterval iv;
-    iv.kind = 'k';
-    if (Error e = rt.record_kernel(iv.start, iv.stop)) {
-      result = e;
-      break;
-    }
-    k.start_event = iv.start;
-    k.stop_event = iv.stop;
-    if (int rc = rt.device().launch_sgemm(k, cs)) {
-      result = rt.device_failure(rc, "gemm", "launch_tile");
-      break;
-    }
-    rt.trace_push(iv);
-    rt.note_kernel_launched();
-    if (Error e = rt.release_after_event(*acq.a, iv.stop, false)) { result = e; break; }
-    if (Error e = rt.release_after_event(*acq.b, iv.stop, false)) { result = e; break; }
-    if (Error e = rt.release_after_event(*acq.c, iv.stop, true)) { result = e; break; }
+    // Sliced fills: settle the entries' state (their whole-panel ready events
+    // completed no later than the last slices, which the stream already waits for).
+    if (!acq.a_ready.empty())
+      if (Error e = rt.wait_ready(*acq.a, cs)) { result = e; break; }
+    if (!acq.b_ready.empty())
+      if (Error e = rt.wait_ready(*acq.b, cs)) { result = e; break; }
+    rt.note_kernel_launched(); // one tile, however many slices
+    if (Error e = rt.release_after_event(*acq.a, done, false)) { result = e; break; }
+    if (Error e = rt.release_after_event(*acq.b, done, false)) { result = e; break; }
+    if (Error e = rt.release_after_event(*acq.c, done, true)) { result = e; break; }
     if (l.last_panel) {
       if (Error e = rt.writeback_and_evict(*acq.c)) {
         result = e;

@@ -555,7 +555,8 @@ Error Runtime::take_event(Event& out) {
   return {};
 }
 
-Error Runtime::fill_entry(Frame& f, const PanelKey& key, uint64_t packed_pitch, bool needs_data) {
+Error Runtime::fill_entry(Frame& f, const PanelKey& key, uint64_t packed_pitch, bool needs_data,
+                          const std::vector<PanelPiece>* pieces, std::vector<Event>* piece_ready) {
   ++t_.cache_misses;
   f.keyed = true;
   f.key = key;
@@ -583,17 +584,27 @@ Error Runtime::fill_entry(Frame& f, const PanelKey& key, uint64_t packed_pitch, 
   HostAllocation* a = find(key.allocation_id);
   if (!a || key.end() > a->bytes)
     return make_error(XVRAM_STATUS_INTERNAL, "cache", "fill", "entry outside its allocation");
-  TraceInterval iv;
-  iv.kind = 'h';
-  iv.bytes = key.bytes();
-  if (Error e = take_event(iv.start)) return e;
-  if (int rc = device_->event_record(iv.start, h2d_)) return device_failure(rc, "cache", "record");
-  if (int rc = device_->copy_h2d_2d(f.address, packed_pitch, a->host + key.offset, key.pitch,
-                                    key.width, key.height, h2d_))
-    return device_failure(rc, "cache", "copy_h2d");
-  if (Error e = take_event(iv.stop)) return e;
-  if (int rc = device_->event_record(iv.stop, h2d_)) return device_failure(rc, "cache", "record");
-  trace_.push_back(iv);
+  static const std::vector<PanelPiece> kWhole;
+  const std::vector<PanelPiece>& parts = pieces ? *pieces : kWhole;
+  const size_t copies = parts.empty() ? 1 : parts.size();
+  for (size_t i = 0; i < copies; ++i) {
+    PanelPiece pc{0, key.height, 0, key.width};
+    if (!parts.empty()) pc = parts[i];
+    TraceInterval iv;
+    iv.kind = 'h';
+    iv.bytes = pc.lines * pc.bytes;
+    if (Error e = take_event(iv.start)) return e;
+    if (int rc = device_->event_record(iv.start, h2d_)) return device_failure(rc, "cache", "record");
+    if (int rc = device_->copy_h2d_2d(f.address + pc.line0 * packed_pitch + pc.byte0, packed_pitch,
+                                      a->host + key.offset + pc.line0 * key.pitch + pc.byte0,
+                                      key.pitch, pc.bytes, pc.lines, h2d_))
+      return device_failure(rc, "cache", "copy_h2d");
+    if (Error e = take_event(iv.stop)) return e;
+    if (int rc = device_->event_record(iv.stop, h2d_)) return device_failure(rc, "cache", "record");
+    trace_.push_back(iv);
+    // The piece's stop event (an operation-owned event) marks it landed.
+    if (piece_ready) piece_ready->push_back(iv.stop);
+  }
   if (int rc = device_->event_record(f.ready, h2d_)) return device_failure(rc, "cache", "record");
   f.ready_pending = true;
   t_.bytes_h2d += key.bytes();
@@ -657,6 +668,30 @@ Error Runtime::carry_fill(const PanelKey& key, uint64_t packed_pitch, bool& issu
   issued = true;
   // Retired by its own copy: evicting or unmapping the frame waits for the fill.
   return release_after(*f, h2d_, false);
+}
+
+Error Runtime::acquire_pieces(const PanelKey& key, uint64_t packed_pitch,
+                              const std::vector<PanelPiece>& pieces, Frame*& out,
+                              std::vector<Event>& piece_ready) {
+  piece_ready.clear();
+  if (pieces.size() < 2 || index_.count(key)) return acquire(key, packed_pitch, true, out);
+  if (poisoned_) return make_error(XVRAM_STATUS_POISONED, "cache", "acquire", "session is poisoned");
+  if (packed_pitch < key.width || packed_pitch * key.height > frame_bytes_)
+    return make_error(XVRAM_STATUS_INTERNAL, "cache", "acquire", "panel does not fit one frame");
+  uint64_t covered = 0;
+  for (const PanelPiece& pc : pieces) {
+    if (pc.line0 + pc.lines > key.height || pc.byte0 + pc.bytes > key.width)
+      return make_error(XVRAM_STATUS_INTERNAL, "cache", "acquire", "piece outside its panel");
+    covered += pc.lines * pc.bytes;
+  }
+  if (covered != key.bytes())
+    return make_error(XVRAM_STATUS_INTERNAL, "cache", "acquire", "pieces do not tile the panel");
+  Frame* f = nullptr;
+  if (Error e = select_frame(f)) return e;
+  if (Error e = map_frame_at(*f, f->slot)) return e;
+  if (Error e = fill_entry(*f, key, packed_pitch, true, &pieces, &piece_ready)) return e;
+  out = f;
+  return {};
 }
 
 // Orders `stream` after the fill; from then on the entry's bytes are resident

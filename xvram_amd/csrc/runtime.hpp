@@ -89,6 +89,12 @@ struct PanelKey {
   uint64_t bytes() const { return width * height; }
 };
 
+// A share of a panel that one copy fills: lines [line0, line0 + lines) and
+// bytes [byte0, byte0 + bytes) of each of them, relative to the panel.
+struct PanelPiece {
+  uint64_t line0 = 0, lines = 0, byte0 = 0, bytes = 0;
+};
+
 // True when the byte sets of two rectangles of one allocation intersect
 // (exact for rectangles of equal pitch, conservative otherwise).
 bool keys_overlap(const PanelKey& a, const PanelKey& b);
@@ -212,6 +218,14 @@ public:
   // Makes `key` resident in a frame with packed line pitch `packed_pitch` and
   // pins it. needs_data=false (a write-only panel) skips the H2D copy.
   Error acquire(const PanelKey& key, uint64_t packed_pitch, bool needs_data, Frame*& out);
+  // acquire() with data, except that a miss is filled by one copy per piece
+  // (the pieces must tile the panel), recorded in order on the H2D stream;
+  // `piece_ready` receives one event per piece, complete when that piece has
+  // landed, so a consumer of one piece need not wait for the whole panel. A
+  // hit (or fewer than two pieces) leaves `piece_ready` empty: wait_ready().
+  Error acquire_pieces(const PanelKey& key, uint64_t packed_pitch,
+                       const std::vector<PanelPiece>& pieces, Frame*& out,
+                       std::vector<Event>& piece_ready);
   // Orders `stream` after the frame's fill.
   Error wait_ready(Frame& frame, Stream stream);
   // Unpins after the consumer enqueued on `stream`; records the retire event.
@@ -297,7 +311,9 @@ private:
   bool allocation_hot(uint64_t allocation_id);
   bool allocation_streaming(uint64_t allocation_id);
   Error release_frame(Frame& frame);
-  Error fill_entry(Frame& f, const PanelKey& key, uint64_t packed_pitch, bool needs_data);
+  Error fill_entry(Frame& f, const PanelKey& key, uint64_t packed_pitch, bool needs_data,
+                   const std::vector<PanelPiece>* pieces = nullptr,
+                   std::vector<Event>* piece_ready = nullptr);
   Error wait_retired(Frame& frame);
   Error evict_key(Frame& frame, bool was_dirty);
   Error drop_overlapping(const PanelKey& written, const Frame* except);
