@@ -1,6 +1,7 @@
 """The host runtime under ThreadSanitizer and under AddressSanitizer + UBSan
-(the reference runs its no-GPU suite under ASan/UBSan; the session queue is
-where threads meet, so TSan too). tests/sanitize/Makefile links the C-ABI
+(the reference's CI runs its no-GPU suite under Clang ASan + UBSan,
+.github/workflows/ci.yml:420-470; the session queue is where threads meet, so
+TSan too). tests/sanitize/Makefile links the C-ABI
 stress driver (several caller threads on one session: GEMMs with cancels,
 transactions, prefetches, telemetry readers) with the runtime sources and the
 host-memory device simulation; both binaries must finish their checks with no
