@@ -4,14 +4,18 @@
 Default workload (BASELINE.json metric "out-of-core FP32 SGEMM TFLOP/s at 3x
 VRAM budget; H2D GB/s vs link peak"): the north-star GEMM, C = A * B^T with
 M = N = K = 65536 (A, B, C = 3 x 16 GiB of pinned host memory) under a 16 GiB
-VRAM budget (operands = 3x the budget). A "step" is one complete gemm_execute:
-every A/B panel streamed from host RAM, every C tile written back.
+VRAM budget of 512 MiB frames (operands = 3x the budget). A "step" is one
+complete gemm_execute: every A/B panel streamed from host RAM, every C tile
+written back.
 
 Prints one JSON line. ``value`` = 2MNK / wall time per step (inputs resident in
 host memory, as the ABI defines them). ``roofline`` describes the dominant
 kernel (the FP32-MFMA tile kernel): algorithmic FLOPs of its launches divided
-by their summed duration, both from HIP events recorded on the library's
-compute stream around every launch (trace file written by the library).
+by their summed duration, both from the HIP events attached to every kernel
+dispatch on the library's compute stream (trace file written by the library);
+``kernel_ms_per_launch`` is that kernel time per tile launch of the plan (an
+operation's first launch may run as several K-slice kernels). Other workloads:
+``--workload`` (config 3's resident sweep, config 4, the config-5 chain).
 ``cpu_baseline`` times the FP64 reference loop (the oracle's restatement of
 the reference's CPU GEMM) on a bounded sample of the same product on all host
 cores; the same sample checks the GPU result against the per-element bound.
