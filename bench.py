@@ -4,7 +4,7 @@
 Default workload (BASELINE.json metric "out-of-core FP32 SGEMM TFLOP/s at 3x
 VRAM budget; H2D GB/s vs link peak"): the north-star GEMM, C = A * B^T with
 M = N = K = 65536 (A, B, C = 3 x 16 GiB of pinned host memory) under a 16 GiB
-VRAM budget of 512 MiB frames (operands = 3x the budget). A "step" is one
+VRAM budget of 1 GiB frames (operands = 3x the budget). A "step" is one
 complete gemm_execute: every A/B panel streamed from host RAM, every C tile
 written back.
 
@@ -44,10 +44,11 @@ PCIE5_X16_THEORETICAL_GBPS = 63.0  # per direction
 OP_N, OP_T = 0, 1
 WORKLOADS = {
     # name: (m, n, k, op_a, op_b, budget, frame, description)
-    # 512 MiB frames: 8192 x 8192 C tiles with 16384-deep K panels (each C tile
-    # passes through HBM 4 times instead of 8 with 256 MiB frames' 8192-deep
-    # panels); 31 frames still hide the larger A/B re-streaming under compute.
-    "ns65536_nt_16g": (65536, 65536, 65536, OP_N, OP_T, 16 * GiB, 512 * MiB,
+    # 1 GiB frames: 8192 x 8192 C tiles with 32768-deep K panels (each C tile
+    # passes through HBM twice, against 4 times with 512 MiB frames' 16384-deep
+    # panels and 8 with 256 MiB frames); the 15 frames still hide the larger
+    # A/B re-streaming (about 126 GB of H2D per step) under compute.
+    "ns65536_nt_16g": (65536, 65536, 65536, OP_N, OP_T, 16 * GiB, 1024 * MiB,
                        "FP32 SGEMM N/T 65536^3, 3 x 16 GiB operands in pinned host RAM, "
                        "16 GiB VRAM budget (3x)"),
     "c4_32768_nt_2g": (32768, 32768, 32768, OP_N, OP_T, 2 * GiB, 64 * MiB,

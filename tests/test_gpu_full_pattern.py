@@ -51,7 +51,7 @@ def fill(alloc, filler, rows, cols, transposed, chunk_bytes=GiB):
         alloc.write(view, offset=c0 * rows * 4)
 
 
-@pytest.mark.parametrize("size,budget,frame", [(65536, 16 * GiB, 512 * MiB),
+@pytest.mark.parametrize("size,budget,frame", [(65536, 16 * GiB, 1024 * MiB),
                                                (32768, 2 * GiB, 64 * MiB)],
                          ids=["ns65536_nt_16g", "c4_32768_nt_2g"])
 def test_every_element_of_the_pattern_product(synth, oracle_mod, size, budget, frame):

@@ -7,6 +7,13 @@ tiles, the K tail after its three-stage unrolled loop, alpha/beta, the fused
 bias/ReLU epilogue, and one out-of-core case whose 4096 x 4096 C tiles
 accumulate over several K panels.
 
+N/T launches whose tiles are all interior (m, n multiples of 256) and whose K
+is a multiple of 4 run the barrier-free variant (sgemm_ring_kernel: each wave
+streams its own operand halves through a private LDS ring); the N/T cases
+above with such shapes (interior, bit-exact pattern, beta = 0 over NaN,
+out-of-core panels) run it, and the ring cases below add K tails around its
+8-pair unrolled loop and 7-pair prefetch distance, alpha/beta and the epilogue.
+
 Random cases are checked element by element against the FP64 oracle on three
 column ranges (first, middle and last tile columns, every row) with the bound
 |C - C_ref| <= 4*K*2^-24*(|alpha|(|A||B|)_ij + |beta*C0_ij|); the analytic
@@ -103,9 +110,32 @@ def test_wide_beta_zero_over_nan(resident, oracle_mod):
     sampled_check(oracle_mod, prob, out, "wide beta=0 over NaN C")
 
 
+@pytest.mark.parametrize("k", [4, 28, 32, 36, 60, 64, 1036])
+def test_ring_k_tails_pattern(resident, oracle_mod, k):
+    """Barrier-free N/T kernel, bit-exact pattern: fewer pairs than the
+    prefetch distance (k = 4, 28), exactly one unrolled block plus tail
+    (32 .. 64) and a long loop with a 3-pair tail (1036)."""
+    m, n = 4096, 4096
+    a_op, b_op = pattern_operands(m, n, k)
+    prob = Problem(a_op, b_op, op_b=abi.OP_T)
+    out = prob.run(resident)
+    assert prob.plan_info.tile_count == 1
+    expected = oracle_mod.pattern_expected_matrix(m, n, k)
+    assert np.array_equal(out.astype(np.float64), expected)
+
+
+def test_ring_alpha_beta(resident, oracle_mod):
+    m, n, k = 4608, 4096, 1000
+    prob = Problem(uniform(oracle_mod, m, k, 1601), uniform(oracle_mod, k, n, 1602),
+                   uniform(oracle_mod, m, n, 1603), op_b=abi.OP_T, alpha=-1.25, beta=0.75)
+    out = prob.run(resident)
+    sampled_check(oracle_mod, prob, out, "ring alpha/beta")
+
+
+@pytest.mark.parametrize("n", [4200, 4096], ids=["wide", "ring"])
 @pytest.mark.parametrize("axis", [abi.BIAS_PER_ROW, abi.BIAS_PER_COLUMN], ids=["row", "col"])
-def test_wide_epilogue(lib, oracle_mod, axis):
-    m, n, k = 4096, 4200, 800
+def test_wide_epilogue(lib, oracle_mod, axis, n):
+    m, k = 4096, 800
     a = uniform(oracle_mod, m, k, 1401)
     b = uniform(oracle_mod, k, n, 1402)
     c0 = uniform(oracle_mod, m, n, 1403)

@@ -109,9 +109,9 @@ def sim():
 F = 16 * KiB
 
 
-def budget_session(lib, policy=abi.CACHE_POLICY_CLOCK, headroom=0):
+def budget_session(lib, policy=abi.CACHE_POLICY_CLOCK, headroom=0, poll_ms=1):
     return xv.Session(lib, chunk_size_bytes=F, cache_target_bytes=0, workspace_cap_bytes=0,
-                      device_headroom_bytes=headroom, budget_poll_ms=1, cache_policy=policy)
+                      device_headroom_bytes=headroom, budget_poll_ms=poll_ms, cache_policy=policy)
 
 
 def touch_all(s, alloc, size, mode=abi.ACCESS_READ_WRITE, value=None):
@@ -174,7 +174,9 @@ def test_grow_needs_ten_samples_and_two_frames(sim):
 
 def test_out_of_memory_frame_allocation_retries_once(sim):
     sim.dll.xvram_hostsim_set_memory(16 * F, 16 * F)
-    with budget_session(sim) as s:
+    # A 1 s poll interval keeps the target stale through the transaction below
+    # however slowly the host runs (with 1 ms a delay could resample first).
+    with budget_session(sim, poll_ms=1000) as s:
         a = s.allocation(3 * F)
         sim.dll.xvram_hostsim_set_memory(2 * F, 16 * F)  # only two frames can still be created
         # Within the poll interval the target is stale; the third frame's

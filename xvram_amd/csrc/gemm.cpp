@@ -328,8 +328,13 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   };
   const bool over_cap = max_launch_flops != 0 &&
                         launch_flops(p.m, p.n, p.k) > static_cast<double>(max_launch_flops);
+  // The 256 x 256 tile kernels address an A or B panel with 32-bit buffer
+  // offsets (sgemm_wide.hip), so those panels stay below 2^31 bytes; a larger
+  // one would fall back to the slower 256 x 128 kernel.
+  constexpr uint64_t kPanelLimit = uint64_t(1) << 31;
   if (!hinted && !over_cap && a_panel_bytes(p, p.m, p.k) <= F && b_panel_bytes(p, p.k, p.n) <= F &&
-      c_panel_bytes(p.m, p.n) <= F) {
+      c_panel_bytes(p.m, p.n) <= F && a_panel_bytes(p, p.m, p.k) < kPanelLimit &&
+      b_panel_bytes(p, p.k, p.n) < kPanelLimit) {
     tm = p.m;
     tn = p.n;
     bk = p.k;
@@ -339,8 +344,13 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
     // 65536 extent, as 11520 would leave), and the growth step below then
     // spends the rest of the frame on a deeper K panel (fewer launches, and
     // fewer passes of each C tile through HBM).
+    // An 8192 x 8192 C tile is already 1024 workgroups of the 256 x 256
+    // kernel (four per CU): a wider start adds nothing to the kernel, so larger
+    // frames go to K instead (below).
+    constexpr uint64_t kMaxSquare = 8192;
     uint64_t s = 16;
     while ((s * 2) * (s * 2) <= F / 4) s *= 2;
+    s = std::min(s, kMaxSquare);
     tm = std::min(p.m, s);
     tn = std::min(p.n, s);
     bk = std::min(p.k, s);
@@ -351,7 +361,8 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
     if (hn) tn = std::min(p.n, hn);
     if (spec.tile_k_hint) bk = std::min(p.k, spec.tile_k_hint);
     const auto fits = [&](uint64_t a, uint64_t b, uint64_t c) {
-      return a_panel_bytes(p, a, c) <= F && b_panel_bytes(p, c, b) <= F && c_panel_bytes(a, b) <= F;
+      return a_panel_bytes(p, a, c) <= F && b_panel_bytes(p, c, b) <= F && c_panel_bytes(a, b) <= F &&
+             a_panel_bytes(p, a, c) < kPanelLimit && b_panel_bytes(p, c, b) < kPanelLimit;
     };
     // Shrink the largest extent until every panel fits a frame.
     while (!fits(tm, tn, bk)) {
@@ -364,8 +375,11 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
       }
       *largest = std::max<uint64_t>(16, *largest / 2 / 16 * 16);
     }
-    // Grow extents the problem did not clamp while the panels still fit.
+    // Grow extents the problem did not clamp while the panels still fit: K
+    // first (each doubling halves the passes of a C tile through HBM and the
+    // launches' fixed costs), then the tile extents.
     if (!hinted) {
+      while (bk < p.k && fits(tm, tn, std::min(p.k, bk * 2))) bk = std::min(p.k, bk * 2);
       bool grew = true;
       while (grew) {
         grew = false;

@@ -32,7 +32,10 @@
 //
 // The host uses this kernel only when every operand panel spans less than
 // 2^31 bytes from a tile's base (32-bit buffer offsets) and the launch has at
-// least one tile per CU.
+// least one tile per CU. N/T launches whose tiles are all interior and whose K
+// is a multiple of 4 run sgemm_ring_kernel instead (below): the same tile and
+// MFMA sequence with each wave streaming its own operand halves through a
+// private LDS ring, so its K loop needs no workgroup barrier.
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
@@ -125,7 +128,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t panel_rsrc(const float* base, 
 
 // One wave-wide direct load: lane l's 16 bytes at rsrc.base + soff + voff land
 // at LDS byte address lds_base + kOff + 16*l (lds_base wave-uniform). Counted
-// by vmcnt only: the caller waits before the barrier that publishes the data.
+// by vmcnt only: the caller waits on vmcnt before the data is read (and, when
+// other waves read it, before the barrier that publishes it).
 template <int kOff>
 __device__ __forceinline__ void load_lds16(uint32_t lds_base, uint32_t voff,
                                            __amdgpu_buffer_rsrc_t rsrc, uint32_t soff) {
@@ -348,17 +352,179 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_wide_kernel(Params p) {
   store_c_tile<4>(p, acc, m0 + wm, n0 + wn, lrow, lhalf);
 }
 
+// ---- barrier-free N/T kernel ------------------------------------------------
+//
+// When both operands are extent-contiguous (A op N, B op T) every operand load
+// can go straight into LDS, and each wave can stream the two 128-wide halves it
+// multiplies (its A rows and its B columns) into an LDS ring of its own: no
+// data is shared between waves, so the K loop has no workgroup barrier at all,
+// only per-wave waits on the wave's own loads. Each half is loaded by the two
+// waves that use it (L2 serves the second read; L2 -> LDS traffic doubles, HBM
+// traffic does not change). The MFMA sequence per accumulator is the one of
+// sgemm_wide_kernel<false, true>, so both produce bit-identical C.
+//
+// Per wave, a ring of kRing slots; slot s holds one k-pair (4 k-rows) of the
+// wave's A half (4 x 128 floats) followed by its B half (4 x 128). Step q
+// multiplies pair q from registers, reads pair q+1's fragments from LDS and
+// issues pair q+kAhead's four loads (two per operand, each a wave-wide
+// buffer_load_dwordx4 ... lds of two 128-float k-rows) into the slot pair q-1
+// vacated: pair q-1's fragments were consumed by step q-1's MFMAs, so its reads
+// have completed. Loads complete in order, so before reading pair q+1 the wave
+// waits until at most the loads of pairs q+2 .. q+kAhead-1 are outstanding.
+//
+// Used only for launches whose tiles are all interior (m and n multiples of
+// 256) and whose K is a multiple of 4: every load then stays inside the tile's
+// rows and columns and inside the K extent (the last load of the last pair ends
+// exactly at the panel's record count), so no predication is needed.
+constexpr int kRing = 8;   // slots (k-pairs) per wave
+constexpr int kAhead = 7;  // prefetch distance in k-pairs
+constexpr int kSlot = 1024; // floats per slot: A 4 x 128, then B 4 x 128
+static_assert(kAhead == kRing - 1, "loads reuse the slot vacated one step earlier");
+static_assert(4 * kAhead <= 63, "outstanding loads fit the vmcnt counter");
+static_assert(4 * (kAhead - 2) == 20, "steady-state wait below");
+
+__global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) float lds[4 * kRing * kSlot];
+  asm volatile("; accumulators in AGPRs" ::: "a0");
+
+  int tile_m, tile_n;
+  tile_coords<kGroupM>(p, tile_m, tile_n);
+  const int m0 = tile_m * kTile;
+  const int n0 = tile_n * kTile;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = (wave & 1) * kWave;
+  const int wn = (wave >> 1) * kWave;
+  const int lrow = lane & 31;
+  const int lhalf = lane >> 5;
+
+  float16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int pairs = p.k / 4;
+  // A(i, k) sits at byte 4*(k*lda + i-m0) from a + m0, B(k, j) at
+  // 4*(k*ldb + j-n0) from b + n0.
+  const __amdgpu_buffer_rsrc_t rs_a =
+      panel_rsrc(p.a + m0, (uint32_t)(((int64_t)p.k * p.lda - m0) * 4));
+  const __amdgpu_buffer_rsrc_t rs_b =
+      panel_rsrc(p.b + n0, (uint32_t)(((int64_t)p.k * p.ldb - n0) * 4));
+  // Load h of a pair: lane l brings k-row 2h + l/32 of the pair, elements
+  // 4*(l%32) .. +3 of the wave's half; it lands at LDS byte 1024*h + 16*l of
+  // the operand's part of the slot, i.e. row-major 4 x 128.
+  uint32_t vo_a[2], vo_b[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    vo_a[h] = (uint32_t)(((int64_t)(2 * h + lhalf) * p.lda + wm + 4 * lrow) * 4);
+    vo_b[h] = (uint32_t)(((int64_t)(2 * h + lhalf) * p.ldb + wn + 4 * lrow) * 4);
+  }
+  const uint32_t pair_a = (uint32_t)(16 * p.lda);
+  const uint32_t pair_b = (uint32_t)(16 * p.ldb);
+  float* ring = lds + wave * (kRing * kSlot);
+  const uint32_t ring_lds = lds_byte_addr(ring);
+
+  // Load L (0, 1: A halves; 2, 3: B halves) of pair q into slot S.
+  auto issue = [&]<int S, int L>(int q, Int<S>, Int<L>) {
+    constexpr int off = (S * kSlot + (L >> 1) * 512 + (L & 1) * 256) * 4;
+    if constexpr (L < 2) {
+      const uint32_t so = __builtin_amdgcn_readfirstlane(pair_a * (uint32_t)q);
+      load_lds16<off>(ring_lds, vo_a[L & 1], rs_a, so);
+    } else {
+      const uint32_t so = __builtin_amdgcn_readfirstlane(pair_b * (uint32_t)q);
+      load_lds16<off>(ring_lds, vo_b[L & 1], rs_b, so);
+    }
+  };
+  // Fragments of one pair: rows 2t + lhalf, four consecutive floats at 4*lrow
+  // (the same element map as sgemm_wide_kernel's read_pair).
+  float4 fa[2][2], fb[2][2];
+  auto read_frag = [&]<int S, int R>(Int<S>, Int<R>) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const float* row = ring + S * kSlot + (2 * t + lhalf) * kWave + 4 * lrow;
+      fa[R][t] = *reinterpret_cast<const float4*>(row);
+      fb[R][t] = *reinterpret_cast<const float4*>(row + 512);
+    }
+  };
+  auto mfma_one = [&]<int R, int X>(Int<R>, Int<X>) {
+    constexpr int t = X / 16, i = (X % 16) / 4, j = X % 4;
+    const float4 a = fa[R][t], b = fb[R][t];
+    const float ao = i == 0 ? a.x : i == 1 ? a.y : i == 2 ? a.z : a.w;
+    const float bo = j == 0 ? b.x : j == 1 ? b.y : j == 2 ? b.z : b.w;
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(ao, bo, acc[i][j], 0, 0, 0);
+  };
+
+  // Pairs 0 .. kAhead-1 in flight, then pair 0's fragments in registers.
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    ((I < pairs ? (issue(I, Int<I % kRing>{}, Int<0>{}), issue(I, Int<I % kRing>{}, Int<1>{}),
+                   issue(I, Int<I % kRing>{}, Int<2>{}), issue(I, Int<I % kRing>{}, Int<3>{}), 0)
+                : 0),
+     ...);
+  }(std::make_integer_sequence<int, kAhead>{});
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  read_frag(Int<0>{}, Int<0>{});
+
+  // Step q, q % kRing == J. kTail: the last steps, which may issue no loads
+  // (and so wait for all outstanding ones) and may have no next pair.
+  auto step = [&]<int J, bool kTail>(int q, Int<J>, std::bool_constant<kTail>) {
+    constexpr int cur = J & 1, nxt = (J + 1) & 1;
+    constexpr int s_next = (J + 1) % kRing, s_load = (J + kAhead) % kRing;
+    if constexpr (!kTail) asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (!kTail || q + 1 < pairs) read_frag(Int<s_next>{}, Int<nxt>{});
+    __builtin_amdgcn_sched_barrier(0);
+    const bool load = !kTail || q + kAhead < pairs;
+    [&]<int... X>(std::integer_sequence<int, X...>) {
+      (([&] {
+         if constexpr (X % 8 == 0) {
+           if (load) {
+             __builtin_amdgcn_sched_barrier(0);
+             issue(q + kAhead, Int<s_load>{}, Int<X / 8>{});
+             __builtin_amdgcn_sched_barrier(0);
+           }
+         }
+         mfma_one(Int<cur>{}, Int<X>{});
+       }()),
+       ...);
+    }(std::make_integer_sequence<int, 32>{});
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  int q = 0;
+  // Full blocks of kRing steps whose loads all exist (q + kRing - 1 + kAhead < pairs).
+  for (; q + kRing + kAhead <= pairs; q += kRing) {
+    [&]<int... J>(std::integer_sequence<int, J...>) {
+      (step(q + J, Int<J>{}, std::false_type{}), ...);
+    }(std::make_integer_sequence<int, kRing>{});
+  }
+  for (; q < pairs; q += kRing) {
+    [&]<int... J>(std::integer_sequence<int, J...>) {
+      ((q + J < pairs ? (step(q + J, Int<J>{}, std::true_type{}), 0) : 0), ...);
+    }(std::make_integer_sequence<int, kRing>{});
+  }
+
+  store_c_tile<4>(p, acc, m0 + wm, n0 + wn, lrow, lhalf);
+}
+
 } // namespace
 
 int wide_tile() { return kTile; }
 
-// Launches the 256 x 256 kernel for `p` (tiles_m / tiles_n already in 256s);
-// start / stop (optional) are recorded by the dispatch itself.
+// Launches a 256 x 256 kernel for `p` (tiles_m / tiles_n already in 256s):
+// the barrier-free one for N/T launches of interior tiles only and K a
+// multiple of 4, else sgemm_wide_kernel. start / stop (optional) are recorded
+// by the dispatch itself.
 hipError_t launch_wide(const Params& p, bool a_kcontig, bool b_ncontig, hipStream_t stream,
                        hipEvent_t start, hipEvent_t stop) {
   const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
   const dim3 block(kThreads);
-  if (!a_kcontig && !b_ncontig)
+  if (!a_kcontig && b_ncontig && p.m % kTile == 0 && p.n % kTile == 0 && p.k % 4 == 0)
+    hipExtLaunchKernelGGL(sgemm_ring_kernel, grid, block, 0, stream, start, stop, 0, p);
+  else if (!a_kcontig && !b_ncontig)
     hipExtLaunchKernelGGL((sgemm_wide_kernel<false, false>), grid, block, 0, stream, start, stop, 0, p);
   else if (!a_kcontig && b_ncontig)
     hipExtLaunchKernelGGL((sgemm_wide_kernel<false, true>), grid, block, 0, stream, start, stop, 0, p);
