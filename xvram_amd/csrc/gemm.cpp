@@ -495,7 +495,7 @@ struct Acquired {
 };
 
 // The first launch of an operation waits for its whole A and B panels before
-// any compute can start (18.8 ms for 2 x 512 MiB at 57 GB/s). When they are
+// any compute can start (37.7 ms for two 1 GiB panels at 57 GB/s). When they are
 // cache misses, each is filled by copies of K slices of at least this depth
 // (at most kFirstSlices of them) and the launch runs as one kernel per slice,
 // each waiting only for its own slices of A and B: compute starts after the
