@@ -1,6 +1,6 @@
 // sgemm_device.hpp — device-side pieces shared by the tile kernels
 // (sgemm_mfma.hip: 256 x 128 tiles, two workgroups per CU; sgemm_wide.hip:
-// 256 x 256 tiles, one workgroup per CU). Compiled only by hipcc.
+// two kernels of 256 x 256 tiles, one workgroup per CU). Compiled only by hipcc.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -277,10 +277,11 @@ hipError_t launch_variant(const Params& p, hipStream_t stream, hipEvent_t start,
 } // namespace
 
 // A launch with at least this many 256 x 256 tiles (one per CU of the chip)
-// runs the 256 x 256 kernel; smaller ones keep two 256 x 128 tiles per CU.
+// runs a 256 x 256 kernel (sgemm_wide.hip picks the barrier-free one for N/T
+// launches of interior tiles); smaller ones keep two 256 x 128 tiles per CU.
 constexpr int64_t kWideMinTiles = 256;
 
-// The 256 x 256 kernel addresses each operand panel with 32-bit buffer
+// The 256 x 256 kernels address each operand panel with 32-bit buffer
 // offsets, so every panel must span less than 2^31 bytes.
 bool wide_fits(const SgemmLaunch& l) {
   constexpr int64_t kLimit = int64_t(1) << 31;
