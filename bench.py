@@ -544,10 +544,15 @@ def main() -> int:
                          f"(FP64 accumulation over FP32 inputs, {cpu_s:.1f} s on {threads} threads)"}
 
     # HBM traffic per launch from the committed rocprofv3 --pmc summary of this
-    # workload's tile kernel (profiles/traffic_<kernel>_<workload>.txt), if any.
+    # workload's tile kernel (profiles/traffic_<kernel>_<workload>.txt), if any;
+    # that summary describes the workload's own launch shape, so a run with a
+    # different frame size or tile hints reports none.
     traffic = None
+    overridden = bool(args.frame_mib) or any(int(v) for v in args.tile_hints.split(","))
     for traffic_file in sorted(glob.glob(os.path.join(ROOT, "profiles",
                                                       f"traffic_*_{args.workload}.txt"))):
+        if overridden:
+            break
         for line in open(traffic_file):
             if line.startswith("traffic_bytes_per_launch:"):
                 traffic = int(float(line.split(":", 1)[1]))
