@@ -124,6 +124,20 @@ def test_ring_k_tails_pattern(resident, oracle_mod, k):
     assert np.array_equal(out.astype(np.float64), expected)
 
 
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 1001), (4100, 4096, 1040), (4096, 4352 + 8, 1040)],
+                         ids=["k%4", "m%256", "n%256"])
+def test_ring_fallback_shapes_pattern(resident, oracle_mod, m, n, k):
+    """N/T launches just outside the barrier-free kernel's conditions (K not a
+    multiple of 4, or m or n not a multiple of 256) run sgemm_wide_kernel:
+    bit-exact pattern."""
+    a_op, b_op = pattern_operands(m, n, k)
+    prob = Problem(a_op, b_op, op_b=abi.OP_T)
+    out = prob.run(resident)
+    assert prob.plan_info.tile_count == 1
+    expected = oracle_mod.pattern_expected_matrix(m, n, k)
+    assert np.array_equal(out.astype(np.float64), expected)
+
+
 def test_ring_alpha_beta(resident, oracle_mod):
     m, n, k = 4608, 4096, 1000
     prob = Problem(uniform(oracle_mod, m, k, 1601), uniform(oracle_mod, k, n, 1602),
