@@ -205,3 +205,20 @@ def test_wide_out_of_core_panels(lib, oracle_mod):
         assert t.clean_evictions + t.dirty_evictions > 0
         assert t.resident_bytes_peak <= t.cache_target_bytes
     sampled_check(oracle_mod, prob, out, "wide out-of-core 8192x8192x6000")
+
+
+def test_mixed_kernels_out_of_core_pattern(lib, oracle_mod):
+    """8192 x 8192 x 6002 N/T on 64 MiB frames: 4096 x 4096 C tiles over a
+    4096-deep K panel (barrier-free kernel) and a 1906-deep one (K not a
+    multiple of 4: sgemm_wide_kernel), accumulated through C between launches
+    (and the first launch sliced): bit-exact pattern."""
+    m, n, k = 8192, 8192, 6002
+    a_op, b_op = pattern_operands(m, n, k)
+    prob = Problem(a_op, b_op, op_b=abi.OP_T)
+    with xv.Session(lib, chunk_size_bytes=64 * MiB, cache_target_bytes=12 * 64 * MiB,
+                    workspace_cap_bytes=0, device_headroom_bytes=0) as s:
+        out = prob.run(s)
+        info = prob.plan_info
+    assert (info.tile_m, info.tile_n, info.tile_k) == (4096, 4096, 4096) and info.tile_count == 8
+    expected = oracle_mod.pattern_expected_matrix(m, n, k)
+    assert np.array_equal(out.astype(np.float64), expected)
