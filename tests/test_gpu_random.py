@@ -5,8 +5,9 @@ Each case draws m, n, k, the N/T forms, the storage layout of A, B and C
 beta, and a cache configuration: resident (whole operands in one frame) or
 out of core (small frames, so the planner tiles C and splits K and the panels
 stream through a few frames). A quarter of the cases are large enough that
-their launches run the 256 x 256 kernel; the rest run the 256 x 128 kernel,
-many with ragged edges in every dimension. With beta = 0, C is filled with NaN
+their launches run a 256 x 256 kernel; the rest run the 256 x 128 kernel,
+many with ragged edges in every dimension. Six more cases are N/T with m and n
+multiples of 256, so their large launches run the barrier-free N/T kernel. With beta = 0, C is filled with NaN
 first (it must never be read).
 
 Every element is compared with the FP64 oracle (the reference's CPU GEMM,
@@ -56,7 +57,24 @@ def make_cases(count=24, seed=2026):
     return cases
 
 
-CASES = make_cases()
+def make_ring_cases(count=6, seed=2027):
+    """N/T with column-major storage, m and n multiples of 256 from 4096 and K a
+    multiple of 4: the 4096 x 4096 (and resident) launches run the barrier-free
+    kernel, the narrower edge launches of the out-of-core cases the others."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(count):
+        resident = i % 2 == 0
+        cases.append(dict(
+            m=256 * int(rng.integers(16, 21)), n=256 * int(rng.integers(16, 21)),
+            k=4 * int(rng.integers(1, 300)), ops=(abi.OP_N, abi.OP_T), layouts=(1, 1, 1),
+            ld_pad=tuple(int(v) for v in rng.integers(0, 8, 3)),
+            alpha=float(rng.choice([1.0, -0.75, 2.5])), beta=float(rng.choice([0.0, 1.0, 0.5])),
+            cache=(0, 0) if resident else (64, 12), seed=5000 + 3 * i))
+    return cases
+
+
+CASES = make_cases() + make_ring_cases()
 
 
 def case_id(c):
