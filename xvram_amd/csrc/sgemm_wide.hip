@@ -375,7 +375,7 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_wide_kernel(Params p) {
 // Used only for launches whose tiles are all interior (m and n multiples of
 // 256) and whose K is a multiple of 4: every load then stays inside the tile's
 // rows and columns and inside the K extent (the last load of the last pair ends
-// exactly at the panel's record count), so no predication is needed.
+// at or before the panel's record count), so no predication is needed.
 constexpr int kRing = 8;   // slots (k-pairs) per wave
 constexpr int kAhead = 7;  // prefetch distance in k-pairs
 constexpr int kSlot = 1024; // floats per slot: A 4 x 128, then B 4 x 128
