@@ -458,14 +458,17 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(ao, bo, acc[i][j], 0, 0, 0);
   };
 
-  // Pairs 0 .. kAhead-1 in flight, then pair 0's fragments in registers.
+  // Pairs 0 .. kAhead-1 in flight, then pair 0's fragments in registers: with
+  // all kAhead pairs issued, only pair 0's four loads need to have landed.
   [&]<int... I>(std::integer_sequence<int, I...>) {
     ((I < pairs ? (issue(I, Int<I % kRing>{}, Int<0>{}), issue(I, Int<I % kRing>{}, Int<1>{}),
                    issue(I, Int<I % kRing>{}, Int<2>{}), issue(I, Int<I % kRing>{}, Int<3>{}), 0)
                 : 0),
      ...);
   }(std::make_integer_sequence<int, kAhead>{});
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  static_assert(4 * (kAhead - 1) == 24, "prologue wait below");
+  if (pairs >= kAhead) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   read_frag(Int<0>{}, Int<0>{});
 
   // Step q, q % kRing == J. kTail: the last steps, which may issue no loads
