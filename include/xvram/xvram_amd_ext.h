@@ -1,9 +1,19 @@
 /*
  * xvram_amd extension table — additions of the MI355X build that have no
  * counterpart in the reference ABI. A caller of the reference interface never
- * needs this header; everything here is reached through one extra export,
- * xvram_amd_get_ext, and works on the same session/allocation/plan handles as
- * include/xvram/xvram.h.
+ * needs this header. The library still exports exactly one symbol,
+ * xvram_get_api@@XVRAM_0.1 (reference include/xvram/xvram.h:532-533,
+ * cmake/xvram.exports.map); the extension table is requested through it with
+ * the private version number XVRAM_AMD_EXT_ABI_VERSION_1, which lies outside
+ * the reference's sequential ABI versions (1, 2, ...):
+ *
+ *     xvram_amd_ext_v1 ext;
+ *     xvram_get_api(XVRAM_AMD_EXT_ABI_VERSION_1, sizeof(ext), &ext);
+ *
+ * Argument rules are those of the v1/v2 tables: NULL or a buffer smaller than
+ * xvram_amd_ext_v1 -> XVRAM_STATUS_INVALID_ARGUMENT; every other unknown
+ * version still returns XVRAM_STATUS_INCOMPATIBLE_ABI. The functions work on
+ * the same session/allocation/plan handles as include/xvram/xvram.h.
  *
  * Version 1: GEMM plans with a fused epilogue,
  *
@@ -29,6 +39,10 @@
 extern "C" {
 #endif
 
+/* The version passed to xvram_get_api for the extension table ('X','A' in the
+   top bytes keeps it clear of the reference's small ABI numbers). */
+#define XVRAM_AMD_EXT_ABI_VERSION_1 UINT32_C(0x58410001)
+/* Value of xvram_amd_ext_v1.ext_version. */
 #define XVRAM_AMD_EXT_VERSION_1 UINT32_C(1)
 
 typedef uint32_t xvram_amd_bias_axis;
@@ -85,9 +99,6 @@ typedef struct xvram_amd_ext_v1 {
   xvram_status(XVRAM_CALL* device_get_info)(int32_t ordinal, xvram_amd_device_info_v1* out);
   uint64_t reserved[3];
 } xvram_amd_ext_v1;
-
-XVRAM_API xvram_status XVRAM_CALL xvram_amd_get_ext(uint32_t requested_version,
-                                                    uint32_t caller_size, void* out_ext);
 
 #ifdef __cplusplus
 }

@@ -95,17 +95,98 @@ def test_ctypes_mirror_matches_header(header_layout):
         assert getattr(CTYPES[s], f).offset == off, (s, f)
 
 
-@pytest.mark.parametrize("path", [xv.PRODUCT_LIB, xv.HOSTSIM_LIB])
-def test_exports(path):
-    out = subprocess.run(["nm", "-D", "--defined-only", path], check=True, capture_output=True,
+def _elf_exports(path):
+    """Defined dynamic symbols as the reference's export contract reads them
+    (tests/contract/sdk_export_contract.py:66-99): `nm -D --defined-only
+    --format=posix`; an absolute symbol named like a version node is that
+    node, every other line is an export, `sym@@NODE` carries its version."""
+    out = subprocess.run(["nm", "-D", "--defined-only", "--format=posix", path], check=True,
+                         capture_output=True, text=True).stdout
+    exports, nodes, versions = set(), set(), {}
+    for line in out.splitlines():
+        fields = line.split()
+        if len(fields) < 2:
+            continue
+        raw, kind = fields[0], fields[1].upper()
+        if kind == "A" and "@" not in raw:
+            nodes.add(raw)
+            continue
+        symbol, sep, version = raw.partition("@")
+        exports.add(symbol)
+        if sep:
+            versions[symbol] = version.lstrip("@")
+    return exports, nodes, versions
+
+
+def _version_definitions(path):
+    """Non-base ELF version definitions (.gnu.version_d). Newer GNU ld no
+    longer emits the absolute version-node symbol that older nm output lists,
+    so the node's presence is read from the section itself."""
+    out = subprocess.run(["readelf", "-V", "-W", path], check=True, capture_output=True,
                          text=True).stdout
-    symbols = sorted(line.split()[-1] for line in out.splitlines() if " T " in line)
-    if path == xv.PRODUCT_LIB:
-        # The reference's one export, versioned like its export map, plus this
-        # build's extension table in a version node of its own.
-        assert symbols == ["xvram_amd_get_ext@@XVRAM_AMD_EXT_1", "xvram_get_api@@XVRAM_0.1"]
-    else:
-        assert "xvram_get_api@@XVRAM_0.1" in symbols
+    nodes = set()
+    in_defs = False
+    for line in out.splitlines():
+        if line.startswith("Version definition section"):
+            in_defs = True
+            continue
+        if in_defs and line.startswith("Version "):
+            break
+        if in_defs and "Name:" in line and "Flags: BASE" not in line:
+            nodes.add(line.split("Name:")[1].split()[0])
+    return nodes
+
+
+def test_product_exports_exactly_the_reference_symbol():
+    """The reference's contract (sdk_export_contract.py:13-14,106-125): the
+    export set is exactly {xvram_get_api}, at ELF version XVRAM_0.1, and the
+    XVRAM_0.1 node exists. The extension table adds no symbol."""
+    exports, nodes, versions = _elf_exports(xv.PRODUCT_LIB)
+    assert exports == {"xvram_get_api"}
+    assert nodes <= {"XVRAM_0.1"}
+    assert _version_definitions(xv.PRODUCT_LIB) == {"XVRAM_0.1"}
+    assert versions == {"xvram_get_api": "XVRAM_0.1"}
+
+
+def test_hostsim_exports_the_same_entry_point():
+    exports, nodes, versions = _elf_exports(xv.HOSTSIM_LIB)
+    assert versions["xvram_get_api"] == "XVRAM_0.1"
+    # Only the simulation's own test hooks besides the entry point.
+    assert all(s == "xvram_get_api" or s.startswith("xvram_hostsim_") for s in exports)
+
+
+@pytest.mark.parametrize("path", [xv.PRODUCT_LIB, xv.HOSTSIM_LIB])
+def test_extension_table_through_get_api(path):
+    """The extension table is one more version of xvram_get_api, with the
+    v1 table's argument rules; other unknown versions stay incompatible."""
+    lib = xv.Library(path)
+    ext = abi.ExtV1()
+    size = ctypes.sizeof(ext)
+    assert lib.get_api(abi.EXT_ABI_VERSION_1, size, ctypes.byref(ext)) == abi.SUCCESS
+    assert ext.struct_size == size and ext.ext_version == abi.EXT_VERSION_1
+    assert ctypes.cast(ext.gemm_plan_create_epilogue, ctypes.c_void_p).value
+    assert ctypes.cast(ext.device_get_info, ctypes.c_void_p).value
+    assert list(ext.reserved) == [0, 0, 0]
+    assert lib.get_api(abi.EXT_ABI_VERSION_1, size - 1, ctypes.byref(ext)) == abi.INVALID_ARGUMENT
+    assert lib.get_api(abi.EXT_ABI_VERSION_1, size, None) == abi.INVALID_ARGUMENT
+    for version in (abi.EXT_ABI_VERSION_1 + 1, abi.EXT_ABI_VERSION_1 - 1, 0x58410000, 1 << 31):
+        assert lib.get_api(version, 4096, (ctypes.c_uint8 * 4096)()) == abi.INCOMPATIBLE_ABI
+
+
+def test_export_parser_rejects_extra_symbols():
+    """The parser above must see what the reference contract rejects."""
+    import types
+    fake = ("XVRAM_0.1 A 0\nXVRAM_AMD_EXT_1 A 0\nxvram_get_api@@XVRAM_0.1 T 100\n"
+            "xvram_amd_get_ext@@XVRAM_AMD_EXT_1 T 200\n")
+    real_run = subprocess.run
+    try:
+        subprocess.run = lambda *a, **k: types.SimpleNamespace(stdout=fake)
+        exports, nodes, versions = _elf_exports("unused")
+    finally:
+        subprocess.run = real_run
+    assert exports == {"xvram_get_api", "xvram_amd_get_ext"}
+    assert nodes == {"XVRAM_0.1", "XVRAM_AMD_EXT_1"}
+    assert versions["xvram_amd_get_ext"] == "XVRAM_AMD_EXT_1"
 
 
 def test_product_library_loads_without_gpu():

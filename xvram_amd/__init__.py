@@ -1,9 +1,10 @@
 """xvram_amd — MI355X-native out-of-core FP32 SGEMM behind the xVRAM v1 C ABI.
 
 The product is the native library ``lib/libxvram.so`` (C++20 host runtime +
-gfx950 FP32-MFMA kernel). It exports ``xvram_get_api`` (the reference's v1
-table) and ``xvram_amd_get_ext`` (this build's extension table: GEMM plans with
-a fused bias/ReLU epilogue). This module is a thin Python client of that C ABI
+gfx950 FP32-MFMA kernel). It exports exactly one symbol, ``xvram_get_api``: the
+reference's v1 and v2 tables, and (under the private version number
+``abi.EXT_ABI_VERSION_1``) this build's extension table: GEMM plans with a
+fused bias/ReLU epilogue and a device query. This module is a thin Python client of that C ABI
 (ctypes), used by the tests and the bench the same way a C caller uses the
 function tables. There is no Python or CPU fallback: if the native library is
 missing, loading raises.
@@ -59,14 +60,10 @@ class Library:
         status = get_api(abi.ABI_VERSION_1, ctypes.sizeof(self.api), ctypes.byref(self.api))
         if status != abi.SUCCESS:
             raise XvramError(status, "xvram_get_api")
-        get_ext = self.dll.xvram_amd_get_ext
-        get_ext.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
-        get_ext.restype = ctypes.c_uint32
-        self.get_ext = get_ext
         self.ext = abi.ExtV1()
-        status = get_ext(abi.EXT_VERSION_1, ctypes.sizeof(self.ext), ctypes.byref(self.ext))
+        status = get_api(abi.EXT_ABI_VERSION_1, ctypes.sizeof(self.ext), ctypes.byref(self.ext))
         if status != abi.SUCCESS:
-            raise XvramError(status, "xvram_amd_get_ext")
+            raise XvramError(status, "xvram_get_api(extension table)")
 
     def status_name(self, status: int) -> str:
         return self.api.status_name(status).decode()

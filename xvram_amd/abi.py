@@ -261,6 +261,9 @@ def plan_info_init() -> GemmPlanInfo:
 
 # ---- xvram_amd extension table (include/xvram/xvram_amd_ext.h) -----------------------
 
+# xvram_get_api version number of the extension table (XVRAM_AMD_EXT_ABI_VERSION_1)
+# and the table's own ext_version (XVRAM_AMD_EXT_VERSION_1).
+EXT_ABI_VERSION_1 = 0x58410001
 EXT_VERSION_1 = 1
 BIAS_NONE, BIAS_PER_ROW, BIAS_PER_COLUMN = 0, 1, 2
 ACTIVATION_NONE, ACTIVATION_RELU = 0, 1

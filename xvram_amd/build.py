@@ -1,8 +1,8 @@
 """Builds the native libraries in-tree.
 
   lib/libxvram.so          the product: C++20 host runtime + gfx950 HIP kernel,
-                           exporting ``xvram_get_api@@XVRAM_0.1`` and the
-                           extension table ``xvram_amd_get_ext@@XVRAM_AMD_EXT_1``;
+                           exporting exactly ``xvram_get_api@@XVRAM_0.1`` (the
+                           extension table is one more version of it);
   lib/build_info.json      compiler, HIP and source versions of that build;
   lib/libxvram_synth.so    seeded synthetic operands for the benchmark;
   lib/libxvram_hostsim.so  the same host runtime over a host-memory device
@@ -106,6 +106,7 @@ def build(hostsim: bool = True, product: bool = True, verbose: bool = True) -> N
         out = os.path.join(LIB, "libxvram.so")
         _run([HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", out + ".tmp", *objs,
               f"-Wl,--version-script={os.path.join(CSRC, 'exports.map')}", "-Wl,--no-undefined",
+              "-Wl,-soname,libxvram.so",
               f"-L{ROCM}/lib", "-lamdhip64", "-lpthread"])
         os.replace(out + ".tmp", out)
         with open(os.path.join(LIB, "build_info.json"), "w") as f:

@@ -868,31 +868,32 @@ const xvram_amd_ext_v1& ext_v1() {
 } // namespace
 } // namespace xvram
 
-// The extension table of this build (no reference counterpart).
-extern "C" XVRAM_API xvram_status XVRAM_CALL xvram_amd_get_ext(uint32_t requested_version,
-                                                               uint32_t caller_size, void* out_ext) {
-  if (requested_version == XVRAM_AMD_EXT_VERSION_1) {
-    if (out_ext == nullptr || caller_size < sizeof(xvram_amd_ext_v1))
-      return XVRAM_STATUS_INVALID_ARGUMENT;
-    std::memcpy(out_ext, &xvram::ext_v1(), sizeof(xvram_amd_ext_v1));
-    return XVRAM_STATUS_SUCCESS;
-  }
-  return XVRAM_STATUS_INCOMPATIBLE_ABI;
-}
-
 extern "C" XVRAM_API xvram_status XVRAM_CALL xvram_get_api(uint32_t requested_abi_version,
                                                            uint32_t caller_api_size, void* out_api) {
-  if (requested_abi_version == XVRAM_ABI_VERSION_1) {
-    if (out_api == nullptr || caller_api_size < sizeof(xvram_api_v1))
-      return XVRAM_STATUS_INVALID_ARGUMENT;
-    std::memcpy(out_api, &xvram::api_v1(), sizeof(xvram_api_v1));
-    return XVRAM_STATUS_SUCCESS;
+  // One table per version; the same argument rules for each (reference
+  // src/sdk/api.cpp:967-1035).
+  const void* table = nullptr;
+  size_t size = 0;
+  switch (requested_abi_version) {
+  case XVRAM_ABI_VERSION_1:
+    table = &xvram::api_v1();
+    size = sizeof(xvram_api_v1);
+    break;
+  case XVRAM_ABI_VERSION_2:
+    table = &xvram::api_v2();
+    size = sizeof(xvram_api_v2);
+    break;
+  case XVRAM_AMD_EXT_ABI_VERSION_1:
+    // This build's extension table (no reference counterpart), reached
+    // through the one export so the library's symbol set stays the
+    // reference's.
+    table = &xvram::ext_v1();
+    size = sizeof(xvram_amd_ext_v1);
+    break;
+  default:
+    return XVRAM_STATUS_INCOMPATIBLE_ABI;
   }
-  if (requested_abi_version == XVRAM_ABI_VERSION_2) {
-    if (out_api == nullptr || caller_api_size < sizeof(xvram_api_v2))
-      return XVRAM_STATUS_INVALID_ARGUMENT;
-    std::memcpy(out_api, &xvram::api_v2(), sizeof(xvram_api_v2));
-    return XVRAM_STATUS_SUCCESS;
-  }
-  return XVRAM_STATUS_INCOMPATIBLE_ABI;
+  if (out_api == nullptr || caller_api_size < size) return XVRAM_STATUS_INVALID_ARGUMENT;
+  std::memcpy(out_api, table, size);
+  return XVRAM_STATUS_SUCCESS;
 }
