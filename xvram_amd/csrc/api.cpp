@@ -261,7 +261,18 @@ xvram_status XVRAM_CALL session_create_entry(const xvram_session_config_v1* conf
   *out = nullptr;
   return boundary({}, "session_create", [&]() -> Error {
     if (Error e = validate_session_config(config)) return e;
-    auto session = std::make_shared<Session>(*config);
+    xvram_session_config_v1 effective = *config;
+    if (config->context_mode == XVRAM_CONTEXT_ATTACH_CURRENT) {
+      // Reference src/sdk/runtime.cpp:1369-1383: the session runs on what is
+      // current on the calling thread at creation (in HIP, the thread's
+      // current device and its primary context); device_ordinal is ignored.
+      int current = -1;
+      if (current_device(&current) != 0 || current < 0)
+        return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "session", "capture_context",
+                          "no HIP device is current on the calling thread");
+      effective.device_ordinal = current;
+    }
+    auto session = std::make_shared<Session>(effective);
     if (Error e = session->start()) {
       (void)session->close(XVRAM_TIMEOUT_INFINITE);
       return e;

@@ -91,5 +91,9 @@ std::unique_ptr<Device> make_device();
 // Describes device `ordinal` without disturbing the calling thread's current
 // device; returns 0 or the native error code.
 int describe_device(int ordinal, DeviceInfo& out);
+// The device current on the calling thread (hipGetDevice: the HIP counterpart
+// of the CUDA context an XVRAM_CONTEXT_ATTACH_CURRENT session captures);
+// returns 0 or the native error code (e.g. no device at all).
+int current_device(int* ordinal);
 
 } // namespace xvram

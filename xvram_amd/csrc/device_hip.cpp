@@ -162,6 +162,13 @@ private:
 
 std::unique_ptr<Device> make_device() { return std::make_unique<HipDevice>(); }
 
+int current_device(int* ordinal) {
+  int count = 0;
+  if (hipError_t e = hipGetDeviceCount(&count); e != hipSuccess) return e;
+  if (count <= 0) return hipErrorNoDevice;
+  return hipGetDevice(ordinal);
+}
+
 int describe_device(int ordinal, DeviceInfo& out) {
   int count = 0;
   if (hipError_t e = hipGetDeviceCount(&count); e != hipSuccess) return e;

@@ -50,6 +50,9 @@ struct SimState {
   uint64_t free_bytes = 16ull << 30;
   uint64_t total_bytes = 16ull << 30;
   uint64_t kernel_launches = 0;
+  int device_count = 1;       // simulated devices 0 .. device_count-1
+  int current_device = 0;     // what the calling thread sees as current (-1: none)
+  int last_init_ordinal = -1; // the device the last session set up on
 } g_sim;
 
 int fault(Site site) {
@@ -72,7 +75,10 @@ public:
 
   int init(int ordinal) override {
     if (int f = fault(kInit)) return f;
-    return ordinal == 0 ? 0 : 101; // hipErrorInvalidDevice
+    std::lock_guard<std::mutex> lock(g_sim.mutex);
+    if (ordinal < 0 || ordinal >= g_sim.device_count) return 101; // hipErrorInvalidDevice
+    g_sim.last_init_ordinal = ordinal;
+    return 0;
   }
   int driver_version(int* version) override {
     *version = 0;
@@ -314,9 +320,16 @@ private:
 
 std::unique_ptr<Device> make_device() { return std::make_unique<HostSimDevice>(); }
 
-int describe_device(int ordinal, DeviceInfo& out) {
-  if (ordinal != 0) return 101; // hipErrorInvalidDevice
+int current_device(int* ordinal) {
   std::lock_guard<std::mutex> lock(g_sim.mutex);
+  if (g_sim.current_device < 0) return 100; // hipErrorNoDevice
+  *ordinal = g_sim.current_device;
+  return 0;
+}
+
+int describe_device(int ordinal, DeviceInfo& out) {
+  std::lock_guard<std::mutex> lock(g_sim.mutex);
+  if (ordinal < 0 || ordinal >= g_sim.device_count) return 101; // hipErrorInvalidDevice
   out.name = "xvram host simulation";
   out.arch = "hostsim";
   out.pci_bus_id.clear();
@@ -346,6 +359,26 @@ extern "C" __attribute__((visibility("default"))) void xvram_hostsim_reset() {
   for (auto& s : g_sim.sites) s = Injection{};
   g_sim.free_bytes = g_sim.total_bytes = 16ull << 30;
   g_sim.kernel_launches = 0;
+  g_sim.device_count = 1;
+  g_sim.current_device = 0;
+  g_sim.last_init_ordinal = -1;
+}
+
+// Simulated device count and the device current on calling threads (-1 = no
+// device current, as when the HIP runtime finds no device).
+extern "C" __attribute__((visibility("default"))) void xvram_hostsim_set_devices(int count,
+                                                                                 int current) {
+  using namespace xvram;
+  std::lock_guard<std::mutex> lock(g_sim.mutex);
+  g_sim.device_count = count;
+  g_sim.current_device = current;
+}
+
+// The ordinal the most recent session set up on (-1 before any).
+extern "C" __attribute__((visibility("default"))) int xvram_hostsim_last_init_ordinal() {
+  using namespace xvram;
+  std::lock_guard<std::mutex> lock(g_sim.mutex);
+  return g_sim.last_init_ordinal;
 }
 
 extern "C" __attribute__((visibility("default"))) void xvram_hostsim_set_memory(uint64_t free_b,
