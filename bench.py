@@ -5,11 +5,16 @@ Default workload (BASELINE.json metric "out-of-core FP32 SGEMM TFLOP/s at 3x
 VRAM budget; H2D GB/s vs link peak"): the north-star GEMM, C = A * B^T with
 M = N = K = 65536 (A, B, C = 3 x 16 GiB of pinned host memory) under a 16 GiB
 VRAM budget of 1 GiB frames (operands = 3x the budget). A "step" is one
-complete gemm_execute: every A/B panel streamed from host RAM, every C tile
-written back.
+complete gemm_execute plus session_drain: every A/B panel streamed from host
+RAM, every C tile written back.
 
 Prints one JSON line. ``value`` = 2MNK / wall time per step (inputs resident in
-host memory, as the ABI defines them). ``roofline`` describes the dominant
+host memory, as the ABI defines them). For the out-of-core workloads a step is
+gemm_execute followed by session_drain, so every C byte is back in host memory
+when the step's clock stops (the cache is write-back: a GEMM leaves its last C
+tiles resident and dirty). The resident config-3 workloads time gemm_execute
+alone: their C stays cached between executions, as a caller repeating a
+resident GEMM sees it. ``roofline`` describes the dominant
 kernel (the FP32-MFMA tile kernel): algorithmic FLOPs of its launches divided
 by their summed duration, both from the HIP events attached to every kernel
 dispatch on the library's compute stream (trace file written by the library);
@@ -17,8 +22,11 @@ dispatch on the library's compute stream (trace file written by the library);
 operation's first launch may run as several K-slice kernels). Other workloads:
 ``--workload`` (config 3's resident sweep, config 4, the config-5 chain).
 ``cpu_baseline`` times the FP64 reference loop (the oracle's restatement of
-the reference's CPU GEMM) on a bounded sample of the same product on all host
-cores; the same sample checks the GPU result against the per-element bound.
+the reference's CPU GEMM) on a bounded sample of the same product, on all host
+cores and, faithful to the reference example, on one thread. ``sample_check``
+verifies the GPU result against the per-element bound on one full column per
+tile column, one full row per tile row and seeded random elements
+(oracle/sample.py), every element with its full K.
 """
 from __future__ import annotations
 
@@ -247,11 +255,54 @@ def fill_allocation(synth, alloc, elements: int, seed: int, chunk_elems: int = 2
         done += n
 
 
-def sample_block(synth, rows, cols, seed, first, row_stride, col_stride):
-    out = np.empty(rows * cols, dtype=np.float32)
-    synth.synth_fill_uniform_strided(out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), rows,
-                                     cols, seed, first, row_stride, col_stride)
-    return np.asfortranarray(out.reshape(cols, rows).T)
+# ---- CPU baseline ----------------------------------------------------------------------
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(a_seeded, b_seeded, m, n, k, seconds):
+    """The oracle's FP64 loop (examples/preview-gemm/main.cpp:107-119 restated)
+    on C[0:r, 0:cols] of the same product with full K: on every host thread
+    (cols scaled to about `seconds`) and, as the reference example runs it, on
+    one thread (a narrower sample scaled to about `seconds` / 2). Rates are
+    2 r cols K / time."""
+    import oracle
+
+    threads = os.cpu_count() or 1
+    r = min(m, 1024)
+    a_s = a_seeded.rows(range(r))
+
+    def timed(cols, nthreads):
+        b_s = b_seeded.cols(range(cols))
+        t = time.perf_counter()
+        oracle.sgemm_f64(a_s, b_s, threads=nthreads)
+        return time.perf_counter() - t
+
+    out = {"unit": "TFLOP/s", "kind": "port", "cores": threads, "nproc": os.cpu_count(),
+           "cpu_model": cpu_model()}
+    probe_cols = min(n, 2 * threads)
+    probe = timed(probe_cols, threads)
+    cols = int(min(n, max(probe_cols, probe_cols * seconds / max(probe, 1e-3))))
+    secs = timed(cols, threads)
+    out["value"] = round(2.0 * r * cols * k / secs / 1e12, 6)
+    out["sample"] = (f"C[0:{r}, 0:{cols}] of the same {m}x{n}x{k} product with full K (FP64 "
+                     f"accumulation over FP32 inputs, {secs:.1f} s on {threads} threads)")
+    probe1 = timed(1, 1)
+    cols1 = int(min(n, max(1, (seconds / 2) / max(probe1, 1e-3))))
+    secs1 = timed(cols1, 1)
+    out["single_thread"] = {
+        "value": round(2.0 * r * cols1 * k / secs1 / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
+        "sample": f"C[0:{r}, 0:{cols1}] with full K ({secs1:.1f} s on one thread)"}
+    log(f"cpu baseline: {out['value']} TFLOP/s on {threads} threads, "
+        f"{out['single_thread']['value']} on one ({out['cpu_model']})")
+    return out
 
 
 # ---- config 5: the inference chain ---------------------------------------------------
@@ -260,7 +311,8 @@ def run_chain(args, xv, lib, synth, link) -> int:
     """One step = one forward of CHAIN["layers"] x [Y = ReLU(X W^T + b)]: each
     layer is one GEMM plan with a fused bias+ReLU epilogue (extension table),
     the 8 operations are submitted back to back, weights stream from pinned host
-    memory through the 2 GiB budget."""
+    memory through the 2 GiB budget, and the step ends with the output read
+    back to the host."""
     import oracle
 
     L, batch, width = CHAIN["layers"], CHAIN["batch"], CHAIN["width"]
@@ -287,13 +339,19 @@ def run_chain(args, xv, lib, synth, link) -> int:
     log(f"chain ready: {L} x {width * width * 4 / GiB:.0f} GiB weights ({time.time() - t0:.1f}s); "
         f"layer plan tiles {info.tile_m}x{info.tile_n}x{info.tile_k}, {info.tile_count} launches")
 
+    y_out = np.empty(batch * width, dtype=np.float32)
+
     def forward():
+        """The 8 layers submitted back to back, then the output read back
+        (intermediate activations stay in the device cache: each layer's C
+        tiles are the next layer's input panels)."""
         ops = [p.submit() for p in plans]
         for op in ops:
             st, res = op.wait()
             if st != 0 or res.result != 0:
                 raise RuntimeError(f"layer failed: {st} {res.result} {op.error().message}")
             op.release()
+        acts[L].read_into(y_out)
 
     trace_path = os.environ["XVRAM_TRACE_FILE"]
     for i in range(args.warmup):
@@ -358,13 +416,22 @@ def run_chain(args, xv, lib, synth, link) -> int:
         oracle.sgemm_f64(np.asfortranarray(x_all[:r]), w0t, threads=threads)
         cpu_s = time.perf_counter() - t
         cpu = {"value": round(2.0 * r * width * width / cpu_s / 1e12, 6), "unit": "TFLOP/s",
-               "cores": threads, "kind": "port",
+               "cores": threads, "kind": "port", "nproc": os.cpu_count(),
+               "cpu_model": cpu_model(),
                "sample": f"layer 0, Y[0:{r}, 0:{width}] with full K={width} (FP64 accumulation "
                          f"over FP32 inputs, {cpu_s:.1f} s on {threads} threads)"}
+        # One thread, as the reference example runs: one batch row.
+        t = time.perf_counter()
+        oracle.sgemm_f64(np.asfortranarray(x_all[:1]), w0t, threads=1)
+        cpu_1 = time.perf_counter() - t
+        cpu["single_thread"] = {"value": round(2.0 * width * width / cpu_1 / 1e12, 6),
+                                "unit": "TFLOP/s", "cores": 1,
+                                "sample": f"layer 0, Y[0:1, 0:{width}] ({cpu_1:.1f} s on one thread)"}
         del w0t
 
-    h2d_compulsory = L * (width * width * 4 + width * 4 + batch * width * 4)
-    d2h_compulsory = L * batch * width * 4
+    # Weights and biases of every layer and the input; the output comes back.
+    h2d_compulsory = L * (width * width * 4 + width * 4) + batch * width * 4
+    d2h_compulsory = batch * width * 4
     t_roof = max(flops / (FP32_MFMA_PEAK_TFLOPS * 1e12), h2d_compulsory / (link["h2d_gbps"] * 1e9),
                  d2h_compulsory / (link["d2h_gbps"] * 1e9))
     kernel_tflops = flops * args.steps / (stats["kernel_ms_total"] * 1e-3) / 1e12
@@ -482,9 +549,17 @@ def main() -> int:
                        tile_hints=tuple(int(v) for v in args.tile_hints.split(",")))
     info = plan.info()
     log(f"plan: tiles {info.tile_m}x{info.tile_n}x{info.tile_k}, {info.tile_count} launches")
+    # Out of core: a step ends when C is entirely back in host memory.
+    drain = budget != 0
+
+    def step():
+        plan.execute()
+        if drain:
+            session.drain()
+
     for i in range(args.warmup):
         t = time.perf_counter()
-        plan.execute()
+        step()
         log(f"warmup {i}: {time.perf_counter() - t:.3f}s")
     with open(trace_path, "a"):
         pass
@@ -493,7 +568,7 @@ def main() -> int:
     times = []
     for i in range(args.steps):
         t = time.perf_counter()
-        plan.execute()
+        step()
         times.append(time.perf_counter() - t)
         log(f"step {i}: {times[-1]:.3f}s = {2.0 * m * n * k / times[-1] / 1e12:.1f} TFLOP/s")
     tele1 = session.telemetry()
@@ -512,36 +587,29 @@ def main() -> int:
     launches_per_step = info.tile_count
     kernels_per_step = stats["launches"] / args.steps
 
-    # Sample check + CPU baseline on the same sample: C[0:sr, 0:sc] with full K.
-    import oracle
+    # Sample check: one full column per tile column, one full row per tile row
+    # and seeded random elements, all with full K, against the FP64 oracle.
+    from oracle.sample import SeededOperand, spread_check
 
-    sr, sc = min(m, 1024), min(n, 64)
-    a_s = sample_block(synth, sr, k, 1, 0, 1 if op_a == OP_N else k, m if op_a == OP_N else 1)
-    b_s = sample_block(synth, k, sc, 2, 0, 1 if op_b == OP_N else n, k if op_b == OP_N else 1)
-    got = np.empty((sc, sr), dtype=np.float32)
-    for j in range(sc):
-        c.read_into(got[j], offset=(j * m) * 4)
-    got = np.asfortranarray(got.T)
-    threads = os.cpu_count() or 1
+    a_seeded = SeededOperand(1, a_rows, a_cols, op_a == OP_T)
+    b_seeded = SeededOperand(2, b_rows, b_cols, op_b == OP_T)
+
+    def read_columns(j0, j1):
+        out = np.empty((j1 - j0) * m, dtype=np.float32)
+        c.read_into(out, offset=j0 * m * 4)
+        return out.reshape(j1 - j0, m).T
+
     t = time.perf_counter()
-    ref, absab = oracle.sgemm_f64(a_s, b_s, threads=threads)
-    cpu_s = time.perf_counter() - t
-    bad, max_err, ratio = oracle.check_bound(got, k, ref, absab)
-    log(f"sample {sr}x{sc}: violations={bad} max_err={max_err:.3e} err/bound={ratio:.3e}")
+    check = spread_check(a_seeded, b_seeded, read_columns, info.tile_m, info.tile_n, seed=7,
+                         randoms=1024)
+    log(f"sample check: {check['elements']} elements ({len(check['full_columns'])} full columns, "
+        f"{len(check['full_rows'])} full rows, {check['random_elements']} random), "
+        f"violations={check['violations']} err/bound={check['max_err_over_bound']:.3e} "
+        f"({time.perf_counter() - t:.1f}s)")
+    bad = check["violations"]
     cpu = None
     if not args.no_cpu_baseline:
-        # Scale the column count so the timed CPU work is about --cpu-seconds.
-        cols = max(sc, int(sc * args.cpu_seconds / max(cpu_s, 1e-3)))
-        cols = min(cols, n)
-        b_cpu = sample_block(synth, k, cols, 2, 0, 1 if op_b == OP_N else n,
-                             k if op_b == OP_N else 1)
-        t = time.perf_counter()
-        oracle.sgemm_f64(a_s, b_cpu, threads=threads)
-        cpu_s = time.perf_counter() - t
-        cpu = {"value": round(2.0 * sr * cols * k / cpu_s / 1e12, 6), "unit": "TFLOP/s",
-               "cores": threads, "kind": "port",
-               "sample": f"C[0:{sr}, 0:{cols}] of the same {m}x{n}x{k} product with full K "
-                         f"(FP64 accumulation over FP32 inputs, {cpu_s:.1f} s on {threads} threads)"}
+        cpu = cpu_baseline(a_seeded, b_seeded, m, n, k, args.cpu_seconds)
 
     # HBM traffic per launch from the committed rocprofv3 --pmc summary of this
     # workload's tile kernel (profiles/traffic_<kernel>_<workload>.txt), if any;
@@ -601,8 +669,9 @@ def main() -> int:
         "cache": {f: getattr(tele1, f) - getattr(tele0, f) for f in (
             "bytes_h2d", "bytes_d2h", "cache_hits", "cache_misses", "clean_evictions",
             "dirty_evictions", "writebacks_completed", "handle_reuses", "event_boundaries")},
-        "sample_check": {"elements": sr * sc, "violations": bad, "max_err_over_bound": ratio},
+        "sample_check": check,
     }
+    result["config"]["step"] = "gemm_execute + session_drain" if drain else "gemm_execute"
     result["roofline_wall"]["frac"] = round(result["roofline_wall"]["t_roof_s"] / step_s, 4)
     plan.release()
     session.close()

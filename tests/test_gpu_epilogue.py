@@ -122,7 +122,7 @@ def run_chain(lib, oracle_mod, prefetch_distance=2, layers=8, batch=256, width=4
 def test_inference_chain_streams_weights(lib, oracle_mod):
     layers, width = 8, 4096
     x0, ys, weights, biases, t0, t1 = run_chain(lib, oracle_mod, layers=layers, width=width)
-    # All weights streamed (8 x 64 MiB), activations in and out once per layer.
+    # All weights streamed (8 x 64 MiB); activations stay in the device cache.
     assert t1.bytes_h2d - t0.bytes_h2d >= layers * width * width * 4
     # Per layer, from the FP32 input the GPU actually used.
     for l in range(layers):
@@ -145,13 +145,17 @@ def test_inference_chain_streams_weights(lib, oracle_mod):
 def test_chain_carried_fills_match(lib, oracle_mod):
     """Fills carried across queued operations (the default) change where and
     when weight panels are loaded, never what a kernel reads: every layer's
-    output is bit-identical to the run without carrying, and no extra bytes
-    cross the link."""
+    output is bit-identical to the run without carrying. The carried panels are
+    the ones the next operation loads first anyway; since the activations stay
+    cached between layers, carrying can change which frames the victim policy
+    frees later, so the byte counts may differ, but carrying adds none here
+    (the accounting depends only on the schedule, so this is deterministic)."""
     _, carried, _, _, c0, c1 = run_chain(lib, oracle_mod, prefetch_distance=2)
     _, plain, _, _, p0, p1 = run_chain(lib, oracle_mod, prefetch_distance=0)
     for l, (a, b) in enumerate(zip(carried, plain)):
         assert np.array_equal(a, b), l
-    assert c1.bytes_h2d - c0.bytes_h2d == p1.bytes_h2d - p0.bytes_h2d
-    assert c1.cache_misses - c0.cache_misses == p1.cache_misses - p0.cache_misses
-    print(f"carried hits {c1.cache_hits - c0.cache_hits} vs {p1.cache_hits - p0.cache_hits}",
-          flush=True)
+    carried_h2d, plain_h2d = c1.bytes_h2d - c0.bytes_h2d, p1.bytes_h2d - p0.bytes_h2d
+    print(f"H2D carried {carried_h2d} vs {plain_h2d} bytes; hits "
+          f"{c1.cache_hits - c0.cache_hits} vs {p1.cache_hits - p0.cache_hits}", flush=True)
+    assert carried_h2d <= plain_h2d
+    assert c1.cache_misses - c0.cache_misses <= p1.cache_misses - p0.cache_misses

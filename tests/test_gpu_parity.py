@@ -98,7 +98,10 @@ def test_pattern_bit_exact_out_of_core(lib, oracle_mod, ops):
         t = s.telemetry()
         assert prob.plan_info.tile_count > 1
         assert t.clean_evictions + t.dirty_evictions > 0
-        assert t.dirty_evictions == t.writebacks_completed
+        # Non-final C blocks are written back and evicted during the GEMM; the
+        # last block's tiles stay dirty until the read of C writes them back.
+        assert 0 < t.dirty_evictions < t.writebacks_completed
+        assert t.bytes_d2h == m * n * 4
         assert t.resident_bytes_peak <= t.cache_target_bytes
     expected = oracle_mod.pattern_expected_matrix(m, n, k)
     assert np.array_equal(out.astype(np.float64), expected)
@@ -110,8 +113,9 @@ def test_repeat_uses_cached_panels(lib, oracle_mod):
     with xv.Session(lib, chunk_size_bytes=64 * MiB) as s:
         out = prob.run(s, repeat=3)
         t = s.telemetry()
-        # A and B were copied once; C is write-only (beta = 0) every time.
+        # A and B were copied once; C is write-only (beta = 0) and stays cached
+        # (dirty) between executions: only the final read writes it back.
         assert t.bytes_h2d == 2 * m * k * 4
-        assert t.bytes_d2h == 3 * m * n * 4
-        assert t.cache_hits > 0
+        assert t.bytes_d2h == m * n * 4
+        assert t.cache_hits == 6
     check(oracle_mod, prob, out, "repeat x3 2048^3")

@@ -6,8 +6,9 @@ between queued operations.
 The chains here are queued behind a transaction whose callback holds the
 worker until every GEMM is submitted, so each operation's tail deterministically
 sees the next one and the accounting is exact. Every layer reads the previous
-layer's output, which is still being written back when the carry runs: those
-panels must not be carried (they would hold stale host bytes)."""
+layer's output, which is still cached (dirty) when the carry runs: those panels
+are never carried (a fill from host memory would hold stale bytes); here they
+are the previous layer's C tiles themselves, found in the cache."""
 import threading
 
 import numpy as np
@@ -106,9 +107,9 @@ def test_carried_fills_keep_results_and_bytes(sim, oracle_mod):
     # Geometry of each layer (16 KiB frames): 64 x 40 C tiles, 64-deep K panels,
     # so 2 tiles x 2 K panels = 4 launches, each with its own W panel, all four
     # inside the next operation's first lookahead window (14 frames: lookahead 3).
-    # The B panels of the next layer are this layer's output, still being
-    # written back when the carry runs: never carried. Hence exactly 4 carried
-    # panels per boundary.
+    # The B panels of the next layer are this layer's output: its C tiles, the
+    # very same rectangles, still cached (dirty) from this layer, so there is
+    # nothing to carry for them. Hence exactly 4 carried panels per boundary.
     assert (info.tile_m, info.tile_n, info.tile_k, info.tile_count) == (64, 40, 64, 4)
     assert d1["cache_hits"] - d0["cache_hits"] == (layers - 1) * 4
     assert d1["bytes_d2h"] == d0["bytes_d2h"]

@@ -115,6 +115,9 @@ def test_threads_share_one_session(sim, oracle_mod):
         assert t.mappings == t.unmaps == t.set_access_calls
         assert t.physical_handles_created == t.physical_handles_released
         assert t.unsafe_transitions == 0 and t.unsafe_remaps == 0
-        assert t.dirty_evictions == t.writebacks_completed
+        # Evictions of dirty entries are a subset of the write-backs (reads of C
+        # and close write back entries that stay cached).
+        assert t.dirty_evictions <= t.writebacks_completed
+        assert t.resident_bytes == 0
         assert t.resident_bytes == 0
         s.release()

@@ -86,7 +86,10 @@ def test_accounting_invariants_and_teardown(sim, oracle_mod):
     out = prob.run(s)
     check(oracle_mod, prob, out)
     t = s.telemetry()
-    assert t.dirty_evictions == t.writebacks_completed > 0
+    # C tiles of every block but the last were written back and evicted during
+    # the operation; the last block's stayed cached, dirty, until the read of C
+    # wrote them back (keeping them cached, clean).
+    assert 0 < t.dirty_evictions < t.writebacks_completed
     assert t.clean_evictions > 0 and t.handle_reuses > 0
     assert t.mappings == t.set_access_calls == t.physical_handles_created <= 12
     assert t.resident_bytes_peak <= t.cache_target_bytes
@@ -125,8 +128,11 @@ def test_repeat_hits_cached_panels(sim, oracle_mod):
         out = prob.run(s, repeat=3)
         t = s.telemetry()
         assert t.bytes_h2d == 2 * m * k * 4
-        assert t.bytes_d2h == 3 * m * n * 4
-        assert t.cache_hits == 4   # A and B hit on the 2nd and 3rd execution
+        # C stays cached (dirty) between executions; only the final read of C
+        # writes it back.
+        assert t.bytes_d2h == m * n * 4
+        assert t.writebacks_completed == 1 and t.dirty_evictions == 0
+        assert t.cache_hits == 6   # A, B and C hit on the 2nd and 3rd execution
     check(oracle_mod, prob, out)
 
 

@@ -83,10 +83,16 @@ def test_reference_normalization_case(sim):
         # Only the mixed chunk (first, 0) is loaded; the other three are full
         # write-only chunks (including the 4-byte-scaled tail).
         assert t1.bytes_h2d - t0.bytes_h2d == F
-        assert t1.writebacks_completed - t0.writebacks_completed == 4
-        assert t1.bytes_d2h - t0.bytes_d2h == 20 * u + 8 * u
+        # The four written chunks stay cached, dirty (write-back cache) ...
+        assert t1.writebacks_completed == t0.writebacks_completed
+        assert t1.bytes_d2h == t0.bytes_d2h
         assert t1.transactions_completed - t0.transactions_completed == 1
         out1, out2 = first.read(), second.read()
+        # ... until the reads write them back.
+        t2 = s.telemetry()
+        assert t2.writebacks_completed - t0.writebacks_completed == 4
+        assert t2.bytes_d2h - t0.bytes_d2h == 20 * u + 8 * u
+        assert t2.dirty_evictions == t0.dirty_evictions
         exp1 = d1.copy()
         exp1[0:4 * u] = (id1 * 16 + 0) & 0xFF
         exp1[4 * u:8 * u] ^= 0x5A

@@ -474,6 +474,7 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
             l.kp = static_cast<uint32_t>(kp);
             l.first_panel = q == 0;
             l.last_panel = q + 1 == out.panels_k;
+            l.evict_c = l.last_panel && block_seq + 1 < blocks_m * blocks_n;
             out.launches.push_back(l);
           }
         }
@@ -538,9 +539,11 @@ LaunchGeom launch_geom(const GemmPlanData& plan, const TileLaunch& l) {
 // (H2D copies queued on the copy stream) before each launch is enqueued on the
 // compute stream; the compute stream waits on the fill events of the launch's
 // three frames; the launch's stop event, recorded by its dispatch, becomes the
-// retire event of those frames; a C tile is written back on the D2H stream as soon as its last K panel is
-// enqueued. The host blocks only when a frame it wants to refill still has an
-// unretired consumer.
+// retire event of those frames. A C tile of any block but the last is written
+// back on the D2H stream and evicted as soon as its last K panel is enqueued
+// (the next block needs the frame); the last block's tiles stay resident and
+// dirty after the operation (write-back cache). The host blocks only when a
+// frame it wants to refill still has an unretired consumer.
 Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
                    const GemmHooks& hooks) {
   const CanonProblem& p = plan.problem;
@@ -706,7 +709,7 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     if (Error e = rt.release_after_event(*acq.a, done, false)) { result = e; break; }
     if (Error e = rt.release_after_event(*acq.b, done, false)) { result = e; break; }
     if (Error e = rt.release_after_event(*acq.c, done, true)) { result = e; break; }
-    if (l.last_panel) {
+    if (l.evict_c) {
       if (Error e = rt.writeback_and_evict(*acq.c)) {
         result = e;
         break;

@@ -117,7 +117,11 @@ CanonProblem canonicalize(const GemmSpec& spec);
 struct TileLaunch {
   uint32_t ti = 0, tj = 0, kp = 0;
   bool first_panel = false; // first K panel applied to this C tile (uses user beta)
-  bool last_panel = false;  // C tile final after this launch (write back)
+  bool last_panel = false;  // C tile final after this launch
+  // The C tile is final and its block is not the plan's last: the next
+  // blocks' tiles need its frame, so it is written back and evicted as soon
+  // as this launch is enqueued. The last block's tiles stay resident, dirty.
+  bool evict_c = false;
 };
 
 struct GemmPlanData {

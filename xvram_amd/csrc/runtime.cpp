@@ -154,11 +154,44 @@ Error Runtime::setup() {
   return {};
 }
 
+// Drain (reference runtime.cpp:1497-1538 with release_mappings = false): every
+// dirty entry is written back and stays cached, clean; then the device idles.
+// A poisoned session only waits for its streams.
 Error Runtime::drain() {
   if (!setup_done_ || closed_) return {};
+  if (!poisoned_)
+    if (Error e = flush_all()) return e;
   for (Stream s : {h2d_, compute_, d2h_})
     if (int rc = device_->stream_sync(s)) return device_failure(rc, "drain", "stream_sync");
+  writebacks_settled();
   return {};
+}
+
+Error Runtime::flush_all() {
+  bool issued = false;
+  for (Frame& f : frames_) {
+    if (!f.keyed || !f.dirty) continue;
+    if (f.pins > 0)
+      return make_error(XVRAM_STATUS_INTERNAL, "cache", "flush", "a dirty entry is still in use");
+    if (Error e = writeback(f, false)) return e;
+    issued = true;
+  }
+  if (issued) {
+    if (int rc = device_->stream_sync(d2h_)) return device_failure(rc, "cache", "stream_sync");
+    writebacks_settled();
+  }
+  return {};
+}
+
+// The D2H stream has drained: every write-back issued so far has landed.
+// Outside an operation (read, write, drain, close) the events those copies
+// took are complete and go back to the pool at once.
+void Runtime::writebacks_settled() {
+  pending_writebacks_.clear();
+  for (Frame& f : frames_) f.writeback_done = nullptr;
+  if (in_operation_) return;
+  event_pool_.insert(event_pool_.end(), events_in_use_.begin(), events_in_use_.end());
+  events_in_use_.clear();
 }
 
 // Teardown (reference runtime.cpp:1540-1857): wait for the device, unmap and
@@ -176,6 +209,11 @@ Error Runtime::close() {
     allocations_.clear();
     return {};
   }
+  // Dirty entries reach host memory first (reference close writes back each
+  // resident_dirty chunk before unmapping it, runtime.cpp:1620-1625).
+  for (Frame& f : frames_) f.pins = 0;
+  if (!poisoned_)
+    if (Error e = flush_all(); e && !first) first = e;
   for (Stream s : {h2d_, compute_, d2h_})
     if (s) note(device_->stream_sync(s), "stream_sync");
   for (Frame& f : frames_) {
@@ -332,8 +370,30 @@ Error Runtime::read(uint64_t id, uint64_t offset, void* destination, uint64_t by
     return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "allocation", "read",
                       "read range exceeds the allocation");
   if (poisoned_) return make_error(XVRAM_STATUS_POISONED, "allocation", "read", "session is poisoned");
-  // Operations write their dirty entries back before completing, so the host
-  // copy is authoritative here.
+  // Dirty entries overlapping the range are written back first and stay
+  // cached, clean (reference Runtime::read -> flush_overlapping(..., false),
+  // runtime.cpp:931-945, 3155-3173).
+  if (bytes > 0) {
+    PanelKey range;
+    range.allocation_id = id;
+    range.offset = offset;
+    range.width = bytes;
+    range.height = 1;
+    range.pitch = bytes;
+    range.kind = EntryKind::chunk;
+    bool issued = false;
+    for (Frame& f : frames_) {
+      if (!f.keyed || !f.dirty || !keys_overlap(f.key, range)) continue;
+      if (f.pins > 0)
+        return make_error(XVRAM_STATUS_BUSY, "cache", "read", "entry is in use by an operation");
+      if (Error e = writeback(f, false)) return e;
+      issued = true;
+    }
+    if (issued) {
+      if (int rc = device_->stream_sync(d2h_)) return device_failure(rc, "allocation", "stream_sync");
+      writebacks_settled();
+    }
+  }
   parallel_copy(destination, a->host + offset, bytes);
   return {};
 }
@@ -436,6 +496,7 @@ Error Runtime::wait_retired(Frame& f) {
   }
   f.retire_pending = false;
   f.completed = f.generation;
+  f.writeback_done = nullptr; // recorded no later than the retire event
   if (f.state == EntryState::evicting) move(f, EntryState::host_clean);
   return {};
 }
@@ -484,6 +545,7 @@ bool Runtime::allocation_streaming(uint64_t allocation_id) {
 // retire records), never on how far the device has progressed, so the
 // accounting of a run is reproducible.
 Error Runtime::select_frame(Frame*& out) {
+  if (Error e = clean_excess_dirty()) return e;
   Frame* free_frame = nullptr;
   Frame* uncreated = nullptr;
   std::vector<VictimCandidate> candidates;
@@ -637,6 +699,7 @@ Error Runtime::acquire(const PanelKey& key, uint64_t packed_pitch, bool needs_da
       ++t_.clean_evictions;
     }
   }
+  if (Error e = flush_overlapping(key, nullptr)) return e;
   Frame* f = nullptr;
   if (Error e = select_frame(f)) return e;
   if (Error e = map_frame_at(*f, f->slot)) return e;
@@ -686,6 +749,7 @@ Error Runtime::acquire_pieces(const PanelKey& key, uint64_t packed_pitch,
   }
   if (covered != key.bytes())
     return make_error(XVRAM_STATUS_INTERNAL, "cache", "acquire", "pieces do not tile the panel");
+  if (Error e = flush_overlapping(key, nullptr)) return e;
   Frame* f = nullptr;
   if (Error e = select_frame(f)) return e;
   if (Error e = map_frame_at(*f, f->slot)) return e;
@@ -696,7 +760,14 @@ Error Runtime::acquire_pieces(const PanelKey& key, uint64_t packed_pitch,
 
 // Orders `stream` after the fill; from then on the entry's bytes are resident
 // for everything enqueued on that stream.
+// A write-back of the entry still in flight is waited for too: the work on
+// `stream` may overwrite the frame.
 Error Runtime::wait_ready(Frame& f, Stream stream) {
+  if (f.writeback_done) {
+    if (int rc = device_->stream_wait_event(stream, f.writeback_done))
+      return device_failure(rc, "cache", "stream_wait");
+    f.writeback_done = nullptr;
+  }
   if (!f.ready_pending) return {};
   if (int rc = device_->stream_wait_event(stream, f.ready))
     return device_failure(rc, "cache", "stream_wait");
@@ -723,9 +794,12 @@ Error Runtime::unpin(Frame& f, bool dirty) {
     if (f.state == EntryState::h2d_in_flight) move(f, EntryState::resident_clean);
     move(f, EntryState::resident_dirty);
   }
-  f.dirty = f.dirty || dirty;
   f.last_use = ++tick_;
-  return {};
+  if (!dirty) return {};
+  f.dirty = true;
+  f.dirty_serial = op_serial_;
+  // Other cached copies of these bytes are stale from now on.
+  return drop_overlapping(f.key, &f);
 }
 
 // Clean, idle entries whose bytes intersect bytes just written back are stale.
@@ -743,8 +817,11 @@ Error Runtime::drop_overlapping(const PanelKey& written, const Frame* except) {
 
 // Dirty write-back (reference writeback, runtime.cpp:3899-4262): the D2H copy
 // is ordered after the frame's last consumer and becomes the frame's retire
-// event, so the frame is refilled only after the host bytes are current.
-Error Runtime::writeback_and_evict(Frame& f) {
+// event, so the frame is refilled only after the host bytes are current; a
+// fill of overlapping host bytes waits for the copy (pending_writebacks_), and
+// so does a later writer of the same frame when the entry stays cached
+// (Frame::writeback_done, waited for in wait_ready).
+Error Runtime::writeback(Frame& f, bool evict) {
   if (!f.keyed || !f.dirty || f.pins > 0)
     return make_error(XVRAM_STATUS_INTERNAL, "cache", "writeback", "frame is not an idle dirty entry");
   HostAllocation* a = find(f.key.allocation_id);
@@ -764,17 +841,53 @@ Error Runtime::writeback_and_evict(Frame& f) {
   move(f, EntryState::d2h_in_flight);
   if (Error e = take_event(iv.stop)) return e;
   if (int rc = device_->event_record(iv.stop, d2h_)) return device_failure(rc, "cache", "record");
-  trace_.push_back(iv);
+  // Intervals are traced per operation; a write-back outside one (read,
+  // drain, close) is not.
+  if (in_operation_) trace_.push_back(iv);
   if (Error e = record_retire(f, d2h_)) return e;
   // The frame now matches what the host will hold once the copy retires; its
   // retire event (the copy) gates any reuse.
   move(f, EntryState::resident_clean);
+  f.dirty = false;
   const PanelKey written = f.key;
   pending_writebacks_[written] = iv.stop;
   t_.bytes_d2h += written.bytes();
   ++t_.writebacks_completed;
+  if (!evict) {
+    f.writeback_done = iv.stop;
+    return {};
+  }
   if (Error e = evict_key(f, true)) return e;
   return drop_overlapping(written, &f);
+}
+
+Error Runtime::flush_overlapping(const PanelKey& key, const Frame* except) {
+  for (Frame& f : frames_) {
+    if (&f == except || !f.keyed || !f.dirty || !keys_overlap(f.key, key)) continue;
+    if (f.pins > 0)
+      return make_error(XVRAM_STATUS_INTERNAL, "cache", "flush_overlapping",
+                        "an entry overlapping the one being filled is written by the operation");
+    if (Error e = writeback(f, false)) return e;
+  }
+  return {};
+}
+
+// Only entries earlier operations wrote count: the running operation's own
+// outputs follow its schedule (TileLaunch::evict_c), and cleaning a C tile that
+// later K panels still accumulate into would only repeat its copy.
+Error Runtime::clean_excess_dirty() {
+  std::vector<Frame*> idle_dirty;
+  for (uint64_t i = 0; i < capacity_; ++i) {
+    Frame& f = frames_[i];
+    if (f.keyed && f.dirty && f.pins == 0 && f.dirty_serial < op_serial_) idle_dirty.push_back(&f);
+  }
+  if (idle_dirty.size() * 2 <= capacity_) return {};
+  std::sort(idle_dirty.begin(), idle_dirty.end(),
+            [](const Frame* x, const Frame* y) { return x->last_use < y->last_use; });
+  const size_t keep = capacity_ / 4;
+  for (size_t i = 0; i + keep < idle_dirty.size(); ++i)
+    if (Error e = writeback(*idle_dirty[i], false)) return e;
+  return {};
 }
 
 Error Runtime::invalidate(uint64_t allocation_id, uint64_t begin, uint64_t end) {
@@ -793,6 +906,7 @@ Error Runtime::invalidate(uint64_t allocation_id, uint64_t begin, uint64_t end) 
     if (f.dirty) {
       if (Error e = writeback_and_evict(f)) return e;
       if (int rc = device_->stream_sync(d2h_)) return device_failure(rc, "cache", "stream_sync");
+      writebacks_settled();
     } else {
       if (Error e = wait_retired(f)) return e;
       if (Error e = evict_key(f, false)) return e;
@@ -805,7 +919,7 @@ Error Runtime::invalidate(uint64_t allocation_id, uint64_t begin, uint64_t end) 
 void Runtime::discard_dirty() {
   for (Frame& f : frames_) {
     f.pins = 0;
-    if (f.keyed && f.dirty) (void)evict_key(f, false);
+    if (f.keyed && f.dirty && f.dirty_serial == op_serial_) (void)evict_key(f, false);
   }
 }
 
@@ -977,6 +1091,7 @@ Error Runtime::acquire_chunk(ChunkUse& use) {
     use.frame = &f;
     return {};
   }
+  if (Error e = flush_overlapping(key, nullptr)) return e;
   const uint64_t address = a->va + key.offset;
   Frame* f = nullptr;
   for (uint64_t i = 0; i < capacity_; ++i) {
@@ -1015,20 +1130,22 @@ Error Runtime::run_transaction(const std::vector<AccessSpan>& ranges, uint64_t w
   if (!result) result = ensure_workspace(workspace_bytes);
   for (size_t i = 0; !result && i < chunks.size(); ++i)
     if (Error e = acquire_chunk(chunks[i])) result = e;
-  // Leaves the cache as if the callback had never run: unpins, and drops every
-  // chunk the work may have written or that was mapped without its data.
-  const auto abandon = [&]() {
+  // Leaves the cache as if the callback had never run: unpins, drops every
+  // chunk that was mapped without its data and, when work may have been
+  // enqueued, every chunk that work may have written (its earlier contents,
+  // dirty or not, are gone either way).
+  const auto abandon = [&](bool work_enqueued) {
     for (ChunkUse& u : chunks) {
       if (!u.frame) continue;
       if (u.frame->pins > 0) --u.frame->pins;
-      if (u.writes || u.filled_empty) {
+      if ((work_enqueued && u.writes) || u.filled_empty) {
         u.frame->dirty = false;
         (void)evict_key(*u.frame, false);
       }
     }
   };
   if (result) {
-    abandon();
+    abandon(false);
     (void)finish_operation(operation_id);
     return result;
   }
@@ -1055,7 +1172,7 @@ Error Runtime::run_transaction(const std::vector<AccessSpan>& ranges, uint64_t w
     // A skipped callback enqueued nothing; a failed one may have enqueued work
     // (the reference's failed_after_possible_submission), which poisons the
     // session once the streams have drained.
-    abandon();
+    abandon(!skipped);
     (void)finish_operation(operation_id);
     if (!skipped) {
       poisoned_ = true;
@@ -1064,12 +1181,9 @@ Error Runtime::run_transaction(const std::vector<AccessSpan>& ranges, uint64_t w
     return body_error;
   }
   trace_.push_back(iv);
+  // Written chunks stay resident and dirty (write-back cache).
   for (ChunkUse& u : chunks)
     if (Error e = release_after(*u.frame, compute_, u.writes)) return e;
-  for (ChunkUse& u : chunks) {
-    if (u.frame->dirty)
-      if (Error e = writeback_and_evict(*u.frame)) return e;
-  }
   ++transactions_in_operation_;
   return finish_operation(operation_id);
 }
@@ -1197,6 +1311,7 @@ Error Runtime::begin_operation() {
                       "the transaction duration guard");
   kernels_in_operation_ = 0;
   transactions_in_operation_ = 0;
+  in_operation_ = true;
   // Entries the previous operation carried over become ordinary clean
   // entries: a consumer still waits for the fill (ready event) and a reuse of
   // the frame still waits for the copy (retire event), so the policy may pick
@@ -1253,7 +1368,10 @@ Error Runtime::finish_operation(uint64_t operation_id) {
     if (f.state == EntryState::h2d_in_flight) move(f, EntryState::resident_clean);
     if (f.state == EntryState::evicting) move(f, EntryState::host_clean);
   }
-  pending_writebacks_.clear();
+  // The D2H stream has drained (or the session is poisoned); the copies' stop
+  // events go back to the pool below, so nothing may refer to them.
+  writebacks_settled();
+  in_operation_ = false;
   bool guard_tripped = false;
   if (!first) {
     FILE* out = nullptr;

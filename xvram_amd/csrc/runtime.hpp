@@ -16,8 +16,18 @@
 // Frames are `frame_bytes` hipMemCreate handles, created lazily up to the
 // budget. A frame is refilled, unmapped or remapped only after the host has
 // seen the hipEvent of its last consumer (kernel, callback work or write-back)
-// complete. Dirty entries are written back before the operation that dirtied
-// them completes; clean entries overlapping written-back bytes are dropped.
+// complete.
+//
+// The cache is write-back (reference runtime.cpp:931-945, 3155-3173): an entry
+// an operation wrote stays resident and dirty after the operation, and its
+// bytes reach host memory only when it is evicted, when an allocation_read or
+// allocation_write overlaps it, when another entry overlapping it is filled,
+// at drain, close or a budget shrink, or when more than half of the pool is
+// dirty and idle (the least recently used half of those is then written back
+// and stays cached, clean). Coherence between overlapping entries: an entry
+// that becomes dirty drops every other cached entry overlapping it (they are
+// stale), and an entry is filled only after every dirty entry overlapping it
+// has been written back.
 //
 // Streams: one compute stream (tile kernels, transaction callbacks), one H2D
 // copy stream and one D2H copy stream, all at the default priority; ordered
@@ -130,6 +140,12 @@ struct Frame {
   // Serial of the operation that started this frame's fill for the operation
   // after it (Runtime::carry_fill); 0 when the frame holds no carried fill.
   uint64_t carry_serial = 0;
+  // Serial of the operation that last wrote the entry (a failed operation
+  // discards only what it wrote itself).
+  uint64_t dirty_serial = 0;
+  // Stop event of a write-back still in flight that left the entry cached: a
+  // later writer of the frame must not overtake the copy.
+  Event writeback_done = nullptr;
 };
 
 // Per-operation intervals for the optional trace file (XVRAM_TRACE_FILE).
@@ -235,13 +251,17 @@ public:
   // `done` must stay unrecorded until the operation ends.
   Error release_after_event(Frame& frame, Event done, bool dirty);
   // Writes a dirty entry back to its host bytes (D2H stream, ordered after the
-  // frame's last consumer), removes it from the cache and drops clean entries
-  // that overlap the written bytes.
-  Error writeback_and_evict(Frame& frame);
+  // frame's last consumer). With `evict` the entry then leaves the cache (and
+  // clean entries overlapping the written bytes are dropped); otherwise it
+  // stays cached, clean (resident_dirty -> writeback_queued -> d2h_in_flight
+  // -> resident_clean).
+  Error writeback(Frame& frame, bool evict);
+  Error writeback_and_evict(Frame& frame) { return writeback(frame, true); }
   // Drops every cached entry of an allocation overlapping [begin, end);
   // used by allocation_write and release.
   Error invalidate(uint64_t allocation_id, uint64_t begin, uint64_t end);
-  // Discards dirty entries without writing them back (failed operation).
+  // Discards the entries the current operation wrote, without writing them
+  // back (a failed operation); unpins everything.
   void discard_dirty();
 
   // ---- working-set transactions and prefetch ----
@@ -317,6 +337,18 @@ private:
   Error wait_retired(Frame& frame);
   Error evict_key(Frame& frame, bool was_dirty);
   Error drop_overlapping(const PanelKey& written, const Frame* except);
+  // Writes back (keeping them cached) the dirty entries overlapping `key`
+  // other than `except`, before `key` is filled; counts the bytes as
+  // write-backs. Fails if such an entry is pinned.
+  Error flush_overlapping(const PanelKey& key, const Frame* except);
+  // Writes back every dirty entry (drain, close); waits for the copies.
+  Error flush_all();
+  // The background flush: when more than half of the pool holds idle dirty
+  // entries written by earlier operations, writes back the least recently
+  // used of them (they stay cached, clean) until a quarter does.
+  Error clean_excess_dirty();
+  // After the host has waited for the D2H stream: no write-back is in flight.
+  void writebacks_settled();
   Error reserve_allocation_va(HostAllocation& a);
   Error ensure_workspace(uint64_t bytes);
   Error plan_chunks(const std::vector<AccessSpan>& ranges, std::vector<ChunkUse>& chunks,
@@ -360,6 +392,7 @@ private:
   std::vector<Event> event_pool_;
   std::vector<Event> events_in_use_;
   uint64_t op_serial_ = 0; // operations begun so far
+  bool in_operation_ = false;
 
   // Fills carried past the current operation (carry_fill): the fence on the
   // H2D stream before the first of them, and where their trace intervals and

@@ -265,7 +265,11 @@ def run_report(lib: Library, m: int, n: int, k: int, op_a: str = "n", op_b: str 
         "set_access_after_map_verified": end.mappings == end.set_access_calls,
         "event_boundaries_verified": end.unsafe_remaps == 0,
         "no_physical_aliases_verified": bool(flags & 2),
-        "dirty_writeback_verified": (end.dirty_evictions == end.writebacks_completed
+        # The reference sets this from writebacks_completed > 0
+        # (src/gemm_bench/executor.cpp:1117); every C byte of every pass must
+        # also have been written back (evicted, or flushed by the verifying read).
+        "dirty_writeback_verified": (end.writebacks_completed > 0
+                                     and end.dirty_evictions <= end.writebacks_completed
                                      and workload["bytes_d2h"] >= m * n * 4 * passes),
         "cache_target_respected": end.resident_bytes_peak <= end.cache_target_maximum_bytes,
         "workspace_bounded": end.workspace_bytes <= workspace_cap_bytes,
