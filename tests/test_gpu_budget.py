@@ -80,7 +80,10 @@ def run(plan):
     op = plan.submit()
     st, info = op.wait()
     assert st == abi.SUCCESS
-    result, message = info.result, op.error().message.decode()
+    e = op.error()
+    result = info.result
+    message = (f"{e.stage.decode()}/{e.operation.decode()} "
+               f"{e.native_name.decode()}:{e.native_code} {e.message.decode()}")
     op.release()
     return result, message
 

@@ -262,6 +262,13 @@ def test_failed_operation_keeps_earlier_outputs(sim):
         run(p1)
         A2, B2 = put(s, ints(big, big, 20)), put(s, ints(big, big, 21))
         C2 = s.allocation(big * big * 4)
+        # Cycle other panels through the frames first, so a frame mapped for a
+        # C2 tile without a load holds stale bytes, not zeros.
+        other = s.allocation(big * big * 4)
+        p0 = xv.GemmPlan(s, xv.matrix(A2, big, big, big), xv.matrix(B2, big, big, big),
+                         xv.matrix(other, big, big, big))
+        run(p0)
+        p0.release()
         # 256^3 tiles: each launch of the host simulation's loop takes tens of ms.
         p2 = xv.GemmPlan(s, xv.matrix(A2, big, big, big), xv.matrix(B2, big, big, big),
                          xv.matrix(C2, big, big, big), deadline_ms=5)
@@ -275,8 +282,17 @@ def test_failed_operation_keeps_earlier_outputs(sim):
             pytest.skip(f"the deadline expired at {where}, before any launch")
         assert 0 < info.units_completed < 8
         np.testing.assert_array_equal(get(C1, m1, n1), a1 @ b1)
+        # Neither C2 tiles the failed GEMM wrote nor those it had mapped ahead
+        # for writing (never written) survive: C2 is its host copy (zeros), so
+        # an accumulating GEMM over it yields exactly A2 B2.
+        p3 = xv.GemmPlan(s, xv.matrix(A2, big, big, big), xv.matrix(B2, big, big, big),
+                         xv.matrix(C2, big, big, big), beta=1.0)
+        run(p3)
+        a2, b2 = ints(big, big, 20), ints(big, big, 21)
+        np.testing.assert_array_equal(get(C2, big, big), a2 @ b2)
         p1.release()
         p2.release()
+        p3.release()
 
 
 def test_background_flush_bounds_idle_dirty_frames(sim):

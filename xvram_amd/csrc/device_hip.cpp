@@ -65,6 +65,9 @@ public:
   int mem_create(uint64_t bytes, uint64_t* handle) override {
     hipMemGenericAllocationHandle_t h{};
     const hipError_t e = hipMemCreate(&h, bytes, &prop_, 0);
+    // The caller handles the failure (out of memory: resample and retry);
+    // leave no error behind for a later hipGetLastError.
+    if (e != hipSuccess) (void)hipGetLastError();
     *handle = reinterpret_cast<uint64_t>(h);
     return e;
   }

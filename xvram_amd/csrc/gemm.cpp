@@ -446,6 +446,10 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   out.lookahead = lookahead;
   out.h2d_bytes_planned = best_h2d;
   out.d2h_bytes_planned = c_bytes;
+  // The block's C tiles, one K panel's A and B panels and the launches
+  // acquired ahead (and the bias frame).
+  out.frames_in_use = std::min<uint64_t>(
+      total_frames, best_gm * best_gn + best_gm + best_gn + 2ull * lookahead + (bias ? 1 : 0));
 
   // Launch order: blocks in a serpentine; K panels alternate direction from
   // block to block so the panels loaded last are the first needed next; inside
@@ -548,6 +552,10 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
                    const GemmHooks& hooks) {
   const CanonProblem& p = plan.problem;
   if (Error e = rt.begin_operation()) return e;
+  if (Error e = rt.make_room(plan.frames_in_use)) {
+    (void)rt.finish_operation(operation_id);
+    return e;
+  }
   std::deque<Acquired> window;
   size_t next = 0;
   const size_t total = plan.launches.size();

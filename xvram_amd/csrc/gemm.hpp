@@ -132,6 +132,7 @@ struct GemmPlanData {
   uint32_t lookahead = 0;                  // launches acquired ahead of the enqueue point
   uint64_t h2d_bytes_planned = 0;          // compulsory traffic of this schedule
   uint64_t d2h_bytes_planned = 0;
+  uint64_t frames_in_use = 0;              // frames the schedule keeps busy at once
   std::vector<TileLaunch> launches;
 };
 

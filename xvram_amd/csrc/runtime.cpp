@@ -507,6 +507,7 @@ Error Runtime::evict_key(Frame& f, bool was_dirty) {
   policy_->erase(f.index);
   f.keyed = false;
   f.dirty = false;
+  f.unwritten = false;
   f.ready_pending = false;
   t_.resident_bytes -= frame_bytes_;
   if (was_dirty) ++t_.dirty_evictions;
@@ -545,7 +546,6 @@ bool Runtime::allocation_streaming(uint64_t allocation_id) {
 // retire records), never on how far the device has progressed, so the
 // accounting of a run is reproducible.
 Error Runtime::select_frame(Frame*& out) {
-  if (Error e = clean_excess_dirty()) return e;
   Frame* free_frame = nullptr;
   Frame* uncreated = nullptr;
   std::vector<VictimCandidate> candidates;
@@ -632,6 +632,7 @@ Error Runtime::fill_entry(Frame& f, const PanelKey& key, uint64_t packed_pitch, 
   t_.resident_bytes += frame_bytes_;
   t_.resident_bytes_peak = std::max(t_.resident_bytes_peak, t_.resident_bytes);
   check_generation(f);
+  f.unwritten = !needs_data;
   if (!needs_data) {
     move(f, EntryState::resident_clean);
     return {};
@@ -797,6 +798,7 @@ Error Runtime::unpin(Frame& f, bool dirty) {
   f.last_use = ++tick_;
   if (!dirty) return {};
   f.dirty = true;
+  f.unwritten = false;
   f.dirty_serial = op_serial_;
   // Other cached copies of these bytes are stale from now on.
   return drop_overlapping(f.key, &f);
@@ -872,20 +874,18 @@ Error Runtime::flush_overlapping(const PanelKey& key, const Frame* except) {
   return {};
 }
 
-// Only entries earlier operations wrote count: the running operation's own
-// outputs follow its schedule (TileLaunch::evict_c), and cleaning a C tile that
-// later K panels still accumulate into would only repeat its copy.
-Error Runtime::clean_excess_dirty() {
+Error Runtime::make_room(uint64_t frames_needed) {
   std::vector<Frame*> idle_dirty;
   for (uint64_t i = 0; i < capacity_; ++i) {
     Frame& f = frames_[i];
     if (f.keyed && f.dirty && f.pins == 0 && f.dirty_serial < op_serial_) idle_dirty.push_back(&f);
   }
-  if (idle_dirty.size() * 2 <= capacity_) return {};
+  const uint64_t spare = capacity_ > frames_needed ? capacity_ - frames_needed : 0;
+  if (idle_dirty.size() <= spare) return {};
   std::sort(idle_dirty.begin(), idle_dirty.end(),
             [](const Frame* x, const Frame* y) { return x->last_use < y->last_use; });
-  const size_t keep = capacity_ / 4;
-  for (size_t i = 0; i + keep < idle_dirty.size(); ++i)
+  const size_t excess = idle_dirty.size() - spare;
+  for (size_t i = 0; i < excess; ++i)
     if (Error e = writeback(*idle_dirty[i], false)) return e;
   return {};
 }
@@ -919,7 +919,10 @@ Error Runtime::invalidate(uint64_t allocation_id, uint64_t begin, uint64_t end) 
 void Runtime::discard_dirty() {
   for (Frame& f : frames_) {
     f.pins = 0;
-    if (f.keyed && f.dirty && f.dirty_serial == op_serial_) (void)evict_key(f, false);
+    if (f.keyed && ((f.dirty && f.dirty_serial == op_serial_) || f.unwritten)) {
+      f.dirty = false;
+      (void)evict_key(f, false);
+    }
   }
 }
 
@@ -1128,6 +1131,7 @@ Error Runtime::run_transaction(const std::vector<AccessSpan>& ranges, uint64_t w
     result = make_error(XVRAM_STATUS_BUDGET_PRESSURE, "transaction", "working_set",
                         "declared working set exceeds the cache target");
   if (!result) result = ensure_workspace(workspace_bytes);
+  if (!result) result = make_room(chunks.size());
   for (size_t i = 0; !result && i < chunks.size(); ++i)
     if (Error e = acquire_chunk(chunks[i])) result = e;
   // Leaves the cache as if the callback had never run: unpins, drops every
@@ -1197,6 +1201,7 @@ Error Runtime::run_prefetch(const std::vector<AccessSpan>& ranges, uint64_t oper
   if (!result && chunks.size() > capacity_)
     result = make_error(XVRAM_STATUS_BUDGET_PRESSURE, "transaction", "prefetch",
                         "prefetch working set exceeds the cache target");
+  if (!result) result = make_room(chunks.size());
   prefetching_ = true; // fills are speculative until a transaction uses them
   for (size_t i = 0; !result && i < chunks.size(); ++i) {
     chunks[i].needs_data = true; // a prefetched chunk must hold valid data

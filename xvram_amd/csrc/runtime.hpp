@@ -22,12 +22,12 @@
 // an operation wrote stays resident and dirty after the operation, and its
 // bytes reach host memory only when it is evicted, when an allocation_read or
 // allocation_write overlaps it, when another entry overlapping it is filled,
-// at drain, close or a budget shrink, or when more than half of the pool is
-// dirty and idle (the least recently used half of those is then written back
-// and stays cached, clean). Coherence between overlapping entries: an entry
-// that becomes dirty drops every other cached entry overlapping it (they are
-// stale), and an entry is filled only after every dirty entry overlapping it
-// has been written back.
+// or at drain, close or a budget shrink. When an operation begins, dirty
+// entries of earlier operations that its schedule will have to evict start
+// their write-back at once (make_room), so the eviction waits for nothing.
+// Coherence between overlapping entries: an entry that becomes dirty drops
+// every other cached entry overlapping it (they are stale), and an entry is
+// filled only after every dirty entry overlapping it has been written back.
 //
 // Streams: one compute stream (tile kernels, transaction callbacks), one H2D
 // copy stream and one D2H copy stream, all at the default priority; ordered
@@ -143,6 +143,10 @@ struct Frame {
   // Serial of the operation that last wrote the entry (a failed operation
   // discards only what it wrote itself).
   uint64_t dirty_serial = 0;
+  // Mapped for an output without loading its bytes and not written yet: its
+  // contents are garbage until the consumer writes them (dropped if the
+  // operation fails first).
+  bool unwritten = false;
   // Stop event of a write-back still in flight that left the entry cached: a
   // later writer of the frame must not overtake the copy.
   Event writeback_done = nullptr;
@@ -261,7 +265,8 @@ public:
   // used by allocation_write and release.
   Error invalidate(uint64_t allocation_id, uint64_t begin, uint64_t end);
   // Discards the entries the current operation wrote, without writing them
-  // back (a failed operation); unpins everything.
+  // back, and those it mapped for output but never wrote (a failed
+  // operation); unpins everything.
   void discard_dirty();
 
   // ---- working-set transactions and prefetch ----
@@ -272,6 +277,12 @@ public:
   // ---- operation bracketing ----
   // Marks the start of an operation: every stream is ordered after it.
   Error begin_operation();
+  // Called when an operation begins with the number of frames its schedule
+  // keeps in use: idle dirty entries written by earlier operations that do
+  // not fit beside them will be evicted during the operation, so their
+  // write-back (least recently used first) starts now and the eviction finds
+  // them clean. The entries stay cached until then.
+  Error make_room(uint64_t frames_needed);
   // Live budget (reference refresh_budget, runtime.cpp:3213-3468): samples
   // hipMemGetInfo at most every budget_poll_ms (always when forced), shrinks
   // the frame pool at once when the safe target falls (writing back and
@@ -343,10 +354,6 @@ private:
   Error flush_overlapping(const PanelKey& key, const Frame* except);
   // Writes back every dirty entry (drain, close); waits for the copies.
   Error flush_all();
-  // The background flush: when more than half of the pool holds idle dirty
-  // entries written by earlier operations, writes back the least recently
-  // used of them (they stay cached, clean) until a quarter does.
-  Error clean_excess_dirty();
   // After the host has waited for the D2H stream: no write-back is in flight.
   void writebacks_settled();
   Error reserve_allocation_va(HostAllocation& a);

@@ -300,6 +300,11 @@ int launch_sgemm(const SgemmLaunch& launch, void* stream) {
       (launch.ldb % 4 == 0) && (launch.ldc % 4 == 0) && launch.padded;
   if (launch.m <= 0 || launch.n <= 0 || launch.k <= 0 || !aligned)
     return static_cast<int>(hipErrorInvalidValue);
+  // The launch's own error is read back with hipGetLastError below, which also
+  // returns an error an earlier runtime call on this thread left behind (an
+  // out-of-memory hipMemCreate the cache already handled, for one): consume
+  // that first so it is not reported as a launch failure.
+  (void)hipGetLastError();
   Params p;
   p.a = launch.a;
   p.b = launch.b;
