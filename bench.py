@@ -306,6 +306,65 @@ def cpu_baseline(a_seeded, b_seeded, m, n, k, seconds):
     return out
 
 
+def cpu_sweep(seconds: float) -> dict:
+    """The reference's CPU GEMM (examples/preview-gemm/main.cpp:107-119, the
+    oracle's FP64 loop) on every BASELINE configuration, in its two forms: all
+    host threads and one thread. A form whose full problem would take more
+    than about `seconds` is timed on a leading column subset of the same
+    product and extrapolated linearly in the column count (labelled so)."""
+    import oracle
+    from oracle.sample import SeededOperand
+
+    threads = os.cpu_count() or 1
+    configs = [("C1 1024^3 NN", 1024, 1024, 1024, OP_N, OP_N, 1.0, 0.0)]
+    for oa, ob in ((OP_N, OP_N), (OP_N, OP_T), (OP_T, OP_N), (OP_T, OP_T)):
+        configs.append((f"C2 3001x2047x4099 {'NT'[oa]}{'NT'[ob]}", 3001, 2047, 4099, oa, ob, 1.5,
+                        0.5))
+    for size in (4096, 8192, 16384):
+        for ob in (OP_N, OP_T):
+            configs.append((f"C3 {size}^3 N{'NT'[ob]}", size, size, size, OP_N, ob, 1.0, 0.0))
+    configs.append(("C4 32768^3 NT", 32768, 32768, 32768, OP_N, OP_T, 1.0, 0.0))
+    configs.append(("NS 65536^3 NT", 65536, 65536, 65536, OP_N, OP_T, 1.0, 0.0))
+    out = {"cpu_model": cpu_model(), "nproc": os.cpu_count(), "threads_all": threads,
+           "unit": "TFLOP/s", "configs": []}
+    for name, m, n, k, oa, ob, alpha, beta in configs:
+        a = SeededOperand(11, *((m, k) if oa == OP_N else (k, m)), oa == OP_T)
+        b = SeededOperand(12, *((k, n) if ob == OP_N else (n, k)), ob == OP_T)
+        rows = min(m, 1024) if m * k > (1 << 28) else m   # large A: a row block
+        a_s = a.rows(range(rows)) if rows < m else a.full()
+        c0 = None
+        if beta != 0.0:
+            c0 = SeededOperand(13, m, n, False).full()[:rows, :]
+        entry = {"config": name}
+        for label, nthreads in (("all_threads", threads), ("one_thread", 1)):
+            cols = min(n, 2 * nthreads)
+            t = time.perf_counter()
+            oracle.sgemm_f64(a_s, b.cols(range(cols)), alpha, beta,
+                             None if c0 is None else np.asfortranarray(c0[:, :cols]),
+                             threads=nthreads)
+            probe = max(time.perf_counter() - t, 1e-4)
+            full_cols = n if rows == m else None
+            want = int(min(n, max(cols, cols * seconds / probe)))
+            if want > cols:
+                t = time.perf_counter()
+                oracle.sgemm_f64(a_s, b.cols(range(want)), alpha, beta,
+                                 None if c0 is None else np.asfortranarray(c0[:, :want]),
+                                 threads=nthreads)
+                secs, cols = time.perf_counter() - t, want
+            else:
+                secs = probe
+            rate = 2.0 * rows * cols * k / secs / 1e12
+            whole = full_cols is not None and cols == n
+            entry[label] = {"value": round(rate, 6), "threads": nthreads,
+                            "sample": f"C[0:{rows}, 0:{cols}] with full K ({secs:.2f} s)",
+                            "extrapolated": not whole,
+                            "full_problem_s": round(2.0 * m * n * k / (rate * 1e12), 1)}
+        log(f"cpu sweep {name}: {entry['all_threads']['value']} TFLOP/s on {threads} threads, "
+            f"{entry['one_thread']['value']} on one")
+        out["configs"].append(entry)
+    return out
+
+
 # ---- config 5: the inference chain ---------------------------------------------------
 
 def run_chain(args, xv, lib, synth, link) -> int:
@@ -505,7 +564,13 @@ def main() -> int:
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run 4 device-to-device copies of BYTES (a plain copy kernel of "
                          "known size, used to scale rocprofv3 FETCH_SIZE/WRITE_SIZE) and exit")
+    ap.add_argument("--cpu-sweep", action="store_true",
+                    help="only time the CPU reference GEMM (both forms) on every BASELINE "
+                         "configuration and print it as one JSON line (no GPU)")
     args = ap.parse_args()
+    if args.cpu_sweep:
+        print(json.dumps(cpu_sweep(args.cpu_seconds)), flush=True)
+        return 0
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return 0

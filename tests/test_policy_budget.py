@@ -20,7 +20,7 @@ import xvram_amd as xv
 from generators import CLEAN, DIRTY, DROP, ERASE, INSERT, NONE, SELECT, SET, TOUCH
 from xvram_amd import abi
 
-from gemm_cases import Problem, uniform
+from gemm_cases import Problem, pattern_operands, uniform
 
 KiB = 1 << 10
 
@@ -232,3 +232,48 @@ def test_both_policies_give_identical_results_out_of_core(sim, oracle_mod, polic
         assert t.clean_evictions > 0 and t.unsafe_transitions == 0
     ref, absab = prob.reference(oracle_mod)
     assert oracle_mod.check_bound(out, k, ref, absab)[0] == 0
+
+
+def test_out_of_memory_in_a_gemm_then_recovery(sim, oracle_mod):
+    """The GPU scenario of tests/test_gpu_budget.py on the host simulation:
+    memory runs out while a GEMM creates its frames, the forced resample
+    cannot shrink under the frames the GEMM holds (BUDGET_PRESSURE, no
+    poison); once memory is back the same session computes the product
+    exactly, and the frame whose creation failed is reused through legal
+    state transitions only."""
+    sim.dll.xvram_hostsim_set_memory(64 * F, 64 * F)
+    s = xv.Session(sim, chunk_size_bytes=F, cache_target_bytes=16 * F, workspace_cap_bytes=0,
+                   device_headroom_bytes=2 * F, budget_poll_ms=10 ** 9)
+    try:
+        m = n = k = 256
+        a_op, b_op = pattern_operands(m, n, k)
+        a, b, c = s.allocation(m * k * 4), s.allocation(k * n * 4), s.allocation(m * n * 4)
+        a.write(np.asfortranarray(a_op).T.copy())
+        b.write(np.asfortranarray(b_op).T.copy())
+
+        def plan():
+            return xv.GemmPlan(s, xv.matrix(a, m, k, m), xv.matrix(b, k, n, k),
+                               xv.matrix(c, m, n, m))
+
+        p = plan()
+        assert p.info().tile_count > 8
+        sim.dll.xvram_hostsim_set_memory(5 * F, 64 * F)  # room for five frames
+        with pytest.raises(xv.XvramError) as e:
+            p.execute()
+        assert e.value.status == abi.BUDGET_PRESSURE
+        t = s.telemetry()
+        assert t.target_oom_retries == 1 and t.budget_shrinks == 0 and t.poisoned == 0
+        assert t.physical_handles_created == 5
+        p.release()
+        sim.dll.xvram_hostsim_set_memory(59 * F, 64 * F)  # the memory is back
+        p = plan()
+        p.execute()
+        out = np.asfortranarray(c.read(dtype=np.float32).reshape(n, m).T)
+        assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))
+        p.release()
+        s.close()
+        t = s.telemetry()
+        assert t.unsafe_transitions == 0 and t.unsafe_remaps == 0
+        assert t.physical_handles_created == t.physical_handles_released
+    finally:
+        s.release()

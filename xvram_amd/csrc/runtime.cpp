@@ -703,10 +703,18 @@ Error Runtime::acquire(const PanelKey& key, uint64_t packed_pitch, bool needs_da
   if (Error e = flush_overlapping(key, nullptr)) return e;
   Frame* f = nullptr;
   if (Error e = select_frame(f)) return e;
-  if (Error e = map_frame_at(*f, f->slot)) return e;
+  if (Error e = map_frame_at(*f, f->slot)) return abandon_mapping(*f, e);
   if (Error e = fill_entry(*f, key, packed_pitch, needs_data)) return e;
   out = f;
   return {};
+}
+
+// A frame select_frame handed out (state mapping) could not be mapped: it
+// goes back to host_clean, so a later selection starts from a legal state.
+Error Runtime::abandon_mapping(Frame& f, Error e) {
+  if (f.state == EntryState::mapping) move(f, EntryState::host_clean);
+  if (!f.handle) f.used_before = false; // its handle was never created
+  return e;
 }
 
 // The carried entry is inserted like any executor fill (not as a speculative
@@ -753,7 +761,7 @@ Error Runtime::acquire_pieces(const PanelKey& key, uint64_t packed_pitch,
   if (Error e = flush_overlapping(key, nullptr)) return e;
   Frame* f = nullptr;
   if (Error e = select_frame(f)) return e;
-  if (Error e = map_frame_at(*f, f->slot)) return e;
+  if (Error e = map_frame_at(*f, f->slot)) return abandon_mapping(*f, e);
   if (Error e = fill_entry(*f, key, packed_pitch, true, &pieces, &piece_ready)) return e;
   out = f;
   return {};
@@ -1110,7 +1118,7 @@ Error Runtime::acquire_chunk(ChunkUse& use) {
   }
   if (!f)
     if (Error e = select_frame(f)) return e;
-  if (Error e = map_frame_at(*f, address)) return e;
+  if (Error e = map_frame_at(*f, address)) return abandon_mapping(*f, e);
   use.frame = f;
   use.filled_empty = !use.needs_data;
   return fill_entry(*f, key, key.width, use.needs_data);

@@ -337,6 +337,7 @@ private:
   void adopt_retire(Frame& frame, Event done);
   Error unpin(Frame& frame, bool dirty);
   Error map_frame_at(Frame& frame, uint64_t address);
+  Error abandon_mapping(Frame& frame, Error error);
   Error unmap_frame(Frame& frame);
   Error select_frame(Frame*& out);
   bool allocation_hot(uint64_t allocation_id);
