@@ -17,10 +17,13 @@ runs -- the resident config-3 workloads keep C cached between executions, as a
 caller repeating a resident GEMM sees it -- and the drain writes back the
 rest). ``ms_per_step`` = the timed region / K. ``roofline`` describes the dominant
 kernel (the FP32-MFMA tile kernel): algorithmic FLOPs of its launches divided
-by their summed duration, both from the HIP events attached to every kernel
-dispatch on the library's compute stream (trace file written by the library);
-``kernel_ms_per_launch`` is that kernel time per tile launch of the plan (an
-operation's first launch may run as several K-slice kernels). Other workloads:
+by the time the kernels ran (the union of their intervals, from the HIP events
+attached to every kernel dispatch on the library's compute lanes; trace file
+written by the library). Launches of a few ms alternate between two compute
+lanes and overlap at their ends, so there the union, not the sum of the
+per-launch durations, is the kernels' time (``kernel_overlap_ms`` reports the
+difference); ``kernel_ms_per_launch`` is that time per tile launch of the plan
+(an operation's first launch may run as several K-slice kernels). Other workloads:
 ``--workload`` (config 3's resident sweep, config 4, the config-5 chain).
 ``cpu_baseline`` times the FP64 reference loop (the oracle's restatement of
 the reference's CPU GEMM) on a bounded sample of the same product, on all host
@@ -494,7 +497,7 @@ def run_chain(args, xv, lib, synth, link) -> int:
     d2h_compulsory = batch * width * 4
     t_roof = max(flops / (FP32_MFMA_PEAK_TFLOPS * 1e12), h2d_compulsory / (link["h2d_gbps"] * 1e9),
                  d2h_compulsory / (link["d2h_gbps"] * 1e9))
-    kernel_tflops = flops * args.steps / (stats["kernel_ms_total"] * 1e-3) / 1e12
+    kernel_tflops = flops * args.steps / (stats["kernel_busy_ms"] * 1e-3) / 1e12
     h2d_gbps = stats["h2d_gbps_while_copying"]
     result = {
         "metric": "config-5 inference chain FP32 TFLOP/s (8 x Linear 16384 + bias + ReLU, "
@@ -650,7 +653,7 @@ def main() -> int:
     flops = 2.0 * m * n * k
     step_s = total_s / args.steps  # the final drain is shared by the steps
     value = flops / step_s / 1e12
-    kernel_tflops = flops * args.steps / (stats["kernel_ms_total"] * 1e-3) / 1e12
+    kernel_tflops = flops * args.steps / (stats["kernel_busy_ms"] * 1e-3) / 1e12
     # Tile launches of the plan; an operation's first launch may run as several
     # K-slice kernels (cache-miss start), so kernels per step can be higher.
     launches_per_step = info.tile_count
@@ -734,7 +737,8 @@ def main() -> int:
                             m * n * 4 / (link["d2h_gbps"] * 1e9)),
             "frac": None,
         },
-        "kernel_ms_per_launch": round(stats["kernel_ms_total"] / max(1, launches_per_step * args.steps), 4),
+        "kernel_ms_per_launch": round(stats["kernel_busy_ms"] / max(1, launches_per_step * args.steps), 4),
+        "kernel_overlap_ms_per_step": round((stats["kernel_ms_total"] - stats["kernel_busy_ms"]) / args.steps, 3),
         "cache": {f: getattr(tele1, f) - getattr(tele0, f) for f in (
             "bytes_h2d", "bytes_d2h", "cache_hits", "cache_misses", "clean_evictions",
             "dirty_evictions", "writebacks_completed", "handle_reuses", "event_boundaries")},

@@ -461,6 +461,10 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
       total > 100000000ull)
     return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "gemm", "make_plan", "too_many_tiles");
   out.launches.reserve(total);
+  out.lanes = 2.0 * static_cast<double>(tm) * static_cast<double>(tn) * static_cast<double>(bk) <=
+                      kDualLaneMaxFlops
+                  ? 2
+                  : 1;
   uint64_t block_seq = 0;
   for (uint64_t bi = 0; bi < blocks_m; ++bi) {
     for (uint64_t s = 0; s < blocks_n; ++s, ++block_seq) {
@@ -479,6 +483,10 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
             l.first_panel = q == 0;
             l.last_panel = q + 1 == out.panels_k;
             l.evict_c = l.last_panel && block_seq + 1 < blocks_m * blocks_n;
+            // Consecutive launches in a K panel are different C tiles of the
+            // block: alternate lanes by the tile's place in the block.
+            const uint64_t place = (i - i_begin) * (j_end - j_begin) + (j - j_begin);
+            l.lane = static_cast<uint8_t>(out.lanes > 1 ? place % 2 : 0);
             out.launches.push_back(l);
           }
         }
@@ -571,7 +579,8 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     key.height = 1;
     key.pitch = key.width;
     Error e = rt.acquire(key, round_up(key.width, 16), true, bias);
-    if (!e) e = rt.wait_ready(*bias, rt.compute_stream());
+    for (int lane = 0; !e && lane < plan.lanes; ++lane)
+      e = rt.wait_ready(*bias, rt.compute_stream(lane));
     if (e) {
       if (bias) (void)rt.release_after(*bias, rt.compute_stream(), false);
       (void)rt.finish_operation(operation_id);
@@ -636,7 +645,8 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     const PanelGeom ag = a_geom(p.a, g.i0, g.h, g.p0, g.w);
     const PanelGeom bg = b_geom(p.b, g.p0, g.w, g.j0, g.g);
     const PanelGeom cg = c_geom(g.i0, g.h, g.j0, g.g);
-    Stream cs = rt.compute_stream();
+    const int lane = l.lane;
+    Stream cs = rt.compute_stream(lane);
     // Whole-panel fills are waited for up front; sliced ones slice by slice.
     if (Error e = rt.wait_ready(*acq.c, cs)) { result = e; break; }
     if (acq.a_ready.empty())
@@ -714,9 +724,9 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     if (!acq.b_ready.empty())
       if (Error e = rt.wait_ready(*acq.b, cs)) { result = e; break; }
     rt.note_kernel_launched(); // one tile, however many slices
-    if (Error e = rt.release_after_event(*acq.a, done, false)) { result = e; break; }
-    if (Error e = rt.release_after_event(*acq.b, done, false)) { result = e; break; }
-    if (Error e = rt.release_after_event(*acq.c, done, true)) { result = e; break; }
+    if (Error e = rt.release_after_event(*acq.a, done, false, lane)) { result = e; break; }
+    if (Error e = rt.release_after_event(*acq.b, done, false, lane)) { result = e; break; }
+    if (Error e = rt.release_after_event(*acq.c, done, true, lane)) { result = e; break; }
     if (l.evict_c) {
       if (Error e = rt.writeback_and_evict(*acq.c)) {
         result = e;
@@ -731,7 +741,7 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
       }
     }
   }
-  if (bias && !result) result = rt.release_after(*bias, rt.compute_stream(), false);
+  if (bias && !result) result = rt.release_after_lanes(*bias);
   if (!result && hooks.tail) result = hooks.tail();
   if (result) {
     // Unpin what was acquired ahead, drop partial C panels, drain the device.

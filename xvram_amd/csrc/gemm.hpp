@@ -122,6 +122,7 @@ struct TileLaunch {
   // blocks' tiles need its frame, so it is written back and evicted as soon
   // as this launch is enqueued. The last block's tiles stay resident, dirty.
   bool evict_c = false;
+  uint8_t lane = 0; // compute lane (Runtime::compute_stream); one lane per C tile
 };
 
 struct GemmPlanData {
@@ -133,8 +134,16 @@ struct GemmPlanData {
   uint64_t h2d_bytes_planned = 0;          // compulsory traffic of this schedule
   uint64_t d2h_bytes_planned = 0;
   uint64_t frames_in_use = 0;              // frames the schedule keeps busy at once
+  int lanes = 1;                           // compute lanes the launches alternate over
   std::vector<TileLaunch> launches;
 };
+
+// Launches of at most this many FLOPs (a few ms) alternate between the two
+// compute lanes: a short launch's fixed costs (its last workgroups' C tile
+// write, the next launch's dispatch and first loads) are then overlapped by
+// the neighbouring launch. Longer launches stay on one lane, where each
+// launch's HIP-event duration is its own run time.
+constexpr double kDualLaneMaxFlops = 2.0e11;
 
 // Floating-point rate assumed when sizing launches against the transaction
 // duration guard: well under the tile kernel's sustained FP32 rate, so a launch

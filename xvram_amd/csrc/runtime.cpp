@@ -145,6 +145,7 @@ Error Runtime::setup() {
     frames_[i].slot = arena_ + i * frame_bytes_;
   }
   if (int rc = device_->stream_create(&compute_)) return device_failure(rc, "setup", "stream");
+  if (int rc = device_->stream_create(&compute2_)) return device_failure(rc, "setup", "stream");
   if (int rc = device_->stream_create(&h2d_)) return device_failure(rc, "setup", "stream");
   if (int rc = device_->stream_create(&d2h_)) return device_failure(rc, "setup", "stream");
   if (int rc = device_->event_create(&op_start_)) return device_failure(rc, "setup", "event");
@@ -161,7 +162,7 @@ Error Runtime::drain() {
   if (!setup_done_ || closed_) return {};
   if (!poisoned_)
     if (Error e = flush_all()) return e;
-  for (Stream s : {h2d_, compute_, d2h_})
+  for (Stream s : {h2d_, compute_, compute2_, d2h_})
     if (int rc = device_->stream_sync(s)) return device_failure(rc, "drain", "stream_sync");
   writebacks_settled();
   return {};
@@ -214,7 +215,7 @@ Error Runtime::close() {
   for (Frame& f : frames_) f.pins = 0;
   if (!poisoned_)
     if (Error e = flush_all(); e && !first) first = e;
-  for (Stream s : {h2d_, compute_, d2h_})
+  for (Stream s : {h2d_, compute_, compute2_, d2h_})
     if (s) note(device_->stream_sync(s), "stream_sync");
   for (Frame& f : frames_) {
     if (f.keyed) {
@@ -256,9 +257,9 @@ Error Runtime::close() {
   if (op_start_) device_->event_destroy(op_start_);
   if (carry_fence_) device_->event_destroy(carry_fence_);
   op_start_ = carry_fence_ = nullptr;
-  for (Stream s : {h2d_, compute_, d2h_})
+  for (Stream s : {h2d_, compute_, compute2_, d2h_})
     if (s) device_->stream_destroy(s);
-  compute_ = h2d_ = d2h_ = nullptr;
+  compute_ = compute2_ = h2d_ = d2h_ = nullptr;
   for (auto& [id, a] : allocations_) {
     if (a.va) note(device_->va_free(a.va, a.va_bytes), "va_free");
     device_->host_free(a.host);
@@ -472,6 +473,14 @@ void Runtime::adopt_retire(Frame& f, Event done) {
   ++f.generation;
 }
 
+// A kernel on compute lane `lane` used the frame: it retires after it, and
+// after the last kernel on the other lane that used it.
+void Runtime::adopt_lane(Frame& f, Event done, int lane) {
+  adopt_retire(f, done);
+  f.lane_ref[lane] = done;
+  f.lane_pending[lane] = true;
+}
+
 Error Runtime::unmap_frame(Frame& f) {
   if (!f.mapped_at) return {};
   if (Error e = wait_retired(f)) return e;
@@ -493,6 +502,13 @@ Error Runtime::wait_retired(Frame& f) {
     if (int rc = device_->event_sync(f.retire_ref)) return device_failure(rc, "cache", "event_sync");
   } else if (q != 0) {
     return device_failure(q, "cache", "event_query");
+  }
+  // The other compute lane's last use may finish later than retire_ref.
+  for (int lane = 0; lane < kLanes; ++lane) {
+    if (!f.lane_pending[lane]) continue;
+    if (f.lane_ref[lane] != f.retire_ref)
+      if (int rc = device_->event_sync(f.lane_ref[lane])) return device_failure(rc, "cache", "event_sync");
+    f.lane_pending[lane] = false;
   }
   f.retire_pending = false;
   f.completed = f.generation;
@@ -790,11 +806,26 @@ Error Runtime::release_after(Frame& f, Stream stream, bool dirty) {
   return unpin(f, dirty);
 }
 
-Error Runtime::release_after_event(Frame& f, Event done, bool dirty) {
+Error Runtime::release_after_event(Frame& f, Event done, bool dirty, int lane) {
   if (f.pins <= 0) return make_error(XVRAM_STATUS_INTERNAL, "cache", "release", "frame is not pinned");
   if (!done) return make_error(XVRAM_STATUS_INTERNAL, "cache", "release", "no retire event");
-  adopt_retire(f, done);
+  if (lane < 0 || lane >= kLanes)
+    return make_error(XVRAM_STATUS_INTERNAL, "cache", "release", "no such compute lane");
+  adopt_lane(f, done, lane);
   return unpin(f, dirty);
+}
+
+Error Runtime::release_after_lanes(Frame& f) {
+  if (f.pins <= 0) return make_error(XVRAM_STATUS_INTERNAL, "cache", "release", "frame is not pinned");
+  Event e1 = nullptr;
+  if (Error e = take_event(e1)) return e;
+  if (int rc = device_->event_record(e1, compute2_)) return device_failure(rc, "cache", "record");
+  if (Error e = record_retire(f, compute_)) return e;
+  f.lane_ref[0] = f.retire;
+  f.lane_pending[0] = true;
+  f.lane_ref[1] = e1;
+  f.lane_pending[1] = true;
+  return unpin(f, false);
 }
 
 Error Runtime::unpin(Frame& f, bool dirty) {
@@ -839,6 +870,10 @@ Error Runtime::writeback(Frame& f, bool evict) {
   if (f.retire_pending)
     if (int rc = device_->stream_wait_event(d2h_, f.retire_ref))
       return device_failure(rc, "cache", "stream_wait");
+  for (int lane = 0; lane < kLanes; ++lane)
+    if (f.lane_pending[lane] && f.lane_ref[lane] != f.retire_ref)
+      if (int rc = device_->stream_wait_event(d2h_, f.lane_ref[lane]))
+        return device_failure(rc, "cache", "stream_wait");
   move(f, EntryState::writeback_queued);
   TraceInterval iv;
   iv.kind = 'd';
@@ -1341,7 +1376,7 @@ Error Runtime::begin_operation() {
   events_in_use_.insert(events_in_use_.end(), carried_events_.begin(), carried_events_.end());
   carried_events_.clear();
   if (int rc = device_->event_record(op_start_, compute_)) return device_failure(rc, "operation", "record");
-  for (Stream s : {h2d_, d2h_})
+  for (Stream s : {h2d_, d2h_, compute2_})
     if (int rc = device_->stream_wait_event(s, op_start_)) return device_failure(rc, "operation", "wait");
   return {};
 }
@@ -1357,7 +1392,7 @@ Error Runtime::record_kernel(Event& start, Event& stop) {
 // max_transaction_ms blocks further launches and fails with a timeout).
 Error Runtime::finish_operation(uint64_t operation_id) {
   Error first;
-  for (Stream s : {compute_, d2h_}) {
+  for (Stream s : {compute_, compute2_, d2h_}) {
     if (int rc = device_->stream_sync(s)) {
       if (!first) first = device_failure(rc, "operation", "stream_sync");
     }
@@ -1377,6 +1412,7 @@ Error Runtime::finish_operation(uint64_t operation_id) {
     // boundary for each frame that still had one outstanding).
     if (f.retire_pending) ++t_.event_boundaries;
     f.retire_pending = false;
+    f.lane_pending[0] = f.lane_pending[1] = false;
     f.completed = f.generation;
     if (f.state == EntryState::h2d_in_flight) move(f, EntryState::resident_clean);
     if (f.state == EntryState::evicting) move(f, EntryState::host_clean);

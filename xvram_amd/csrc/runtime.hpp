@@ -29,9 +29,11 @@
 // every other cached entry overlapping it (they are stale), and an entry is
 // filled only after every dirty entry overlapping it has been written back.
 //
-// Streams: one compute stream (tile kernels, transaction callbacks), one H2D
-// copy stream and one D2H copy stream, all at the default priority; ordered
-// with events only.
+// Streams: two compute lanes (tile kernels; lane 0 also runs transaction
+// callbacks), one H2D copy stream and one D2H copy stream, all at the default
+// priority; ordered with events only. Short tile launches alternate between
+// the lanes so one launch's tail and the next one's start overlap; every
+// launch of one C tile stays on one lane.
 #pragma once
 
 #include <cstdint>
@@ -150,6 +152,11 @@ struct Frame {
   // Stop event of a write-back still in flight that left the entry cached: a
   // later writer of the frame must not overtake the copy.
   Event writeback_done = nullptr;
+  // The last kernel on each compute lane that used the frame (pending until
+  // the host has seen it complete): launches on the two lanes finish in any
+  // order, so the frame is reused only after both.
+  Event lane_ref[2] = {nullptr, nullptr};
+  bool lane_pending[2] = {false, false};
 };
 
 // Per-operation intervals for the optional trace file (XVRAM_TRACE_FILE).
@@ -225,7 +232,8 @@ public:
   uint64_t granularity() const { return granularity_; }
   const RuntimeConfig& config() const { return config_; }
   bool poisoned() const { return poisoned_; }
-  Stream compute_stream() const { return compute_; }
+  static constexpr int kLanes = 2;
+  Stream compute_stream(int lane = 0) const { return lane == 0 ? compute_ : compute2_; }
 
   // ---- allocations (authoritative pinned host copies) ----
   Error allocate(uint64_t bytes, uint64_t alignment, uint32_t priority, HostAllocation*& out);
@@ -251,9 +259,12 @@ public:
   // Unpins after the consumer enqueued on `stream`; records the retire event.
   Error release_after(Frame& frame, Stream stream, bool dirty);
   // Unpins after a consumer whose completion `done` already marks (the stop
-  // event of a tile launch, recorded by its dispatch): no event is recorded.
-  // `done` must stay unrecorded until the operation ends.
-  Error release_after_event(Frame& frame, Event done, bool dirty);
+  // event of a tile launch on compute lane `lane`, recorded by its dispatch):
+  // no event is recorded. `done` must stay unrecorded until the operation ends.
+  Error release_after_event(Frame& frame, Event done, bool dirty, int lane = 0);
+  // Unpins after work enqueued on both compute lanes (a frame every launch of
+  // an operation reads, such as a bias vector).
+  Error release_after_lanes(Frame& frame);
   // Writes a dirty entry back to its host bytes (D2H stream, ordered after the
   // frame's last consumer). With `evict` the entry then leaves the cache (and
   // clean entries overlapping the written bytes are dropped); otherwise it
@@ -335,6 +346,7 @@ private:
   void check_generation(const Frame& frame);
   Error record_retire(Frame& frame, Stream stream);
   void adopt_retire(Frame& frame, Event done);
+  void adopt_lane(Frame& frame, Event done, int lane);
   Error unpin(Frame& frame, bool dirty);
   Error map_frame_at(Frame& frame, uint64_t address);
   Error abandon_mapping(Frame& frame, Error error);
@@ -394,6 +406,7 @@ private:
   uint64_t workspace_handle_ = 0;
 
   Stream compute_ = nullptr;
+  Stream compute2_ = nullptr; // compute lane 1
   Stream h2d_ = nullptr;
   Stream d2h_ = nullptr;
   Event op_start_ = nullptr;
