@@ -71,9 +71,89 @@ __device__ __forceinline__ void tile_coords(const Params& p, int& tm, int& tn) {
 // C = alpha*acc + beta*C (C not read when beta == 0), then + bias_row[i] +
 // bias_col[j], then ReLU (NaN kept: v < 0 is false). Only in-range elements
 // are touched.
-template <int kNJ>
+//
+// A wave whose whole 128 x 32*kNJ region lies inside C takes the interior path:
+// no per-element bounds, and the loads of old C (beta != 0), of the column
+// biases and of the row biases are issued in batches before any is used, so
+// the wave waits for memory once per kBatch columns of its lane instead of
+// once per float4 (a serial chain of 16*kNJ round trips that every workgroup of
+// a launch would otherwise run at the same moment). Same arithmetic, in the
+// same order, as the general path. Row biases are loaded ahead only with
+// kRowBiasAhead (64 more registers: the 256 x 256 kernels have them, the
+// 256 x 128 kernel at two workgroups per CU does not). store_c_tile uses
+// batches of one column (two would make the kernels that also compile the
+// general path spill); kernels whose tiles are all interior call
+// store_c_interior directly.
+template <int kNJ, int kBatch, bool kRowBiasAhead>
+__device__ __forceinline__ void store_c_interior(const Params& p, const float16_t (&acc)[4][kNJ],
+                                                 int row0, int col0, int lrow, int lhalf) {
+  const bool read_c = p.beta != 0.f;
+  const bool extra = p.bias_row != nullptr || p.bias_col != nullptr || p.relu != 0;
+  const auto row_of = [&](int v) { return row0 + 4 * (8 * (v >> 2) + 4 * lhalf + (v & 3)); };
+  float brow[16][4];
+  if (kRowBiasAhead && p.bias_row != nullptr) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) brow[v][t] = p.bias_row[row_of(v) + t];
+  }
+  const auto finish = [&](float v, int vi, int t, float bias_c) {
+    if (p.bias_row != nullptr) v += kRowBiasAhead ? brow[vi][t] : p.bias_row[row_of(vi) + t];
+    v += bias_c;
+    return (p.relu != 0 && v < 0.f) ? 0.f : v;
+  };
+  static_assert(kNJ % kBatch == 0, "columns come in whole batches");
+#pragma unroll
+  for (int j0 = 0; j0 < kNJ; j0 += kBatch) {
+    float4 old[kBatch][16];
+    float bias_c[kBatch];
+#pragma unroll
+    for (int jb = 0; jb < kBatch; ++jb) {
+      const int col = col0 + kNJ * lrow + j0 + jb;
+      bias_c[jb] = p.bias_col != nullptr ? p.bias_col[col] : 0.f;
+      if (read_c) {
+        const float* cline = p.c + (int64_t)col * p.ldc;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) old[jb][v] = *reinterpret_cast<const float4*>(cline + row_of(v));
+      }
+    }
+#pragma unroll
+    for (int jb = 0; jb < kBatch; ++jb) {
+      const int j = j0 + jb;
+      float* cline = p.c + (int64_t)(col0 + kNJ * lrow + j) * p.ldc;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        float4 r;
+        if (read_c) {
+          r.x = p.alpha * acc[0][j][v] + p.beta * old[jb][v].x;
+          r.y = p.alpha * acc[1][j][v] + p.beta * old[jb][v].y;
+          r.z = p.alpha * acc[2][j][v] + p.beta * old[jb][v].z;
+          r.w = p.alpha * acc[3][j][v] + p.beta * old[jb][v].w;
+        } else {
+          r.x = p.alpha * acc[0][j][v];
+          r.y = p.alpha * acc[1][j][v];
+          r.z = p.alpha * acc[2][j][v];
+          r.w = p.alpha * acc[3][j][v];
+        }
+        if (extra) {
+          r.x = finish(r.x, v, 0, bias_c[jb]);
+          r.y = finish(r.y, v, 1, bias_c[jb]);
+          r.z = finish(r.z, v, 2, bias_c[jb]);
+          r.w = finish(r.w, v, 3, bias_c[jb]);
+        }
+        *reinterpret_cast<float4*>(cline + row_of(v)) = r;
+      }
+    }
+  }
+}
+
+template <int kNJ, bool kRowBiasAhead>
 __device__ __forceinline__ void store_c_tile(const Params& p, const float16_t (&acc)[4][kNJ],
                                              int row0, int col0, int lrow, int lhalf) {
+  if (row0 + 128 <= p.m && col0 + 32 * kNJ <= p.n) {
+    store_c_interior<kNJ, 1, kRowBiasAhead>(p, acc, row0, col0, lrow, lhalf);
+    return;
+  }
   const bool read_c = p.beta != 0.f;
   const bool extra = p.bias_row != nullptr || p.bias_col != nullptr || p.relu != 0;
   const auto finish = [&](float v, int r, float bias_c) {

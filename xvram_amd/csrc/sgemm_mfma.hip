@@ -263,7 +263,7 @@ __global__ __launch_bounds__(kThreads, 2) void sgemm_mfma_kernel(Params p) {
     mfmas((kSteps - 1) & 1);
   }
 
-  store_c_tile<2>(p, acc, m0 + wm, n0 + wn, lrow, lhalf);
+  store_c_tile<2, false>(p, acc, m0 + wm, n0 + wn, lrow, lhalf);
 }
 
 template <bool AK, bool BN>

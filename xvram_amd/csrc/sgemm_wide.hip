@@ -349,7 +349,7 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_wide_kernel(Params p) {
     mfma_range((kPairs - 1) & 1, 0, 32);
   }
 
-  store_c_tile<4>(p, acc, m0 + wm, n0 + wn, lrow, lhalf);
+  store_c_tile<4, true>(p, acc, m0 + wm, n0 + wn, lrow, lhalf);
 }
 
 // ---- barrier-free N/T kernel ------------------------------------------------
@@ -510,7 +510,8 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
     }(std::make_integer_sequence<int, kRing>{});
   }
 
-  store_c_tile<4>(p, acc, m0 + wm, n0 + wn, lrow, lhalf);
+  // Every tile is interior: two columns of C per batch of loads.
+  store_c_interior<4, 2, true>(p, acc, m0 + wm, n0 + wn, lrow, lhalf);
 }
 
 } // namespace
