@@ -22,8 +22,9 @@ attached to every kernel dispatch on the library's compute lanes; trace file
 written by the library). Launches of a few ms alternate between two compute
 lanes and overlap at their ends, so there the union, not the sum of the
 per-launch durations, is the kernels' time (``kernel_overlap_ms`` reports the
-difference); ``kernel_ms_per_launch`` is that time per tile launch of the plan
-(an operation's first launch may run as several K-slice kernels). Other workloads:
+difference); ``kernel_ms_per_tile`` is that time per tile of the plan (one C
+tile x one K panel; a launch covers one or two K panels, and the launches of
+an operation's first K pass may run as several K-slice kernels). Other workloads:
 ``--workload`` (config 3's resident sweep, config 4, the config-5 chain).
 ``cpu_baseline`` times the FP64 reference loop (the oracle's restatement of
 the reference's CPU GEMM) on a bounded sample of the same product, on all host
@@ -199,6 +200,7 @@ def analyse(ops):
     """Busy times per operation (each operation's times are relative to its own
     start event, so intervals of different operations are never merged)."""
     k_busy = h_busy = d_busy = copy_busy = hidden = kernel_ms = 0.0
+    span = first_kernel = host_enqueued = host_drained = 0.0
     launches = h2d_bytes = d2h_bytes = 0
     for op in ops:
         kernels = [(s, e) for s, e, _ in op["kernels"]]
@@ -217,7 +219,21 @@ def analyse(ops):
         d_busy += db
         copy_busy += cb
         hidden += _intersection(copies_union, k_union)
+        span += max(e for s, e in kernels + h2d + d2h)
+        first_kernel += min(s for s, e in kernels)
+        host = op.get("host") or [0.0, 0.0]
+        host_enqueued += host[0]
+        host_drained += host[1]
+    n = max(1, len(ops))
     return {
+        # Per operation, averaged: the device timeline (from the operation's
+        # start event to its last kernel or copy), the first kernel's start,
+        # and host time from begin_operation to the last enqueue and to the
+        # device drained.
+        "op_timeline_ms": {"device_span": span / n, "first_kernel_start": first_kernel / n,
+                           "kernel_idle_in_span": (span - k_busy) / n,
+                           "host_last_enqueue": host_enqueued / n,
+                           "host_drained": host_drained / n},
         "launches": launches,
         "kernel_ms_total": kernel_ms,
         "kernel_busy_ms": k_busy,
@@ -400,7 +416,7 @@ def run_chain(args, xv, lib, synth, link) -> int:
             epilogue=xv.epilogue(b_alloc, xv.abi.BIAS_PER_COLUMN, relu=True)))
     info = plans[0].info()
     log(f"chain ready: {L} x {width * width * 4 / GiB:.0f} GiB weights ({time.time() - t0:.1f}s); "
-        f"layer plan tiles {info.tile_m}x{info.tile_n}x{info.tile_k}, {info.tile_count} launches")
+        f"layer plan tiles {info.tile_m}x{info.tile_n}x{info.tile_k}, {info.tile_count} tiles")
 
     y_out = np.empty(batch * width, dtype=np.float32)
 
@@ -509,7 +525,7 @@ def run_chain(args, xv, lib, synth, link) -> int:
         "config": {"workload": CHAIN["name"], "layers": L, "batch": batch, "width": width,
                    "vram_budget_bytes": CHAIN["budget"], "frame_bytes": CHAIN["frame"],
                    "tile": [info.tile_m, info.tile_n, info.tile_k],
-                   "launches_per_step": L * info.tile_count,
+                   "tiles_per_step": L * info.tile_count,
                    "kernels_per_step": stats["launches"] / args.steps,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(kernel_tflops, 3),
@@ -617,7 +633,7 @@ def main() -> int:
                        xv.matrix(b, b_rows, b_cols, b_rows), xv.matrix(c, m, n, m), op_a, op_b,
                        tile_hints=tuple(int(v) for v in args.tile_hints.split(",")))
     info = plan.info()
-    log(f"plan: tiles {info.tile_m}x{info.tile_n}x{info.tile_k}, {info.tile_count} launches")
+    log(f"plan: tiles {info.tile_m}x{info.tile_n}x{info.tile_k}, {info.tile_count} tiles")
     # The timed region ends with session_drain: every C byte is back in host
     # memory when the clock stops (the write-back cache leaves a GEMM's last C
     # tiles dirty on the device; the next execution writes them back while it
@@ -654,9 +670,10 @@ def main() -> int:
     step_s = total_s / args.steps  # the final drain is shared by the steps
     value = flops / step_s / 1e12
     kernel_tflops = flops * args.steps / (stats["kernel_busy_ms"] * 1e-3) / 1e12
-    # Tile launches of the plan; an operation's first launch may run as several
-    # K-slice kernels (cache-miss start), so kernels per step can be higher.
-    launches_per_step = info.tile_count
+    # Tiles of the plan (C tile x K panel); a launch covers one or two K panels
+    # and the first pass's launches may run as several K-slice kernels
+    # (cache-miss start), so kernels per step can differ.
+    tiles_per_step = info.tile_count
     kernels_per_step = stats["launches"] / args.steps
 
     # Sample check: one full column per tile column, one full row per tile row
@@ -714,7 +731,7 @@ def main() -> int:
         "config": {"workload": args.workload, "description": desc, "m": m, "n": n, "k": k,
                    "op_a": "NT"[op_a], "op_b": "NT"[op_b], "vram_budget_bytes": budget,
                    "frame_bytes": frame, "tile": [info.tile_m, info.tile_n, info.tile_k],
-                   "launches_per_step": launches_per_step, "kernels_per_step": kernels_per_step,
+                   "tiles_per_step": tiles_per_step, "kernels_per_step": kernels_per_step,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(kernel_tflops, 3),
                      "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
@@ -737,8 +754,9 @@ def main() -> int:
                             m * n * 4 / (link["d2h_gbps"] * 1e9)),
             "frac": None,
         },
-        "kernel_ms_per_launch": round(stats["kernel_busy_ms"] / max(1, launches_per_step * args.steps), 4),
+        "kernel_ms_per_tile": round(stats["kernel_busy_ms"] / max(1, tiles_per_step * args.steps), 4),
         "kernel_overlap_ms_per_step": round((stats["kernel_ms_total"] - stats["kernel_busy_ms"]) / args.steps, 3),
+        "op_timeline_ms": {key: round(v, 3) for key, v in stats["op_timeline_ms"].items()},
         "cache": {f: getattr(tele1, f) - getattr(tele0, f) for f in (
             "bytes_h2d", "bytes_d2h", "cache_hits", "cache_misses", "clean_evictions",
             "dirty_evictions", "writebacks_completed", "handle_reuses", "event_boundaries")},

@@ -1,0 +1,125 @@
+"""Launches over two K panels on the MI355X, through the C ABI.
+
+A 4096 x 4096 x 16384 N/T product under 64 MiB frames plans 4096 x 4096 x
+4096 tiles, four K panels per C tile, two panels per launch (the two-panel
+barrier-free kernel: one C-tile read and write per two panels). The first
+launch (the whole first pass) runs as eight 1024-deep slices, waiting for its
+four panels slice by slice on the first execution, and the second launch is
+one two-panel dispatch (beta 1 over the first pass's C, then the epilogue). A
+repeated execution finds every panel cached and runs the same dispatches.
+
+* Analytic pattern, every element bit for bit (exact in FP32: 28 * 16384 <
+  2^24) -- a panel routed to the wrong half of the launch, a skipped panel or
+  a wrong k_split changes whole columns.
+* Seeded U[-1,1) with alpha = -0.75, beta = 0.5, per-column bias and ReLU,
+  executed twice (C1 = act(alpha A B + beta C0 + b), C2 from C1), each checked
+  against the FP64 oracle on 16 full columns and 16 full rows (one at a seeded
+  offset in each sixteenth of C) with the bound |C - C_ref| <=
+  4*K*2^-24*(|alpha||A||B| + |beta C| + |b|)."""
+import json
+
+import numpy as np
+import pytest
+
+import xvram_amd as xv
+from xvram_amd import abi
+
+from test_gpu_configs import FP, closed, fill_pattern, fill_uniform, synth  # noqa: F401
+
+pytestmark = pytest.mark.gpu
+
+MiB = 1 << 20
+M = N = 4096
+K = 16384
+
+
+def log(msg):
+    print(f"[two-panel] {msg}", flush=True)
+
+
+@pytest.fixture()
+def traced(tmp_path, monkeypatch):
+    trace = tmp_path / "trace.jsonl"
+    monkeypatch.setenv("XVRAM_TRACE_FILE", str(trace))
+    return trace
+
+
+def kernels(trace):
+    return [len(json.loads(line)["kernels"]) for line in open(trace)]
+
+
+def session(lib):
+    return xv.Session(lib, chunk_size_bytes=64 * MiB, cache_target_bytes=16 * 64 * MiB)
+
+
+def test_two_panel_pattern_every_element(traced, synth, oracle_mod):
+    lib = xv.load()
+    s = session(lib)
+    try:
+        a, b, c = s.allocation(M * K * 4), s.allocation(N * K * 4), s.allocation(M * N * 4)
+        fill_pattern(a, synth.synth_fill_pattern_a, M, K, 0)
+        fill_pattern(b, synth.synth_fill_pattern_b, N, K, 1)
+        plan = xv.GemmPlan(s, xv.matrix(a, M, K, M), xv.matrix(b, N, K, N), xv.matrix(c, M, N, M),
+                           abi.OP_N, abi.OP_T)
+        info = plan.info()
+        log(f"plan {info.tile_m}x{info.tile_n}x{info.tile_k}, {info.tile_count} tiles, working set "
+            f"{info.maximum_working_set_bytes >> 20} MiB")
+        assert (info.tile_m, info.tile_n, info.tile_k, info.tile_count) == (4096, 4096, 4096, 4)
+        assert info.maximum_working_set_bytes == 5 * 64 * MiB  # two panels per launch
+        expect = oracle_mod.pattern_expected_matrix(M, N, K).astype(np.float32)
+        for run in range(2):
+            plan.execute()
+            got = c.read(dtype=np.float32).reshape(N, M).T
+            bad = int(np.count_nonzero(got != expect))
+            log(f"execution {run}: {bad} elements differ; kernels {kernels(traced)}")
+            assert bad == 0
+        assert kernels(traced) == [9, 9]  # 8 slices + one two-panel dispatch, each time
+        plan.release()
+    finally:
+        closed(s)
+
+
+def test_two_panel_alpha_beta_epilogue(traced, synth, oracle_mod):
+    from oracle.sample import SeededOperand
+
+    lib = xv.load()
+    s = session(lib)
+    rng = np.random.default_rng(5)
+    try:
+        a, b, c = s.allocation(M * K * 4), s.allocation(N * K * 4), s.allocation(M * N * 4)
+        fill_uniform(synth, a, M * K, 501)
+        fill_uniform(synth, b, N * K, 502)
+        fill_uniform(synth, c, M * N, 503)
+        bias = (oracle_mod.fill_uniform(N, 504) * 0.5).astype(np.float32)
+        v = s.allocation(N * 4)
+        v.write(bias)
+        alpha, beta = -0.75, 0.5
+        plan = xv.GemmPlan(s, xv.matrix(a, M, K, M), xv.matrix(b, N, K, N), xv.matrix(c, M, N, M),
+                           abi.OP_N, abi.OP_T, alpha, beta,
+                           epilogue=xv.epilogue(v, abi.BIAS_PER_COLUMN, relu=True))
+        A = SeededOperand(501, M, K, False).full().astype(np.float64)   # M x K
+        B = SeededOperand(502, N, K, True).full().astype(np.float64)    # K x N (op T)
+        prev = c.read(dtype=np.float32).reshape(N, M).T.astype(np.float64)
+        cols = np.arange(16) * (N // 16) + rng.integers(0, N // 16, 16)
+        rows = np.arange(16) * (M // 16) + rng.integers(0, M // 16, 16)
+        for run in range(2):
+            plan.execute()
+            got = c.read(dtype=np.float32).reshape(N, M).T.astype(np.float64)
+            worst, violations = 0.0, 0
+            for sel_r, sel_c in ((slice(None), cols), (rows, slice(None))):
+                ab = A[sel_r] @ B[:, sel_c]
+                absab = np.abs(A[sel_r]) @ np.abs(B[:, sel_c])
+                ref = np.maximum(alpha * ab + beta * prev[sel_r][:, sel_c] + bias[sel_c], 0.0)
+                bound = 4 * K * 2.0 ** -24 * (abs(alpha) * absab + abs(beta) * np.abs(prev[sel_r][:, sel_c])
+                                              + np.abs(bias[sel_c]))
+                err = np.abs(got[sel_r][:, sel_c] - ref)
+                violations += int(np.count_nonzero(err > bound))
+                worst = max(worst, float(np.max(err / (bound + 1e-300))))
+            log(f"execution {run}: {len(cols)} columns + {len(rows)} rows, violations {violations}, "
+                f"err/bound {worst:.3e}; kernels {kernels(traced)}")
+            assert violations == 0
+            prev = got
+        assert kernels(traced) == [9, 9]
+        plan.release()
+    finally:
+        closed(s)

@@ -682,11 +682,15 @@ xvram_status XVRAM_CALL gemm_plan_get_info_entry(xvram_gemm_plan p, xvram_gemm_p
     local.tile_m = plan.problem.swapped ? plan.tn : plan.tm;
     local.tile_n = plan.problem.swapped ? plan.tm : plan.tn;
     local.tile_k = plan.bk;
-    // One launch's working set: its C tile, A panel and B panel frames.
+    // One launch's working set: its C tile and an A and a B panel frame per
+    // K panel it covers.
     auto session = p->backend->owner.lock();
-    local.maximum_working_set_bytes = session ? 3 * session->chunk_size_bytes() : 0;
+    local.maximum_working_set_bytes =
+        session ? (1 + 2 * uint64_t{plan.panels_per_launch}) * session->chunk_size_bytes() : 0;
     local.workspace_bytes = 0;
-    local.tile_count = plan.launches.size();
+    // Tiles of the plan's geometry (reference planner.cpp:163 tile_count):
+    // C tiles x K panels, however many K panels one launch covers.
+    local.tile_count = plan.tiles_m * plan.tiles_n * plan.panels_k;
     local.effective_compute_mode = XVRAM_COMPUTE_FP32_STRICT;
     local.uses_cublas_lt = 0;
     local.struct_size = caller;

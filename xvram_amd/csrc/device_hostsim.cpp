@@ -14,6 +14,7 @@
 // time of the work done between their records.
 // Faults can be injected per call site (xvram_hostsim_inject), and the
 // reported device memory can be set (xvram_hostsim_set_memory).
+#include <algorithm>
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -235,30 +236,58 @@ public:
                          reinterpret_cast<uintptr_t>(l.c) % 16 == 0 && l.lda % 4 == 0 &&
                          l.ldb % 4 == 0 && l.ldc % 4 == 0 && l.padded;
     if (l.m <= 0 || l.n <= 0 || l.k <= 0 || !aligned) return 1; // hipErrorInvalidValue
+    const bool two = l.a2 != nullptr || l.b2 != nullptr;
+    if (two) {
+      // Two K panels: the N/T interior-tile contract of the gfx950 kernel.
+      constexpr int64_t kLimit = int64_t(1) << 31;
+      const bool ok = l.a2 != nullptr && l.b2 != nullptr &&
+                      reinterpret_cast<uintptr_t>(l.a2) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(l.b2) % 16 == 0 && !l.a_kcontig && l.b_ncontig &&
+                      l.m % 256 == 0 && l.n % 256 == 0 && l.k % 4 == 0 && l.k_split % 32 == 0 &&
+                      l.k_split > 0 && l.k_split < l.k && (l.m / 256) * (l.n / 256) >= 256 &&
+                      int64_t{l.k_split} * l.lda * 4 < kLimit &&
+                      int64_t{l.k - l.k_split} * l.lda * 4 < kLimit &&
+                      int64_t{l.k_split} * l.ldb * 4 < kLimit &&
+                      int64_t{l.k - l.k_split} * l.ldb * 4 < kLimit;
+      if (!ok) return 1; // hipErrorInvalidValue
+    }
+    const int64_t k1 = two ? l.k_split : l.k; // K rows read from a / b
     const auto span = [](int64_t rows, int64_t cols, int64_t ld) {
       return static_cast<uint64_t>(((cols - 1) * ld + rows) * 4);
     };
-    const int64_t a_rows = l.a_kcontig ? l.k : l.m, a_cols = l.a_kcontig ? l.m : l.k;
-    const int64_t b_rows = l.b_ncontig ? l.n : l.k, b_cols = l.b_ncontig ? l.k : l.n;
+    const int64_t a_rows = l.a_kcontig ? k1 : l.m, a_cols = l.a_kcontig ? l.m : k1;
+    const int64_t b_rows = l.b_ncontig ? l.n : k1, b_cols = l.b_ncontig ? k1 : l.n;
     if (!accessible(reinterpret_cast<uint64_t>(l.a), span(a_rows, a_cols, l.lda)) ||
         !accessible(reinterpret_cast<uint64_t>(l.b), span(b_rows, b_cols, l.ldb)) ||
         !accessible(reinterpret_cast<uint64_t>(l.c), span(l.m, l.n, l.ldc)))
+      return kSimBadAccess;
+    if (two && (!accessible(reinterpret_cast<uint64_t>(l.a2), span(l.m, l.k - k1, l.lda)) ||
+                !accessible(reinterpret_cast<uint64_t>(l.b2), span(l.n, l.k - k1, l.ldb))))
       return kSimBadAccess;
     if ((l.bias_row && !accessible(reinterpret_cast<uint64_t>(l.bias_row), l.m * 4ull)) ||
         (l.bias_col && !accessible(reinterpret_cast<uint64_t>(l.bias_col), l.n * 4ull)))
       return kSimBadAccess;
     // Events attached to the dispatch are stamped around the kernel itself.
     if (l.start_event) recorded_[l.start_event] = std::chrono::steady_clock::now();
+    // Column by column; each element accumulates its K products in order
+    // (p ascending, the second panel after the first), in FP32.
+    std::vector<float> acc(static_cast<size_t>(l.m));
     for (int64_t j = 0; j < l.n; ++j) {
-      for (int64_t i = 0; i < l.m; ++i) {
-        float acc = 0.f;
-        for (int64_t p = 0; p < l.k; ++p) {
+      std::fill(acc.begin(), acc.end(), 0.f);
+      for (int64_t p = 0; p < k1; ++p) {
+        const float y = l.b_ncontig ? l.b[j + p * l.ldb] : l.b[p + j * l.ldb];
+        for (int64_t i = 0; i < l.m; ++i) {
           const float x = l.a_kcontig ? l.a[p + i * l.lda] : l.a[i + p * l.lda];
-          const float y = l.b_ncontig ? l.b[j + p * l.ldb] : l.b[p + j * l.ldb];
-          acc += x * y;
+          acc[i] += x * y;
         }
+      }
+      for (int64_t p = 0; p < l.k - k1; ++p) { // second panel (N/T only)
+        const float y = l.b2[j + p * l.ldb];
+        for (int64_t i = 0; i < l.m; ++i) acc[i] += l.a2[i + p * l.lda] * y;
+      }
+      for (int64_t i = 0; i < l.m; ++i) {
         float& out = l.c[i + j * l.ldc];
-        float v = l.beta != 0.f ? l.alpha * acc + l.beta * out : l.alpha * acc;
+        float v = l.beta != 0.f ? l.alpha * acc[i] + l.beta * out : l.alpha * acc[i];
         if (l.bias_row) v += l.bias_row[i];
         if (l.bias_col) v += l.bias_col[j];
         if (l.relu && v < 0.f) v = 0.f;

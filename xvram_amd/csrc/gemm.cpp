@@ -421,50 +421,82 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   lookahead = static_cast<uint32_t>(
       std::min<uint64_t>(lookahead, frame_count >= 6 ? frame_count / 3 - 1 : 0));
 
+  // Block search for `panels` K panels per launch: the block's C tiles, the
+  // pass's A and B panels and the frames the lookahead brings in ahead
+  // (`ahead` launches); the block minimising the scheduled H2D traffic wins.
   const uint64_t a_bytes = p.m * p.k * 4, b_bytes = p.k * p.n * 4, c_bytes = p.m * p.n * 4;
-  uint64_t best_gm = 1, best_gn = 1, best_h2d = UINT64_MAX;
-  for (uint64_t gm = 1; gm <= out.tiles_m; ++gm) {
-    for (uint64_t gn = 1; gn <= out.tiles_n; ++gn) {
-      const uint64_t need = gm * gn + gm + gn + 2ull * lookahead;
-      if (need > frame_count && !(gm == 1 && gn == 1)) continue;
-      const uint64_t h2d = ceil_div(out.tiles_m, gm) * b_bytes +
-                           ceil_div(out.tiles_n, gn) * a_bytes + (p.beta != 0.f ? c_bytes : 0);
-      if (h2d < best_h2d || (h2d == best_h2d && gm * gn > best_gm * best_gn)) {
-        best_h2d = h2d;
-        best_gm = gm;
-        best_gn = gn;
+  struct Block {
+    uint64_t gm = 1, gn = 1, h2d = UINT64_MAX, need = 0;
+  };
+  const auto search = [&](uint64_t panels, uint64_t ahead) {
+    Block best;
+    for (uint64_t gm = 1; gm <= out.tiles_m; ++gm) {
+      for (uint64_t gn = 1; gn <= out.tiles_n; ++gn) {
+        const uint64_t need = gm * gn + panels * (gm + gn) + 2ull * ahead;
+        if (need > frame_count && !(gm == 1 && gn == 1)) continue;
+        const uint64_t h2d = ceil_div(out.tiles_m, gm) * b_bytes +
+                             ceil_div(out.tiles_n, gn) * a_bytes + (p.beta != 0.f ? c_bytes : 0);
+        if (h2d < best.h2d || (h2d == best.h2d && gm * gn > best.gm * best.gn))
+          best = Block{gm, gn, h2d, need};
       }
     }
+    return best;
+  };
+  Block best = search(1, lookahead);
+  // Two K panels per launch: the launch is twice as long, so half the
+  // lookahead covers the same time. Taken only where the two-panel kernel
+  // applies to every launch (no ragged tiles or panels), the schedule's H2D
+  // traffic does not grow and the frames hold the block, both panels of every
+  // A and B of a pass and four new frames per launch acquired ahead: with
+  // less, panels of the running pass are evicted before their last use and
+  // loaded again (measured on 32768^3 under 2 GiB of 64 MiB frames: 23 % more
+  // H2D and the copies, not the kernels, setting the pace).
+  uint32_t panels = 1;
+  const double one_panel_flops = launch_flops(tm, tn, bk);
+  const bool two_panel_kernel = !p.a.transposed && p.b.transposed && tm % 256 == 0 &&
+                                tn % 256 == 0 && (tm / 256) * (tn / 256) >= 256 &&
+                                p.m % tm == 0 && p.n % tn == 0 && bk % 32 == 0 &&
+                                p.k % 4 == 0 && out.panels_k >= 2;
+  if (two_panel_kernel && one_panel_flops <= kTwoPanelMaxFlops &&
+      (max_launch_flops == 0 || 2.0 * one_panel_flops <= static_cast<double>(max_launch_flops))) {
+    const uint32_t ahead2 = std::max<uint32_t>(1, lookahead / 2);
+    const Block two = search(2, 2ull * ahead2);
+    if (two.need <= frame_count && two.h2d <= best.h2d) {
+      best = two;
+      panels = 2;
+      lookahead = ahead2;
+    }
   }
+  const uint64_t best_gm = best.gm, best_gn = best.gn;
   out.block_m = best_gm;
   out.block_n = best_gn;
-  if (best_gm * best_gn + best_gm + best_gn + 2ull * lookahead > frame_count) {
+  out.panels_per_launch = panels;
+  if (best.need > frame_count) {
     // Only the 1 x 1 block is possible: shrink the lookahead to fit.
     const uint64_t spare = frame_count > 3 ? frame_count - 3 : 0;
     lookahead = static_cast<uint32_t>(std::min<uint64_t>(lookahead, spare / 3));
+    best.need = 3 + 2ull * lookahead;
   }
   out.lookahead = lookahead;
-  out.h2d_bytes_planned = best_h2d;
+  out.h2d_bytes_planned = best.h2d;
   out.d2h_bytes_planned = c_bytes;
-  // The block's C tiles, one K panel's A and B panels and the launches
-  // acquired ahead (and the bias frame).
-  out.frames_in_use = std::min<uint64_t>(
-      total_frames, best_gm * best_gn + best_gm + best_gn + 2ull * lookahead + (bias ? 1 : 0));
+  // The block's C tiles, one pass's A and B panels and the launches acquired
+  // ahead (and the bias frame).
+  out.frames_in_use = std::min<uint64_t>(total_frames, best.need + (bias ? 1 : 0));
 
-  // Launch order: blocks in a serpentine; K panels alternate direction from
-  // block to block so the panels loaded last are the first needed next; inside
-  // a K panel, tiles row by row so each A panel serves consecutive launches.
+  // Launch order: blocks in a serpentine; K passes (groups of `panels` K
+  // panels, fixed boundaries) alternate direction from block to block so the
+  // panels loaded last are the first needed next; inside a pass, tiles row by
+  // row so each A panel serves consecutive launches.
   const uint64_t blocks_m = ceil_div(out.tiles_m, best_gm);
   const uint64_t blocks_n = ceil_div(out.tiles_n, best_gn);
+  const uint64_t passes = ceil_div(out.panels_k, panels);
   uint64_t total = 0;
-  if (!checked_mul(out.tiles_m, out.tiles_n, total) || !checked_mul(total, out.panels_k, total) ||
+  if (!checked_mul(out.tiles_m, out.tiles_n, total) || !checked_mul(total, passes, total) ||
       total > 100000000ull)
     return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "gemm", "make_plan", "too_many_tiles");
   out.launches.reserve(total);
-  out.lanes = 2.0 * static_cast<double>(tm) * static_cast<double>(tn) * static_cast<double>(bk) <=
-                      kDualLaneMaxFlops
-                  ? 2
-                  : 1;
+  out.lanes = panels * one_panel_flops <= kDualLaneMaxFlops ? 2 : 1;
   uint64_t block_seq = 0;
   for (uint64_t bi = 0; bi < blocks_m; ++bi) {
     for (uint64_t s = 0; s < blocks_n; ++s, ++block_seq) {
@@ -472,18 +504,21 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
       const uint64_t i_begin = bi * best_gm, i_end = std::min(out.tiles_m, i_begin + best_gm);
       const uint64_t j_begin = bj * best_gn, j_end = std::min(out.tiles_n, j_begin + best_gn);
       const bool forward = block_seq % 2 == 0;
-      for (uint64_t q = 0; q < out.panels_k; ++q) {
-        const uint64_t kp = forward ? q : out.panels_k - 1 - q;
+      if (block_seq == 0) out.head_launches = (i_end - i_begin) * (j_end - j_begin);
+      for (uint64_t q = 0; q < passes; ++q) {
+        const uint64_t pass = forward ? q : passes - 1 - q;
+        const uint64_t kp = pass * panels;
         for (uint64_t i = i_begin; i < i_end; ++i) {
           for (uint64_t j = j_begin; j < j_end; ++j) {
             TileLaunch l;
             l.ti = static_cast<uint32_t>(i);
             l.tj = static_cast<uint32_t>(j);
             l.kp = static_cast<uint32_t>(kp);
+            l.panels = static_cast<uint8_t>(std::min<uint64_t>(panels, out.panels_k - kp));
             l.first_panel = q == 0;
-            l.last_panel = q + 1 == out.panels_k;
+            l.last_panel = q + 1 == passes;
             l.evict_c = l.last_panel && block_seq + 1 < blocks_m * blocks_n;
-            // Consecutive launches in a K panel are different C tiles of the
+            // Consecutive launches in a pass are different C tiles of the
             // block: alternate lanes by the tile's place in the block.
             const uint64_t place = (i - i_begin) * (j_end - j_begin) + (j - j_begin);
             l.lane = static_cast<uint8_t>(out.lanes > 1 ? place % 2 : 0);
@@ -500,20 +535,25 @@ namespace {
 
 struct Acquired {
   size_t index = 0;
-  Frame* a = nullptr;
-  Frame* b = nullptr;
+  Frame* a[2] = {nullptr, nullptr}; // one A and one B frame per K panel of the launch
+  Frame* b[2] = {nullptr, nullptr};
   Frame* c = nullptr;
-  uint64_t slice = 0;                  // K depth of each slice; 0 = one launch
-  std::vector<Event> a_ready, b_ready; // per-slice fill events (empty: whole panel)
+  uint64_t slice = 0;                        // K depth of each slice; 0 = unsliced
+  std::vector<Event> a_ready[2], b_ready[2]; // per-slice fill events (empty: whole panel)
 };
 
 // The first launch of an operation waits for its whole A and B panels before
-// any compute can start (37.7 ms for two 1 GiB panels at 57 GB/s). When they are
-// cache misses, each is filled by copies of K slices of at least this depth
-// (at most kFirstSlices of them) and the launch runs as one kernel per slice,
-// each waiting only for its own slices of A and B: compute starts after the
-// first slices land and runs under the rest of the fill.
-constexpr uint64_t kFirstSliceMin = 2048;
+// any compute can start (37.7 ms for two 1 GiB panels at 57 GB/s), and while
+// the first pass of the first block fills (each of its launches brings in at
+// least one new panel) the copies, not the kernels, set the pace. Those head
+// launches run as one kernel per K slice of at least this depth (at most
+// kFirstSlices per panel); a missing panel is filled by one copy per slice and
+// each kernel waits only for its own slices of A and B, so compute follows the
+// fill slice by slice instead of panel by panel. The slicing is part of the
+// plan, not of the cache state: a head launch whose panels are cached runs the
+// same slices (without waits), so C is bit-identical whichever panels a
+// previous operation left behind.
+constexpr uint64_t kFirstSliceMin = 1024;
 constexpr uint64_t kFirstSlices = 8;
 
 // The K slices of a panel as copy pieces: K runs along its lines (op-N A,
@@ -529,8 +569,11 @@ std::vector<PanelPiece> k_slices(const PanelGeom& g, bool k_within_lines, uint64
   return out;
 }
 
+// A launch's C tile and its K panels: panel t covers K rows [p0[t], p0[t] + w[t]).
 struct LaunchGeom {
-  uint64_t i0, h, j0, g, p0, w;
+  uint64_t i0, h, j0, g;
+  uint32_t panels;
+  uint64_t p0[2], w[2];
 };
 
 LaunchGeom launch_geom(const GemmPlanData& plan, const TileLaunch& l) {
@@ -540,22 +583,37 @@ LaunchGeom launch_geom(const GemmPlanData& plan, const TileLaunch& l) {
   g.h = std::min(plan.tm, p.m - g.i0);
   g.j0 = l.tj * plan.tn;
   g.g = std::min(plan.tn, p.n - g.j0);
-  g.p0 = static_cast<uint64_t>(l.kp) * plan.bk;
-  g.w = std::min(plan.bk, p.k - g.p0);
+  g.panels = l.panels;
+  for (uint32_t t = 0; t < 2; ++t) {
+    g.p0[t] = (static_cast<uint64_t>(l.kp) + t) * plan.bk;
+    g.w[t] = t < l.panels ? std::min(plan.bk, p.k - g.p0[t]) : 0;
+  }
   return g;
 }
+
+// One tile-kernel dispatch of a launch: K rows [k0, k0 + depth) of panel
+// `panel`, or both panels of a two-panel launch (two == true).
+struct KernelPiece {
+  uint32_t panel = 0;
+  uint64_t k0 = 0, depth = 0;
+  bool two = false;
+  int slice = -1; // index into the per-slice ready events, -1 = none
+};
 
 } // namespace
 
 // Pipelined execution. Panels of the next `lookahead` launches are acquired
 // (H2D copies queued on the copy stream) before each launch is enqueued on the
 // compute stream; the compute stream waits on the fill events of the launch's
-// three frames; the launch's stop event, recorded by its dispatch, becomes the
+// frames; the launch's stop event, recorded by its dispatch, becomes the
 // retire event of those frames. A C tile of any block but the last is written
-// back on the D2H stream and evicted as soon as its last K panel is enqueued
+// back on the D2H stream and evicted as soon as its last K pass is enqueued
 // (the next block needs the frame); the last block's tiles stay resident and
 // dirty after the operation (write-back cache). The host blocks only when a
-// frame it wants to refill still has an unretired consumer.
+// frame it wants to refill still has an unretired consumer. A launch over two
+// K panels runs as one dispatch of the two-panel kernel when that kernel's
+// contract holds (the planner only makes such launches), else as one
+// dispatch per panel.
 Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
                    const GemmHooks& hooks) {
   const CanonProblem& p = plan.problem;
@@ -588,6 +646,13 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     }
   }
 
+  // Unpins what an acquisition already holds (its launch never runs).
+  const auto drop = [&](Acquired& acq) {
+    Stream cs = rt.compute_stream();
+    for (Frame* f : {acq.c, acq.a[0], acq.b[0], acq.a[1], acq.b[1]})
+      if (f) (void)rt.release_after(*f, cs, false);
+  };
+
   const auto acquire_launch = [&](size_t idx) -> Error {
     // Sample the live budget (rate-limited) before each launch's panels.
     if (Error e = rt.refresh_budget(3, 0, false)) return e;
@@ -595,12 +660,10 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     const LaunchGeom g = launch_geom(plan, l);
     Acquired acq;
     acq.index = idx;
-    const PanelGeom ag = a_geom(p.a, g.i0, g.h, g.p0, g.w);
-    const PanelGeom bg = b_geom(p.b, g.p0, g.w, g.j0, g.g);
     const PanelGeom cg = c_geom(g.i0, g.h, g.j0, g.g);
     const bool c_needs_data = !l.first_panel || p.beta != 0.f;
-    if (idx == 0 && plan.launches.size() > 1 && g.w >= 2 * kFirstSliceMin)
-      acq.slice = std::max(kFirstSliceMin, round_up(ceil_div(g.w, kFirstSlices), 16));
+    if (idx < plan.head_launches && plan.launches.size() > 1 && g.w[0] >= 2 * kFirstSliceMin)
+      acq.slice = std::max(kFirstSliceMin, round_up(ceil_div(g.w[0], kFirstSlices), 16));
     if (Error e = rt.acquire(panel_key(p.c, cg), packed_ld(cg) * 4, c_needs_data, acq.c)) return e;
     // A hit (or an unsliced launch) leaves the per-slice event lists empty.
     const auto operand = [&](const CanonOperand& op, const PanelGeom& pg, bool k_within,
@@ -609,16 +672,16 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
       return rt.acquire_pieces(panel_key(op, pg), packed_ld(pg) * 4,
                                k_slices(pg, k_within, acq.slice), out, ready);
     };
-    if (Error e = operand(p.a, ag, p.a.transposed, acq.a, acq.a_ready)) {
-      (void)rt.release_after(*acq.c, rt.compute_stream(), false);
-      return e;
+    for (uint32_t t = 0; t < g.panels; ++t) {
+      const PanelGeom ag = a_geom(p.a, g.i0, g.h, g.p0[t], g.w[t]);
+      const PanelGeom bg = b_geom(p.b, g.p0[t], g.w[t], g.j0, g.g);
+      Error e = operand(p.a, ag, p.a.transposed, acq.a[t], acq.a_ready[t]);
+      if (!e) e = operand(p.b, bg, !p.b.transposed, acq.b[t], acq.b_ready[t]);
+      if (e) {
+        drop(acq);
+        return e;
+      }
     }
-    if (Error e = operand(p.b, bg, !p.b.transposed, acq.b, acq.b_ready)) {
-      (void)rt.release_after(*acq.c, rt.compute_stream(), false);
-      (void)rt.release_after(*acq.a, rt.compute_stream(), false);
-      return e;
-    }
-    if (acq.a_ready.empty() && acq.b_ready.empty()) acq.slice = 0; // both cached
     window.push_back(std::move(acq));
     return {};
   };
@@ -642,54 +705,78 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     window.pop_front();
     const TileLaunch& l = plan.launches[idx];
     const LaunchGeom g = launch_geom(plan, l);
-    const PanelGeom ag = a_geom(p.a, g.i0, g.h, g.p0, g.w);
-    const PanelGeom bg = b_geom(p.b, g.p0, g.w, g.j0, g.g);
     const PanelGeom cg = c_geom(g.i0, g.h, g.j0, g.g);
     const int lane = l.lane;
     Stream cs = rt.compute_stream(lane);
     // Whole-panel fills are waited for up front; sliced ones slice by slice.
     if (Error e = rt.wait_ready(*acq.c, cs)) { result = e; break; }
-    if (acq.a_ready.empty())
-      if (Error e = rt.wait_ready(*acq.a, cs)) { result = e; break; }
-    if (acq.b_ready.empty())
-      if (Error e = rt.wait_ready(*acq.b, cs)) { result = e; break; }
-    const uint64_t depth = acq.slice ? acq.slice : g.w;
-    const uint64_t slices = ceil_div(g.w, depth);
-    const int64_t lda = static_cast<int64_t>(packed_ld(ag));
-    const int64_t ldb = static_cast<int64_t>(packed_ld(bg));
+    for (uint32_t t = 0; t < g.panels && !result; ++t) {
+      if (acq.a_ready[t].empty())
+        if (Error e = rt.wait_ready(*acq.a[t], cs)) result = e;
+      if (!result && acq.b_ready[t].empty())
+        if (Error e = rt.wait_ready(*acq.b[t], cs)) result = e;
+    }
+    if (result) break;
+    const int64_t lda = static_cast<int64_t>(packed_ld(a_geom(p.a, g.i0, g.h, g.p0[0], g.w[0])));
+    const int64_t ldb = static_cast<int64_t>(packed_ld(b_geom(p.b, g.p0[0], g.w[0], g.j0, g.g)));
+    // The dispatches of this launch: K slices of each panel (sliced fill),
+    // one two-panel dispatch, or one dispatch per panel.
+    std::vector<KernelPiece> pieces;
+    const bool two_ok = g.panels == 2 && !acq.slice && !p.a.transposed && p.b.transposed &&
+                        g.h % 256 == 0 && g.g % 256 == 0 && (g.h / 256) * (g.g / 256) >= 256 &&
+                        g.w[0] % 32 == 0 && (g.w[0] + g.w[1]) % 4 == 0;
+    if (two_ok) {
+      pieces.push_back(KernelPiece{0, 0, g.w[0] + g.w[1], true, -1});
+    } else {
+      for (uint32_t t = 0; t < g.panels; ++t) {
+        // A sliced launch runs every panel slice by slice (waiting on the
+        // slices of those filled in pieces); an unsliced one panel by panel.
+        const bool waits = !acq.a_ready[t].empty() || !acq.b_ready[t].empty();
+        const uint64_t depth = acq.slice ? acq.slice : g.w[t];
+        for (uint64_t k0 = 0, s = 0; k0 < g.w[t]; k0 += depth, ++s)
+          pieces.push_back(KernelPiece{t, k0, std::min(depth, g.w[t] - k0), false,
+                                       waits ? static_cast<int>(s) : -1});
+      }
+    }
     Event done = nullptr;
-    for (uint64_t s = 0; s < slices && !result; ++s) {
-      const uint64_t k0 = s * depth;
-      if (!acq.a_ready.empty())
-        if (int rc = rt.device().stream_wait_event(cs, acq.a_ready[s])) {
-          result = rt.device_failure(rc, "gemm", "stream_wait");
-          break;
+    for (size_t n = 0; n < pieces.size() && !result; ++n) {
+      const KernelPiece& kp = pieces[n];
+      const uint32_t t = kp.panel;
+      if (kp.slice >= 0) {
+        for (const std::vector<Event>* ready : {&acq.a_ready[t], &acq.b_ready[t]}) {
+          if (ready->empty()) continue;
+          if (int rc = rt.device().stream_wait_event(cs, (*ready)[kp.slice])) {
+            result = rt.device_failure(rc, "gemm", "stream_wait");
+            break;
+          }
         }
-      if (!acq.b_ready.empty())
-        if (int rc = rt.device().stream_wait_event(cs, acq.b_ready[s])) {
-          result = rt.device_failure(rc, "gemm", "stream_wait");
-          break;
-        }
-      // K slice s of a packed panel: whole lines (op-N A: A(i,p) = a[i + p*lda];
+        if (result) break;
+      }
+      // K rows k0.. of a packed panel: whole lines (op-N A: A(i,p) = a[i + p*lda];
       // op-T B: B(p,j) = b[j + p*ldb]) or a column range of every line.
-      const float* a = reinterpret_cast<const float*>(acq.a->address);
-      const float* b = reinterpret_cast<const float*>(acq.b->address);
+      const float* a = reinterpret_cast<const float*>(acq.a[t]->address);
+      const float* b = reinterpret_cast<const float*>(acq.b[t]->address);
       kernels::SgemmLaunch k;
-      k.a = a + (p.a.transposed ? k0 : k0 * lda);
-      k.b = b + (p.b.transposed ? k0 * ldb : k0);
+      k.a = a + (p.a.transposed ? kp.k0 : kp.k0 * lda);
+      k.b = b + (p.b.transposed ? kp.k0 * ldb : kp.k0);
+      if (kp.two) {
+        k.a2 = reinterpret_cast<const float*>(acq.a[1]->address);
+        k.b2 = reinterpret_cast<const float*>(acq.b[1]->address);
+        k.k_split = static_cast<int>(g.w[0]);
+      }
       k.c = reinterpret_cast<float*>(acq.c->address);
       k.lda = lda;
       k.ldb = ldb;
       k.ldc = static_cast<int64_t>(packed_ld(cg));
       k.m = static_cast<int>(g.h);
       k.n = static_cast<int>(g.g);
-      k.k = static_cast<int>(std::min(depth, g.w - k0));
+      k.k = static_cast<int>(kp.depth);
       k.alpha = p.alpha;
-      k.beta = (s == 0 && l.first_panel) ? p.beta : 1.f;
+      k.beta = (n == 0 && l.first_panel) ? p.beta : 1.f;
       k.a_kcontig = p.a.transposed;
       k.b_ncontig = p.b.transposed;
       k.padded = true;
-      if (l.last_panel && s + 1 == slices && p.has_epilogue()) {
+      if (l.last_panel && n + 1 == pieces.size() && p.has_epilogue()) {
         if (bias) {
           const float* v = reinterpret_cast<const float*>(bias->address);
           if (p.bias_rows) k.bias_row = v + g.i0;
@@ -698,9 +785,9 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
         k.relu = p.relu;
       }
       // The launch's timing events are recorded by its dispatch; the last
-      // slice's stop event is also the retire event of the three frames (each
-      // marker packet between kernels would otherwise cost the compute stream
-      // a few microseconds).
+      // dispatch's stop event is also the retire event of the launch's frames
+      // (each marker packet between kernels would otherwise cost the compute
+      // stream a few microseconds).
       TraceInterval iv;
       iv.kind = 'k';
       if (Error e = rt.record_kernel(iv.start, iv.stop)) {
@@ -719,13 +806,19 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     if (result) break;
     // Sliced fills: settle the entries' state (their whole-panel ready events
     // completed no later than the last slices, which the stream already waits for).
-    if (!acq.a_ready.empty())
-      if (Error e = rt.wait_ready(*acq.a, cs)) { result = e; break; }
-    if (!acq.b_ready.empty())
-      if (Error e = rt.wait_ready(*acq.b, cs)) { result = e; break; }
-    rt.note_kernel_launched(); // one tile, however many slices
-    if (Error e = rt.release_after_event(*acq.a, done, false, lane)) { result = e; break; }
-    if (Error e = rt.release_after_event(*acq.b, done, false, lane)) { result = e; break; }
+    for (uint32_t t = 0; t < g.panels && !result; ++t) {
+      if (!acq.a_ready[t].empty())
+        if (Error e = rt.wait_ready(*acq.a[t], cs)) result = e;
+      if (!result && !acq.b_ready[t].empty())
+        if (Error e = rt.wait_ready(*acq.b[t], cs)) result = e;
+    }
+    if (result) break;
+    rt.note_kernel_launched(g.panels); // one retired tile per K panel, however many dispatches
+    for (uint32_t t = 0; t < g.panels && !result; ++t) {
+      if (Error e = rt.release_after_event(*acq.a[t], done, false, lane)) result = e;
+      else if (Error e2 = rt.release_after_event(*acq.b[t], done, false, lane)) result = e2;
+    }
+    if (result) break;
     if (Error e = rt.release_after_event(*acq.c, done, true, lane)) { result = e; break; }
     if (l.evict_c) {
       if (Error e = rt.writeback_and_evict(*acq.c)) {
@@ -776,11 +869,13 @@ Error carry_gemm_head(Runtime& rt, const GemmPlanData& plan, uint64_t launches) 
   const uint64_t n = std::min<uint64_t>(launches, plan.launches.size());
   for (uint64_t idx = 0; idx < n && !stop; ++idx) {
     const LaunchGeom g = launch_geom(plan, plan.launches[idx]);
-    const PanelGeom ag = a_geom(p.a, g.i0, g.h, g.p0, g.w);
-    const PanelGeom bg = b_geom(p.b, g.p0, g.w, g.j0, g.g);
-    if (Error e = carry(panel_key(p.a, ag), packed_ld(ag) * 4, stop)) return e;
-    if (stop) break;
-    if (Error e = carry(panel_key(p.b, bg), packed_ld(bg) * 4, stop)) return e;
+    for (uint32_t t = 0; t < g.panels && !stop; ++t) {
+      const PanelGeom ag = a_geom(p.a, g.i0, g.h, g.p0[t], g.w[t]);
+      const PanelGeom bg = b_geom(p.b, g.p0[t], g.w[t], g.j0, g.g);
+      if (Error e = carry(panel_key(p.a, ag), packed_ld(ag) * 4, stop)) return e;
+      if (stop) break;
+      if (Error e = carry(panel_key(p.b, bg), packed_ld(bg) * 4, stop)) return e;
+    }
   }
   return {};
 }

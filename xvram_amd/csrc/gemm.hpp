@@ -113,9 +113,11 @@ Error validate_epilogue(const GemmSpec& spec);
 
 CanonProblem canonicalize(const GemmSpec& spec);
 
-// One tile-kernel launch of a plan: C' tile (ti, tj), K panel kp.
+// One tile-kernel launch of a plan: C' tile (ti, tj), K panels kp ..
+// kp + panels - 1 (each its own A and B frame).
 struct TileLaunch {
   uint32_t ti = 0, tj = 0, kp = 0;
+  uint8_t panels = 1;
   bool first_panel = false; // first K panel applied to this C tile (uses user beta)
   bool last_panel = false;  // C tile final after this launch
   // The C tile is final and its block is not the plan's last: the next
@@ -135,6 +137,8 @@ struct GemmPlanData {
   uint64_t d2h_bytes_planned = 0;
   uint64_t frames_in_use = 0;              // frames the schedule keeps busy at once
   int lanes = 1;                           // compute lanes the launches alternate over
+  uint32_t panels_per_launch = 1;          // K panels one launch covers (1 or 2)
+  uint64_t head_launches = 0;              // the first block's first pass (sliced when missing)
   std::vector<TileLaunch> launches;
 };
 
@@ -143,7 +147,14 @@ struct GemmPlanData {
 // write, the next launch's dispatch and first loads) are then overlapped by
 // the neighbouring launch. Longer launches stay on one lane, where each
 // launch's HIP-event duration is its own run time.
-constexpr double kDualLaneMaxFlops = 2.0e11;
+constexpr double kDualLaneMaxFlops = 3.0e11;
+
+// One-panel launches of at most this many FLOPs take two K panels per launch
+// when the two-panel tile kernel accepts them (N/T, interior 256 x 256 tiles,
+// at least one per CU, panel depth a multiple of 32) and the schedule keeps
+// its H2D traffic: each launch pays a C-tile read and write through HBM and a
+// prologue, ~20 us on a 4096 x 4096 tile (2 % of a 4096-deep launch).
+constexpr double kTwoPanelMaxFlops = 1.5e11;
 
 // Floating-point rate assumed when sizing launches against the transaction
 // duration guard: well under the tile kernel's sustained FP32 rate, so a launch

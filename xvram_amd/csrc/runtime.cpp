@@ -558,9 +558,11 @@ bool Runtime::allocation_streaming(uint64_t allocation_id) {
 // write-back was just queued) would make the host wait for that consumer while
 // launches it could already enqueue sit idle; a clean entry whose last
 // consumer was recorded earlier in the schedule is evicted instead when the
-// policy names one. The choice depends only on the schedule (the order of
-// retire records), never on how far the device has progressed, so the
-// accounting of a run is reproducible.
+// policy names one. Likewise an entry whose write-back was started ahead
+// (make_room) is a victim only when the policy finds no other: its new
+// contents would have to wait for the copy. The choice depends only on the
+// schedule (the order of retire records and write-backs), never on how far
+// the device has progressed, so the accounting of a run is reproducible.
 Error Runtime::select_frame(Frame*& out) {
   Frame* free_frame = nullptr;
   Frame* uncreated = nullptr;
@@ -601,7 +603,13 @@ Error Runtime::select_frame(Frame*& out) {
     }
   }
   if (!chosen) {
-    const std::optional<uint64_t> victim = policy_->select_victim(candidates);
+    std::optional<uint64_t> victim;
+    std::vector<VictimCandidate> settled;
+    for (const VictimCandidate& c : candidates)
+      if (!frames_[c.id].writeback_done) settled.push_back(c);
+    if (!settled.empty() && settled.size() < candidates.size())
+      victim = policy_->select_victim(settled);
+    if (!victim) victim = policy_->select_victim(candidates);
     if (!victim)
       return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "cache", "select_frame",
                         "every cache frame is pinned by the current working set");
@@ -1375,6 +1383,7 @@ Error Runtime::begin_operation() {
   carried_trace_.clear();
   events_in_use_.insert(events_in_use_.end(), carried_events_.begin(), carried_events_.end());
   carried_events_.clear();
+  op_host_start_ = std::chrono::steady_clock::now();
   if (int rc = device_->event_record(op_start_, compute_)) return device_failure(rc, "operation", "record");
   for (Stream s : {h2d_, d2h_, compute2_})
     if (int rc = device_->stream_wait_event(s, op_start_)) return device_failure(rc, "operation", "wait");
@@ -1391,6 +1400,12 @@ Error Runtime::record_kernel(Event& start, Event& stop) {
 // the duration guard (reference runtime.cpp:1396-1408: work longer than
 // max_transaction_ms blocks further launches and fails with a timeout).
 Error Runtime::finish_operation(uint64_t operation_id) {
+  const auto host_ms = [&]() {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() -
+                                                     op_host_start_)
+        .count();
+  };
+  const double enqueued_ms = host_ms(); // everything is enqueued: the host waits from here
   Error first;
   for (Stream s : {compute_, compute2_, d2h_}) {
     if (int rc = device_->stream_sync(s)) {
@@ -1417,6 +1432,7 @@ Error Runtime::finish_operation(uint64_t operation_id) {
     if (f.state == EntryState::h2d_in_flight) move(f, EntryState::resident_clean);
     if (f.state == EntryState::evicting) move(f, EntryState::host_clean);
   }
+  const double synced_ms = host_ms();
   // The D2H stream has drained (or the session is poisoned); the copies' stop
   // events go back to the pool below, so nothing may refer to them.
   writebacks_settled();
@@ -1425,7 +1441,11 @@ Error Runtime::finish_operation(uint64_t operation_id) {
   if (!first) {
     FILE* out = nullptr;
     if (tracing()) out = std::fopen(trace_path_.c_str(), "a");
-    if (out) std::fprintf(out, "{\"operation_id\": %llu", static_cast<unsigned long long>(operation_id));
+    // Host timestamps (ms from begin_operation): the last launch enqueued, the
+    // device drained.
+    if (out)
+      std::fprintf(out, "{\"operation_id\": %llu, \"host\": [%.3f, %.3f]",
+                   static_cast<unsigned long long>(operation_id), enqueued_ms, synced_ms);
     const char* names[4] = {"kernels", "h2d", "d2h", "transactions"};
     const char kinds[4] = {'k', 'h', 'd', 't'};
     const size_t own = carrying ? carry_trace_mark_ : trace_.size();

@@ -36,6 +36,7 @@
 // launch of one C tile stays on one lane.
 #pragma once
 
+#include <chrono>
 #include <cstdint>
 #include <functional>
 #include <map>
@@ -318,7 +319,7 @@ public:
   // Kernel bookkeeping used by the executor.
   Error record_kernel(Event& start, Event& stop);
   Error take_event(Event& out);
-  void note_kernel_launched() { ++kernels_in_operation_; }
+  void note_kernel_launched(uint64_t tiles = 1) { kernels_in_operation_ += tiles; }
 
   // Telemetry snapshot in public form.
   void telemetry(xvram_session_telemetry_v1& out) const;
@@ -410,6 +411,8 @@ private:
   Stream h2d_ = nullptr;
   Stream d2h_ = nullptr;
   Event op_start_ = nullptr;
+  // Host clock at begin_operation (the trace's host timestamps count from it).
+  std::chrono::steady_clock::time_point op_host_start_{};
   std::vector<Event> event_pool_;
   std::vector<Event> events_in_use_;
   uint64_t op_serial_ = 0; // operations begun so far

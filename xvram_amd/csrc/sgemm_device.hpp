@@ -23,6 +23,11 @@ struct Params {
   const float* bias_row; // per-row bias (nullptr = none)
   const float* bias_col; // per-column bias (nullptr = none)
   int relu;
+  // Second K panel (ring kernel only): k rows [k_split, k) of A and B come
+  // from a2 / b2 (same leading dimensions) instead of a / b; nullptr = none.
+  const float* a2;
+  const float* b2;
+  int k_split;
 };
 
 __device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.f); }

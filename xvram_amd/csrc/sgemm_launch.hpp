@@ -12,6 +12,14 @@
 // line may be read as whole 16-byte vectors up to its leading dimension), which
 // frame-packed panels always satisfy; anything else returns hipErrorInvalidValue.
 //
+// Two K panels (optional): with a2 / b2 set, k rows [0, k_split) of op(A) and
+// op(B) come from a / b and rows [k_split, k) from a2 / b2 (same leading
+// dimensions): one launch over two separately stored panels. Only for the
+// N/T form (a_kcontig false, b_ncontig true) with m and n multiples of 256, k
+// a multiple of 4, k_split a multiple of 32 inside (0, k), at least 256 tiles
+// of 256 x 256, 16-byte aligned a2 / b2 and each panel below 2^31 bytes;
+// anything else returns hipErrorInvalidValue.
+//
 // start_event / stop_event (hipEvent_t, optional) are recorded by the dispatch
 // itself (hipExtLaunchKernelGGL): no separate marker packets run between
 // kernels, and stop_event completes when the kernel does, so it can serve as
@@ -35,6 +43,9 @@ struct SgemmLaunch {
   const float* bias_row = nullptr;
   const float* bias_col = nullptr;
   bool relu = false;
+  const float* a2 = nullptr;
+  const float* b2 = nullptr;
+  int k_split = 0;
   void* start_event = nullptr;
   void* stop_event = nullptr;
 };

@@ -376,6 +376,13 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_wide_kernel(Params p) {
 // 256) and whose K is a multiple of 4: every load then stays inside the tile's
 // rows and columns and inside the K extent (the last load of the last pair ends
 // at or before the panel's record count), so no predication is needed.
+//
+// Two-panel instance (kTwo): the launch's K rows come from two separately
+// stored panels with the same leading dimensions, [0, k_split) from a / b and
+// [k_split, k) from a2 / b2, one buffer descriptor pair each; a C tile then
+// takes two K panels per pass through HBM (one read and one write of C, one
+// prologue) instead of one. Only the loads' source changes, so C is bit-identical
+// to a one-panel launch over the same K.
 constexpr int kRing = 8;   // slots (k-pairs) per wave
 constexpr int kAhead = 7;  // prefetch distance in k-pairs
 constexpr int kSlot = 1024; // floats per slot: A 4 x 128, then B 4 x 128
@@ -383,6 +390,14 @@ static_assert(kAhead == kRing - 1, "loads reuse the slot vacated one step earlie
 static_assert(4 * kAhead <= 63, "outstanding loads fit the vmcnt counter");
 static_assert(4 * (kAhead - 2) == 20, "steady-state wait below");
 
+// One K panel's buffer descriptors for A and B; pair q of the launch is pair
+// q - base of that panel.
+struct RingSource {
+  __amdgpu_buffer_rsrc_t a, b;
+  int base;
+};
+
+template <bool kTwo>
 __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float lds[4 * kRing * kSlot];
   asm volatile("; accumulators in AGPRs" ::: "a0");
@@ -409,11 +424,20 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
 
   const int pairs = p.k / 4;
   // A(i, k) sits at byte 4*(k*lda + i-m0) from a + m0, B(k, j) at
-  // 4*(k*ldb + j-n0) from b + n0.
-  const __amdgpu_buffer_rsrc_t rs_a =
-      panel_rsrc(p.a + m0, (uint32_t)(((int64_t)p.k * p.lda - m0) * 4));
-  const __amdgpu_buffer_rsrc_t rs_b =
-      panel_rsrc(p.b + n0, (uint32_t)(((int64_t)p.k * p.ldb - n0) * 4));
+  // 4*(k*ldb + j-n0) from b + n0. kTwo: k rows [0, k_split) come from a / b
+  // and rows [k_split, k) from a2 / b2 (row k_split is their row 0); k_split
+  // is a multiple of 4 * kRing, so every block of kRing steps below loads from
+  // at most two sources, fixed per block.
+  const int k1 = kTwo ? p.k_split : p.k;
+  const int q_split = k1 / 4;
+  const RingSource lo{panel_rsrc(p.a + m0, (uint32_t)(((int64_t)k1 * p.lda - m0) * 4)),
+                      panel_rsrc(p.b + n0, (uint32_t)(((int64_t)k1 * p.ldb - n0) * 4)), 0};
+  RingSource hi = lo;
+  if constexpr (kTwo) {
+    const int k2 = p.k - k1;
+    hi = RingSource{panel_rsrc(p.a2 + m0, (uint32_t)(((int64_t)k2 * p.lda - m0) * 4)),
+                    panel_rsrc(p.b2 + n0, (uint32_t)(((int64_t)k2 * p.ldb - n0) * 4)), q_split};
+  }
   // Load h of a pair: lane l brings k-row 2h + l/32 of the pair, elements
   // 4*(l%32) .. +3 of the wave's half; it lands at LDS byte 1024*h + 16*l of
   // the operand's part of the slot, i.e. row-major 4 x 128.
@@ -429,14 +453,15 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
   const uint32_t ring_lds = lds_byte_addr(ring);
 
   // Load L (0, 1: A halves; 2, 3: B halves) of pair q into slot S.
-  auto issue = [&]<int S, int L>(int q, Int<S>, Int<L>) {
+  auto issue = [&]<int S, int L>(int q, Int<S>, Int<L>, const RingSource& src) {
     constexpr int off = (S * kSlot + (L >> 1) * 512 + (L & 1) * 256) * 4;
+    const uint32_t qq = (uint32_t)(q - src.base);
     if constexpr (L < 2) {
-      const uint32_t so = __builtin_amdgcn_readfirstlane(pair_a * (uint32_t)q);
-      load_lds16<off>(ring_lds, vo_a[L & 1], rs_a, so);
+      const uint32_t so = __builtin_amdgcn_readfirstlane(pair_a * qq);
+      load_lds16<off>(ring_lds, vo_a[L & 1], src.a, so);
     } else {
-      const uint32_t so = __builtin_amdgcn_readfirstlane(pair_b * (uint32_t)q);
-      load_lds16<off>(ring_lds, vo_b[L & 1], rs_b, so);
+      const uint32_t so = __builtin_amdgcn_readfirstlane(pair_b * qq);
+      load_lds16<off>(ring_lds, vo_b[L & 1], src.b, so);
     }
   };
   // Fragments of one pair: rows 2t + lhalf, four consecutive floats at 4*lrow
@@ -461,8 +486,8 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
   // Pairs 0 .. kAhead-1 in flight, then pair 0's fragments in registers: with
   // all kAhead pairs issued, only pair 0's four loads need to have landed.
   [&]<int... I>(std::integer_sequence<int, I...>) {
-    ((I < pairs ? (issue(I, Int<I % kRing>{}, Int<0>{}), issue(I, Int<I % kRing>{}, Int<1>{}),
-                   issue(I, Int<I % kRing>{}, Int<2>{}), issue(I, Int<I % kRing>{}, Int<3>{}), 0)
+    ((I < pairs ? (issue(I, Int<I % kRing>{}, Int<0>{}, lo), issue(I, Int<I % kRing>{}, Int<1>{}, lo),
+                   issue(I, Int<I % kRing>{}, Int<2>{}, lo), issue(I, Int<I % kRing>{}, Int<3>{}, lo), 0)
                 : 0),
      ...);
   }(std::make_integer_sequence<int, kAhead>{});
@@ -473,7 +498,10 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
 
   // Step q, q % kRing == J. kTail: the last steps, which may issue no loads
   // (and so wait for all outstanding ones) and may have no next pair.
-  auto step = [&]<int J, bool kTail>(int q, Int<J>, std::bool_constant<kTail>) {
+  // Step J of a block (q % kRing == J) loads pair q + kAhead: from `first`
+  // for J == 0, from `rest` for the others (pairs q - J + kRing ..).
+  auto step = [&]<int J, bool kTail>(int q, Int<J>, std::bool_constant<kTail>,
+                                      const RingSource& first, const RingSource& rest) {
     constexpr int cur = J & 1, nxt = (J + 1) & 1;
     constexpr int s_next = (J + 1) % kRing, s_load = (J + kAhead) % kRing;
     if constexpr (!kTail) asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
@@ -486,7 +514,8 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
          if constexpr (X % 8 == 0) {
            if (load) {
              __builtin_amdgcn_sched_barrier(0);
-             issue(q + kAhead, Int<s_load>{}, Int<X / 8>{});
+             if constexpr (J == 0) issue(q + kAhead, Int<s_load>{}, Int<X / 8>{}, first);
+             else issue(q + kAhead, Int<s_load>{}, Int<X / 8>{}, rest);
              __builtin_amdgcn_sched_barrier(0);
            }
          }
@@ -497,16 +526,28 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
     __builtin_amdgcn_sched_barrier(0);
   };
 
+  // The block starting at q (a multiple of kRing) loads pair q + kAhead in its
+  // first step and pairs q + kRing .. in the rest; q_split is a multiple of
+  // kRing, so each of the two groups lies wholly in one panel.
+  static_assert(kAhead + 1 == kRing, "the first step loads the last pair of its block");
+  const auto source = [&](int pair) -> RingSource {
+    if constexpr (kTwo) return pair < q_split ? lo : hi;
+    else return lo;
+  };
   int q = 0;
   // Full blocks of kRing steps whose loads all exist (q + kRing - 1 + kAhead < pairs).
   for (; q + kRing + kAhead <= pairs; q += kRing) {
+    const RingSource first = source(q + kAhead);
+    const RingSource rest = source(q + kRing);
     [&]<int... J>(std::integer_sequence<int, J...>) {
-      (step(q + J, Int<J>{}, std::false_type{}), ...);
+      (step(q + J, Int<J>{}, std::false_type{}, first, rest), ...);
     }(std::make_integer_sequence<int, kRing>{});
   }
   for (; q < pairs; q += kRing) {
+    const RingSource first = source(q + kAhead);
+    const RingSource rest = source(q + kRing);
     [&]<int... J>(std::integer_sequence<int, J...>) {
-      ((q + J < pairs ? (step(q + J, Int<J>{}, std::true_type{}), 0) : 0), ...);
+      ((q + J < pairs ? (step(q + J, Int<J>{}, std::true_type{}, first, rest), 0) : 0), ...);
     }(std::make_integer_sequence<int, kRing>{});
   }
 
@@ -520,15 +561,19 @@ int wide_tile() { return kTile; }
 
 // Launches a 256 x 256 kernel for `p` (tiles_m / tiles_n already in 256s):
 // the barrier-free one for N/T launches of interior tiles only and K a
-// multiple of 4, else sgemm_wide_kernel. start / stop (optional) are recorded
-// by the dispatch itself.
+// multiple of 4 (its two-panel instance when p.a2 is set; the caller has
+// checked that launch's contract), else sgemm_wide_kernel. start / stop
+// (optional) are recorded by the dispatch itself.
 hipError_t launch_wide(const Params& p, bool a_kcontig, bool b_ncontig, hipStream_t stream,
                        hipEvent_t start, hipEvent_t stop) {
   const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
   const dim3 block(kThreads);
-  if (!a_kcontig && b_ncontig && p.m % kTile == 0 && p.n % kTile == 0 && p.k % 4 == 0)
-    hipExtLaunchKernelGGL(sgemm_ring_kernel, grid, block, 0, stream, start, stop, 0, p);
-  else if (!a_kcontig && !b_ncontig)
+  if (!a_kcontig && b_ncontig && p.m % kTile == 0 && p.n % kTile == 0 && p.k % 4 == 0) {
+    if (p.a2 != nullptr)
+      hipExtLaunchKernelGGL(sgemm_ring_kernel<true>, grid, block, 0, stream, start, stop, 0, p);
+    else
+      hipExtLaunchKernelGGL(sgemm_ring_kernel<false>, grid, block, 0, stream, start, stop, 0, p);
+  } else if (!a_kcontig && !b_ncontig)
     hipExtLaunchKernelGGL((sgemm_wide_kernel<false, false>), grid, block, 0, stream, start, stop, 0, p);
   else if (!a_kcontig && b_ncontig)
     hipExtLaunchKernelGGL((sgemm_wide_kernel<false, true>), grid, block, 0, stream, start, stop, 0, p);
