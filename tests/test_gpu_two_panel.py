@@ -3,9 +3,9 @@
 A 4096 x 4096 x 16384 N/T product under 64 MiB frames plans 4096 x 4096 x
 4096 tiles, four K panels per C tile, two panels per launch (the two-panel
 barrier-free kernel: one C-tile read and write per two panels). The first
-launch (the whole first pass) runs as eight 1024-deep slices, waiting for its
-four panels slice by slice on the first execution, and the second launch is
-one two-panel dispatch (beta 1 over the first pass's C, then the epilogue). A
+launch runs as four 2048-deep slices (two per panel), waiting for its four
+panels slice by slice on the first execution, and the second launch is one
+two-panel dispatch (beta 1 over the first pass's C, then the epilogue). A
 repeated execution finds every panel cached and runs the same dispatches.
 
 * Analytic pattern, every element bit for bit (exact in FP32: 28 * 16384 <
@@ -73,7 +73,7 @@ def test_two_panel_pattern_every_element(traced, synth, oracle_mod):
             bad = int(np.count_nonzero(got != expect))
             log(f"execution {run}: {bad} elements differ; kernels {kernels(traced)}")
             assert bad == 0
-        assert kernels(traced) == [9, 9]  # 8 slices + one two-panel dispatch, each time
+        assert kernels(traced) == [5, 5]  # 4 slices + one two-panel dispatch, each time
         plan.release()
     finally:
         closed(s)
@@ -119,7 +119,7 @@ def test_two_panel_alpha_beta_epilogue(traced, synth, oracle_mod):
                 f"err/bound {worst:.3e}; kernels {kernels(traced)}")
             assert violations == 0
             prev = got
-        assert kernels(traced) == [9, 9]
+        assert kernels(traced) == [5, 5]
         plan.release()
     finally:
         closed(s)

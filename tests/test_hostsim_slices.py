@@ -1,17 +1,17 @@
-"""CPU tests of the sliced head launches over libxvram_hostsim.so.
+"""CPU tests of the sliced first launch over libxvram_hostsim.so.
 
-A launch of the first block's first K pass (the head of the operation, where
-the copies set the pace) whose panel depth is at least twice the minimum slice
-(1024) runs as one kernel per K slice (at most 8, each at least 1024 deep);
-each of its missing A or B panels is filled by one copy per slice and each
-kernel waits only for its own slices. The slicing belongs to the plan: a head
-launch whose panels are cached runs the same slices, so C does not depend on
-what an earlier operation left in the cache. These cases make the head launches 4096 or 8192 deep and check: the
-kernel count (one per slice of a sliced launch, one per later launch),
-bit-exact analytic-pattern results in all four N/T forms, beta over the slices
-(the first slice applies the caller's beta, the later ones accumulate), the
-epilogue applied once after the last slice, and unchanged accounting (the
-slices tile the panels: same H2D bytes; one retired tile per tile)."""
+An operation's first launch whose panel depth is at least twice the minimum
+slice (2048) runs as one kernel per K slice (at most 8, each at least 2048
+deep); each of its missing A or B panels is filled by one copy per slice and
+each kernel waits only for its own slices. The slicing belongs to the plan: a
+first launch whose panels are cached runs the same slices, so C does not
+depend on what an earlier operation left in the cache. These cases make the
+first launch 4096 or 8192 deep and check: the kernel count (one per slice of
+the first launch, one per later launch), bit-exact analytic-pattern results in
+all four N/T forms, beta over the slices (the first slice applies the caller's
+beta, the later ones accumulate), the epilogue applied once after the last
+slice, and unchanged accounting (the slices tile the panels: same H2D bytes;
+one retired tile per tile)."""
 import json
 
 import numpy as np
@@ -51,7 +51,7 @@ def kernels_per_operation(trace):
 def test_first_launch_runs_in_k_slices(sim, oracle_mod, ops):
     lib, trace = sim
     # 2 MiB frames: 128 x 4096 panels, so K = 8192 is two 4096-deep launches and
-    # the first one (the whole first pass) runs as four 1024-deep slices.
+    # the first one runs as two 2048-deep slices.
     m, n, k = 128, 64, 8192
     a_op, b_op = pattern_operands(m, n, k)
     with session(lib) as s:
@@ -60,7 +60,7 @@ def test_first_launch_runs_in_k_slices(sim, oracle_mod, ops):
         t = s.telemetry()
         info = prob.plan_info
     assert (info.tile_m, info.tile_n, info.tile_k, info.tile_count) == (128, 64, 4096, 2)
-    assert kernels_per_operation(trace) == [5]          # 4 slices + the second launch
+    assert kernels_per_operation(trace) == [3]          # 2 slices + the second launch
     assert t.transactions_completed == info.tile_count  # one retired tile per tile
     assert t.bytes_h2d == (m * k + k * n) * 4           # slices tile the panels exactly
     assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))
@@ -74,7 +74,7 @@ def test_slices_apply_beta_once(sim, oracle_mod):
                    layouts=(abi.COLUMN_MAJOR, abi.ROW_MAJOR, abi.COLUMN_MAJOR))
     with session(lib) as s:
         out = prob.run(s)
-    assert kernels_per_operation(trace) == [5]
+    assert kernels_per_operation(trace) == [3]
     ref, absab = prob.reference(oracle_mod)
     assert oracle_mod.check_bound(out, k, ref, absab)[0] == 0
 
@@ -89,16 +89,15 @@ def test_cached_panels_keep_the_slicing(sim, oracle_mod):
         prob = Problem(a_op, b_op)
         out = prob.run(s, repeat=2)
         t = s.telemetry()
-    assert kernels_per_operation(trace) == [5, 5]
+    assert kernels_per_operation(trace) == [3, 3]
     assert t.bytes_h2d == (m * k + k * n) * 4  # the second execution hit every panel
     assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))
 
 
 def test_epilogue_after_the_last_slice(sim, oracle_mod):
-    """One 8192-deep K panel per tile (8 MiB frames, two C tiles, both in the
-    first pass): each launch runs as eight 1024-deep slices (the second one's A
-    panel is missing too; its B panel is cached but shares the slicing) and the
-    bias/ReLU epilogue must apply once per tile, on its last slice only."""
+    """One 8192-deep K panel per tile (8 MiB frames, two C tiles): the first
+    launch runs as four slices and the bias/ReLU epilogue must apply once, on
+    the last slice only."""
     lib, trace = sim
     m, n, k = 256, 128, 8192
     a_op = uniform(oracle_mod, m, k, 31)
@@ -118,7 +117,7 @@ def test_epilogue_after_the_last_slice(sim, oracle_mod):
         out = np.asfortranarray(C.read(dtype=np.float32).reshape(n, m).T)
         plan.release()
     assert info.tile_k == k and info.tile_count == 2
-    assert kernels_per_operation(trace) == [16]         # 8 slices per tile
+    assert kernels_per_operation(trace) == [5]          # 4 slices + the second tile
     ref, absab = oracle_mod.sgemm_f64(a_op, b_op)
     pre = ref + bias_vec.astype(np.float64)[None, :]
     bound = 4 * k * 2.0 ** -24 * (absab + np.abs(bias_vec)[None, :])

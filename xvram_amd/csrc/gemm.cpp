@@ -504,7 +504,6 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
       const uint64_t i_begin = bi * best_gm, i_end = std::min(out.tiles_m, i_begin + best_gm);
       const uint64_t j_begin = bj * best_gn, j_end = std::min(out.tiles_n, j_begin + best_gn);
       const bool forward = block_seq % 2 == 0;
-      if (block_seq == 0) out.head_launches = (i_end - i_begin) * (j_end - j_begin);
       for (uint64_t q = 0; q < passes; ++q) {
         const uint64_t pass = forward ? q : passes - 1 - q;
         const uint64_t kp = pass * panels;
@@ -543,17 +542,15 @@ struct Acquired {
 };
 
 // The first launch of an operation waits for its whole A and B panels before
-// any compute can start (37.7 ms for two 1 GiB panels at 57 GB/s), and while
-// the first pass of the first block fills (each of its launches brings in at
-// least one new panel) the copies, not the kernels, set the pace. Those head
-// launches run as one kernel per K slice of at least this depth (at most
-// kFirstSlices per panel); a missing panel is filled by one copy per slice and
-// each kernel waits only for its own slices of A and B, so compute follows the
-// fill slice by slice instead of panel by panel. The slicing is part of the
-// plan, not of the cache state: a head launch whose panels are cached runs the
-// same slices (without waits), so C is bit-identical whichever panels a
+// any compute can start (37.7 ms for two 1 GiB panels at 57 GB/s). It runs as
+// one kernel per K slice of at least this depth (at most kFirstSlices per
+// panel); a missing panel is filled by one copy per slice and each kernel
+// waits only for its own slices of A and B, so compute starts after the first
+// slices land and runs under the rest of the fill. The slicing is part of the
+// plan, not of the cache state: a first launch whose panels are cached runs
+// the same slices (without waits), so C is bit-identical whichever panels a
 // previous operation left behind.
-constexpr uint64_t kFirstSliceMin = 1024;
+constexpr uint64_t kFirstSliceMin = 2048;
 constexpr uint64_t kFirstSlices = 8;
 
 // The K slices of a panel as copy pieces: K runs along its lines (op-N A,
@@ -662,7 +659,7 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     acq.index = idx;
     const PanelGeom cg = c_geom(g.i0, g.h, g.j0, g.g);
     const bool c_needs_data = !l.first_panel || p.beta != 0.f;
-    if (idx < plan.head_launches && plan.launches.size() > 1 && g.w[0] >= 2 * kFirstSliceMin)
+    if (idx == 0 && plan.launches.size() > 1 && g.w[0] >= 2 * kFirstSliceMin)
       acq.slice = std::max(kFirstSliceMin, round_up(ceil_div(g.w[0], kFirstSlices), 16));
     if (Error e = rt.acquire(panel_key(p.c, cg), packed_ld(cg) * 4, c_needs_data, acq.c)) return e;
     // A hit (or an unsliced launch) leaves the per-slice event lists empty.

@@ -138,7 +138,6 @@ struct GemmPlanData {
   uint64_t frames_in_use = 0;              // frames the schedule keeps busy at once
   int lanes = 1;                           // compute lanes the launches alternate over
   uint32_t panels_per_launch = 1;          // K panels one launch covers (1 or 2)
-  uint64_t head_launches = 0;              // the first block's first pass (sliced when missing)
   std::vector<TileLaunch> launches;
 };
 

@@ -558,11 +558,9 @@ bool Runtime::allocation_streaming(uint64_t allocation_id) {
 // write-back was just queued) would make the host wait for that consumer while
 // launches it could already enqueue sit idle; a clean entry whose last
 // consumer was recorded earlier in the schedule is evicted instead when the
-// policy names one. Likewise an entry whose write-back was started ahead
-// (make_room) is a victim only when the policy finds no other: its new
-// contents would have to wait for the copy. The choice depends only on the
-// schedule (the order of retire records and write-backs), never on how far
-// the device has progressed, so the accounting of a run is reproducible.
+// policy names one. The choice depends only on the schedule (the order of
+// retire records), never on how far the device has progressed, so the
+// accounting of a run is reproducible.
 Error Runtime::select_frame(Frame*& out) {
   Frame* free_frame = nullptr;
   Frame* uncreated = nullptr;
@@ -603,13 +601,7 @@ Error Runtime::select_frame(Frame*& out) {
     }
   }
   if (!chosen) {
-    std::optional<uint64_t> victim;
-    std::vector<VictimCandidate> settled;
-    for (const VictimCandidate& c : candidates)
-      if (!frames_[c.id].writeback_done) settled.push_back(c);
-    if (!settled.empty() && settled.size() < candidates.size())
-      victim = policy_->select_victim(settled);
-    if (!victim) victim = policy_->select_victim(candidates);
+    const std::optional<uint64_t> victim = policy_->select_victim(candidates);
     if (!victim)
       return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "cache", "select_frame",
                         "every cache frame is pinned by the current working set");
