@@ -714,14 +714,21 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
         if (Error e = rt.wait_ready(*acq.b[t], cs)) result = e;
     }
     if (result) break;
-    const int64_t lda = static_cast<int64_t>(packed_ld(a_geom(p.a, g.i0, g.h, g.p0[0], g.w[0])));
-    const int64_t ldb = static_cast<int64_t>(packed_ld(b_geom(p.b, g.p0[0], g.w[0], g.j0, g.g)));
+    // Packed leading dimensions of panel t (a K-within-lines panel's depends
+    // on its depth; both panels of a two-panel dispatch share theirs).
+    const auto lda_of = [&](uint32_t t) {
+      return static_cast<int64_t>(packed_ld(a_geom(p.a, g.i0, g.h, g.p0[t], g.w[t])));
+    };
+    const auto ldb_of = [&](uint32_t t) {
+      return static_cast<int64_t>(packed_ld(b_geom(p.b, g.p0[t], g.w[t], g.j0, g.g)));
+    };
     // The dispatches of this launch: K slices of each panel (sliced fill),
     // one two-panel dispatch, or one dispatch per panel.
     std::vector<KernelPiece> pieces;
     const bool two_ok = g.panels == 2 && !acq.slice && !p.a.transposed && p.b.transposed &&
                         g.h % 256 == 0 && g.g % 256 == 0 && (g.h / 256) * (g.g / 256) >= 256 &&
-                        g.w[0] % 32 == 0 && (g.w[0] + g.w[1]) % 4 == 0;
+                        g.w[0] % 32 == 0 && (g.w[0] + g.w[1]) % 4 == 0 &&
+                        lda_of(0) == lda_of(1) && ldb_of(0) == ldb_of(1);
     if (two_ok) {
       pieces.push_back(KernelPiece{0, 0, g.w[0] + g.w[1], true, -1});
     } else {
@@ -753,6 +760,7 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
       // op-T B: B(p,j) = b[j + p*ldb]) or a column range of every line.
       const float* a = reinterpret_cast<const float*>(acq.a[t]->address);
       const float* b = reinterpret_cast<const float*>(acq.b[t]->address);
+      const int64_t lda = lda_of(t), ldb = ldb_of(t);
       kernels::SgemmLaunch k;
       k.a = a + (p.a.transposed ? kp.k0 : kp.k0 * lda);
       k.b = b + (p.b.transposed ? kp.k0 * ldb : kp.k0);
