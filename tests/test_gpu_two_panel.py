@@ -79,6 +79,32 @@ def test_two_panel_pattern_every_element(traced, synth, oracle_mod):
         closed(s)
 
 
+def test_two_panel_ragged_second_panel(traced, synth, oracle_mod):
+    """K = 14336: panels 4096, 4096, 4096, 2048; the second launch pairs a
+    4096-deep panel with the 2048-deep one (k_split 4096, k 6144)."""
+    k = 14336
+    lib = xv.load()
+    s = session(lib)
+    try:
+        a, b, c = s.allocation(M * k * 4), s.allocation(N * k * 4), s.allocation(M * N * 4)
+        fill_pattern(a, synth.synth_fill_pattern_a, M, k, 0)
+        fill_pattern(b, synth.synth_fill_pattern_b, N, k, 1)
+        plan = xv.GemmPlan(s, xv.matrix(a, M, k, M), xv.matrix(b, N, k, N), xv.matrix(c, M, N, M),
+                           abi.OP_N, abi.OP_T)
+        info = plan.info()
+        assert (info.tile_k, info.tile_count) == (4096, 4)
+        plan.execute()
+        got = c.read(dtype=np.float32).reshape(N, M).T
+        expect = oracle_mod.pattern_expected_matrix(M, N, k).astype(np.float32)
+        bad = int(np.count_nonzero(got != expect))
+        log(f"ragged second panel: {bad} elements differ; kernels {kernels(traced)}")
+        assert bad == 0
+        assert kernels(traced) == [5]  # 4 slices + one two-panel dispatch of 4096 + 2048
+        plan.release()
+    finally:
+        closed(s)
+
+
 def test_two_panel_alpha_beta_epilogue(traced, synth, oracle_mod):
     from oracle.sample import SeededOperand
 

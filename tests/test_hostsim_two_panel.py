@@ -97,6 +97,19 @@ def test_odd_panel_count_ends_with_one_panel(sim, oracle_mod):
     assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(M, N, k))
 
 
+def test_ragged_second_panel(sim, oracle_mod):
+    """K = 112 in 32-deep panels: the second pass pairs a 32-deep panel with a
+    16-deep one (k_split 32, k 48) in one two-panel dispatch."""
+    lib, trace = sim
+    k = 112
+    a_op, b_op = pattern_operands(M, N, k)
+    with session(lib) as s:
+        out, info = run_nt(s, a_op, b_op)
+    assert info.tile_count == 4
+    assert kernels_per_operation(trace) == [2]
+    assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(M, N, k))
+
+
 def test_alpha_beta_and_epilogue_over_two_panel_passes(sim, oracle_mod):
     lib, trace = sim
     k = 128
