@@ -9,7 +9,9 @@ order, so these cases check the planner's choice, the executor's acquisition
 and dispatch of both panels (one dispatch per launch), alpha/beta applied once
 per C tile pass, the fused epilogue after the last pass, the accounting (one
 retired tile per C tile x K panel, the same H2D bytes as one-panel launches)
-and bit-exact analytic-pattern results."""
+and bit-exact analytic-pattern results. The operation's first K pass (its
+first block's) runs as one-panel launches: there the link sets the pace and
+one panel per launch needs half the new bytes per launch."""
 import json
 
 import numpy as np
@@ -72,15 +74,15 @@ def run_nt(s, a_op, b_op, c0=None, alpha=1.0, beta=0.0, tile_k=32, epilogue=None
 
 def test_two_panel_launches_are_exact(sim, oracle_mod):
     lib, trace = sim
-    k = 128  # four 32-deep K panels: two launches of two panels each
+    k = 192  # six 32-deep K panels: the first pass as two one-panel launches, then two of two
     a_op, b_op = pattern_operands(M, N, k)
     with session(lib) as s:
         out, info = run_nt(s, a_op, b_op)
         t = s.telemetry()
     assert (info.tile_m, info.tile_n, info.tile_k) == (4096, 4096, 32)
-    assert info.tile_count == 4                          # C tiles x K panels
+    assert info.tile_count == 6                          # C tiles x K panels
     assert info.maximum_working_set_bytes == 5 * 64 * MiB  # C + two A + two B frames
-    assert kernels_per_operation(trace) == [2]           # one dispatch per two-panel launch
+    assert kernels_per_operation(trace) == [4]           # one dispatch per launch
     assert t.transactions_completed == info.tile_count   # one retired tile per K panel
     assert t.bytes_h2d == (M * k + k * N) * 4            # every panel loaded once
     assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(M, N, k))
@@ -88,25 +90,26 @@ def test_two_panel_launches_are_exact(sim, oracle_mod):
 
 def test_odd_panel_count_ends_with_one_panel(sim, oracle_mod):
     lib, trace = sim
-    k = 96  # three panels: one two-panel launch, then a one-panel launch
+    k = 160  # five panels: two one-panel launches (first pass), one of two, one of one
     a_op, b_op = pattern_operands(M, N, k)
     with session(lib) as s:
         out, info = run_nt(s, a_op, b_op)
-    assert info.tile_count == 3
-    assert kernels_per_operation(trace) == [2]
+    assert info.tile_count == 5
+    assert kernels_per_operation(trace) == [4]
     assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(M, N, k))
 
 
 def test_ragged_second_panel(sim, oracle_mod):
-    """K = 112 in 32-deep panels: the second pass pairs a 32-deep panel with a
-    16-deep one (k_split 32, k 48) in one two-panel dispatch."""
+    """K = 112 in 32-deep panels: after the first pass's two one-panel launches,
+    the second pass pairs a 32-deep panel with a 16-deep one (k_split 32, k 48)
+    in one two-panel dispatch."""
     lib, trace = sim
     k = 112
     a_op, b_op = pattern_operands(M, N, k)
     with session(lib) as s:
         out, info = run_nt(s, a_op, b_op)
     assert info.tile_count == 4
-    assert kernels_per_operation(trace) == [2]
+    assert kernels_per_operation(trace) == [3]
     assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(M, N, k))
 
 
@@ -119,7 +122,7 @@ def test_alpha_beta_and_epilogue_over_two_panel_passes(sim, oracle_mod):
     bias = (oracle_mod.fill_uniform(N, 34) * 0.25).astype(np.float32)
     with session(lib) as s:
         out, info = run_nt(s, a_op, b_op, c0, alpha=-0.75, beta=0.5, epilogue="relu", bias=bias)
-    assert kernels_per_operation(trace) == [2]
+    assert kernels_per_operation(trace) == [3]
     # FP64 reference of act(alpha A B + beta C0 + bias) on a column subset.
     cols = np.arange(0, N, 97)
     ref = (-0.75 * (a_op.astype(np.float64) @ b_op[:, cols].astype(np.float64))

@@ -445,12 +445,12 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   Block best = search(1, lookahead);
   // Two K panels per launch: the launch is twice as long, so half the
   // lookahead covers the same time. Taken only where the two-panel kernel
-  // applies to every launch (no ragged tiles or panels), the schedule's H2D
-  // traffic does not grow and the frames hold the block, both panels of every
-  // A and B of a pass and four new frames per launch acquired ahead: with
-  // less, panels of the running pass are evicted before their last use and
-  // loaded again (measured on 32768^3 under 2 GiB of 64 MiB frames: 23 % more
-  // H2D and the copies, not the kernels, setting the pace).
+  // applies to every launch (no ragged tiles or panels) and the schedule's H2D
+  // traffic does not grow. The frames must hold the block, both panels of
+  // every A and B of a pass and two new frames per launch acquired ahead; the
+  // executor keeps the panels of the coming pass out of victim selection
+  // (Runtime::set_protected), without which such a tight budget evicted panels
+  // before their last use (32768^3 under 2 GiB of 64 MiB frames: 23 % more H2D).
   uint32_t panels = 1;
   const double one_panel_flops = launch_flops(tm, tn, bk);
   const bool two_panel_kernel = !p.a.transposed && p.b.transposed && tm % 256 == 0 &&
@@ -460,7 +460,7 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   if (two_panel_kernel && one_panel_flops <= kTwoPanelMaxFlops &&
       (max_launch_flops == 0 || 2.0 * one_panel_flops <= static_cast<double>(max_launch_flops))) {
     const uint32_t ahead2 = std::max<uint32_t>(1, lookahead / 2);
-    const Block two = search(2, 2ull * ahead2);
+    const Block two = search(2, ahead2);
     if (two.need <= frame_count && two.h2d <= best.h2d) {
       best = two;
       panels = 2;
@@ -492,7 +492,7 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   const uint64_t blocks_n = ceil_div(out.tiles_n, best_gn);
   const uint64_t passes = ceil_div(out.panels_k, panels);
   uint64_t total = 0;
-  if (!checked_mul(out.tiles_m, out.tiles_n, total) || !checked_mul(total, passes, total) ||
+  if (!checked_mul(out.tiles_m, out.tiles_n, total) || !checked_mul(total, out.panels_k, total) ||
       total > 100000000ull)
     return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "gemm", "make_plan", "too_many_tiles");
   out.launches.reserve(total);
@@ -507,21 +507,30 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
       for (uint64_t q = 0; q < passes; ++q) {
         const uint64_t pass = forward ? q : passes - 1 - q;
         const uint64_t kp = pass * panels;
-        for (uint64_t i = i_begin; i < i_end; ++i) {
-          for (uint64_t j = j_begin; j < j_end; ++j) {
-            TileLaunch l;
-            l.ti = static_cast<uint32_t>(i);
-            l.tj = static_cast<uint32_t>(j);
-            l.kp = static_cast<uint32_t>(kp);
-            l.panels = static_cast<uint8_t>(std::min<uint64_t>(panels, out.panels_k - kp));
-            l.first_panel = q == 0;
-            l.last_panel = q + 1 == passes;
-            l.evict_c = l.last_panel && block_seq + 1 < blocks_m * blocks_n;
-            // Consecutive launches in a pass are different C tiles of the
-            // block: alternate lanes by the tile's place in the block.
-            const uint64_t place = (i - i_begin) * (j_end - j_begin) + (j - j_begin);
-            l.lane = static_cast<uint8_t>(out.lanes > 1 ? place % 2 : 0);
-            out.launches.push_back(l);
+        const uint64_t in_pass = std::min<uint64_t>(panels, out.panels_k - kp);
+        // The operation's first pass fills the cache with every panel it
+        // uses, so the link sets its pace: one panel per launch there needs
+        // half the new bytes per launch (a two-panel head left the kernels
+        // idle 2.7 ms longer per 32768^3 operation), so it runs as one-panel
+        // passes.
+        const uint64_t split = (block_seq == 0 && q == 0) ? in_pass : 1;
+        for (uint64_t sub = 0; sub < split; ++sub) {
+          for (uint64_t i = i_begin; i < i_end; ++i) {
+            for (uint64_t j = j_begin; j < j_end; ++j) {
+              TileLaunch l;
+              l.ti = static_cast<uint32_t>(i);
+              l.tj = static_cast<uint32_t>(j);
+              l.kp = static_cast<uint32_t>(kp + sub);
+              l.panels = static_cast<uint8_t>(split > 1 ? 1 : in_pass);
+              l.first_panel = q == 0 && sub == 0;
+              l.last_panel = q + 1 == passes && sub + 1 == split;
+              l.evict_c = l.last_panel && block_seq + 1 < blocks_m * blocks_n;
+              // Consecutive launches in a pass are different C tiles of the
+              // block: alternate lanes by the tile's place in the block.
+              const uint64_t place = (i - i_begin) * (j_end - j_begin) + (j - j_begin);
+              l.lane = static_cast<uint8_t>(out.lanes > 1 ? place % 2 : 0);
+              out.launches.push_back(l);
+            }
           }
         }
       }
@@ -650,9 +659,30 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
       if (f) (void)rt.release_after(*f, cs, false);
   };
 
+  // The panels (and C tiles) of launches idx .. idx + one pass of a block:
+  // everything the schedule uses again before a pass goes by, which victim
+  // selection then passes over while it has another choice (a tight budget
+  // would otherwise evict a panel the pass still needs and load it again).
+  const size_t horizon = std::max<uint64_t>(1, plan.block_m * plan.block_n);
+  const auto protect_from = [&](size_t idx) {
+    std::vector<PanelKey> keys;
+    const size_t end = std::min(total, idx + horizon);
+    keys.reserve((end - idx) * 5);
+    for (size_t i = idx; i < end; ++i) {
+      const LaunchGeom g = launch_geom(plan, plan.launches[i]);
+      keys.push_back(panel_key(p.c, c_geom(g.i0, g.h, g.j0, g.g)));
+      for (uint32_t t = 0; t < g.panels; ++t) {
+        keys.push_back(panel_key(p.a, a_geom(p.a, g.i0, g.h, g.p0[t], g.w[t])));
+        keys.push_back(panel_key(p.b, b_geom(p.b, g.p0[t], g.w[t], g.j0, g.g)));
+      }
+    }
+    rt.set_protected(std::move(keys));
+  };
+
   const auto acquire_launch = [&](size_t idx) -> Error {
     // Sample the live budget (rate-limited) before each launch's panels.
     if (Error e = rt.refresh_budget(3, 0, false)) return e;
+    protect_from(idx);
     const TileLaunch& l = plan.launches[idx];
     const LaunchGeom g = launch_geom(plan, l);
     Acquired acq;

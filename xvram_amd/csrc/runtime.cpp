@@ -7,6 +7,7 @@
 #include <cstring>
 #include <numeric>
 #include <thread>
+#include <utility>
 
 namespace xvram {
 
@@ -550,6 +551,12 @@ bool Runtime::allocation_streaming(uint64_t allocation_id) {
   return a && a->priority == XVRAM_ALLOCATION_STREAMING;
 }
 
+void Runtime::set_protected(std::vector<PanelKey> keys) {
+  std::sort(keys.begin(), keys.end());
+  keys.erase(std::unique(keys.begin(), keys.end()), keys.end());
+  protected_ = std::move(keys);
+}
+
 // Frame choice (reference acquire_frame, runtime.cpp:3470-3529): a free frame
 // (the one idle longest), else a not-yet-created frame, else the victim the
 // session's policy names among unpinned resident entries (a dirty victim is
@@ -558,9 +565,14 @@ bool Runtime::allocation_streaming(uint64_t allocation_id) {
 // write-back was just queued) would make the host wait for that consumer while
 // launches it could already enqueue sit idle; a clean entry whose last
 // consumer was recorded earlier in the schedule is evicted instead when the
-// policy names one. The choice depends only on the schedule (the order of
-// retire records), never on how far the device has progressed, so the
-// accounting of a run is reproducible.
+// policy names one. Entries the executor declared protected (the panels of its
+// next launches) are offered to the policy as part of the working set, i.e.
+// not eligible, unless no other entry is: the policy's order of eviction among
+// the rest is unchanged, it just never evicts a panel a launch about to run
+// needs while something else could go. The choice depends only on the
+// schedule (the order of retire records and the declared panels), never on
+// how far the device has progressed, so the accounting of a run is
+// reproducible.
 Error Runtime::select_frame(Frame*& out) {
   Frame* free_frame = nullptr;
   Frame* uncreated = nullptr;
@@ -581,8 +593,17 @@ Error Runtime::select_frame(Frame*& out) {
     c.id = f.index;
     c.state = f.state;
     c.hot = allocation_hot(f.key.allocation_id);
+    c.in_working_set = std::binary_search(protected_.begin(), protected_.end(), f.key);
     candidates.push_back(c);
   }
+  // The policy with the protected entries held back, then, if that finds
+  // nothing, over every candidate.
+  const auto choose = [&](std::vector<VictimCandidate>& list) -> std::optional<uint64_t> {
+    if (std::optional<uint64_t> v = policy_->select_victim(list)) return v;
+    bool any = false;
+    for (VictimCandidate& c : list) any = any || std::exchange(c.in_working_set, false);
+    return any ? policy_->select_victim(list) : std::nullopt;
+  };
   Frame* chosen = free_frame ? free_frame : uncreated;
   if (free_frame && free_frame->retire_pending) {
     std::vector<VictimCandidate> older;
@@ -592,6 +613,7 @@ Error Runtime::select_frame(Frame*& out) {
         older.push_back(c);
     }
     if (!older.empty()) {
+      // Only an unprotected entry is worth evicting to spare the wait.
       if (const std::optional<uint64_t> victim = policy_->select_victim(older)) {
         Frame& v = frames_[*victim];
         if (Error e = evict_key(v, false)) return e;
@@ -601,7 +623,7 @@ Error Runtime::select_frame(Frame*& out) {
     }
   }
   if (!chosen) {
-    const std::optional<uint64_t> victim = policy_->select_victim(candidates);
+    const std::optional<uint64_t> victim = choose(candidates);
     if (!victim)
       return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "cache", "select_frame",
                         "every cache frame is pinned by the current working set");
@@ -1429,6 +1451,7 @@ Error Runtime::finish_operation(uint64_t operation_id) {
   // events go back to the pool below, so nothing may refer to them.
   writebacks_settled();
   in_operation_ = false;
+  protected_.clear();
   bool guard_tripped = false;
   if (!first) {
     FILE* out = nullptr;

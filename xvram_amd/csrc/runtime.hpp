@@ -255,6 +255,10 @@ public:
   Error acquire_pieces(const PanelKey& key, uint64_t packed_pitch,
                        const std::vector<PanelPiece>& pieces, Frame*& out,
                        std::vector<Event>& piece_ready);
+  // Entries the running schedule will use again soon (the executor's next
+  // launches): victim selection passes over them while any other entry is
+  // eligible. Empty = none; cleared at the end of every operation.
+  void set_protected(std::vector<PanelKey> keys);
   // Orders `stream` after the frame's fill.
   Error wait_ready(Frame& frame, Stream stream);
   // Unpins after the consumer enqueued on `stream`; records the retire event.
@@ -399,6 +403,7 @@ private:
   uint64_t arena_bytes_ = 0;
   std::vector<Frame> frames_;
   std::map<PanelKey, uint64_t> index_; // key -> frame index
+  std::vector<PanelKey> protected_;    // sorted; see set_protected
   uint64_t tick_ = 0;
   uint64_t retire_records_ = 0; // retire events recorded so far (schedule order)
 
