@@ -12,7 +12,8 @@ ABI, against the FP64 oracle.
   one full column per tile column, one full row per tile row of the plan's C
   grid, and 1024 random elements -- every C block of the out-of-core schedule
   is sampled (the pattern's mod-3/mod-5 structure cannot see a block routed
-  to the wrong place).
+  to the wrong place); executed twice, each execution's H2D within the planned
+  schedule's 20 GiB.
 * Config 5: 8 x [Y = ReLU(X W^T + b)] with X 256 x 16384 ~ N(0,1), W 16384^2
   and b ~ N(0, 1/16384), 2 GiB budget of 64 MiB frames, the layers queued back
   to back. Each layer is checked against an FP64 forward of the input the GPU
@@ -177,14 +178,21 @@ def test_c4_random_every_block_sampled(lib, synth):
         fill_uniform(synth, b, k * n, 402)
         log(f"C4 operands ready ({time.perf_counter() - t:.1f} s); plan {info.tile_m}x"
             f"{info.tile_n}x{info.tile_k}, {info.tile_count} launches")
-        t0 = s.telemetry()
-        t = time.perf_counter()
-        run_op(plan)
-        secs = time.perf_counter() - t
-        t1 = s.telemetry()
-        log(f"C4 executed in {secs:.3f} s ({2.0 * m * n * k / secs / 1e12:.1f} TFLOP/s), "
-            f"H2D {(t1.bytes_h2d - t0.bytes_h2d) / 1e9:.1f} GB")
-        assert t1.bytes_h2d - t0.bytes_h2d > 3 * budget  # genuinely out of core
+        # Twice: the second execution starts from the first one's cache (its
+        # last block's C tiles dirty), where a budget this tight once made the
+        # schedule evict panels before their last use. Either way the H2D
+        # stays within the planned schedule's: 3 C-block rows x |B| + 2 C-block
+        # columns x |A| = 20 GiB.
+        for run in range(2):
+            t0 = s.telemetry()
+            t = time.perf_counter()
+            run_op(plan)
+            secs = time.perf_counter() - t
+            t1 = s.telemetry()
+            h2d = t1.bytes_h2d - t0.bytes_h2d
+            log(f"C4 execution {run}: {secs:.3f} s ({2.0 * m * n * k / secs / 1e12:.1f} TFLOP/s), "
+                f"H2D {h2d / 1e9:.2f} GB")
+            assert 3 * budget < h2d <= 20 * GiB  # genuinely out of core, no re-loads
         t = time.perf_counter()
         res = spread_check(SeededOperand(401, m, k, False), SeededOperand(402, n, k, True),
                            column_reader(c, m), info.tile_m, info.tile_n, seed=4, randoms=1024)
