@@ -415,8 +415,10 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   out.panels_k = ceil_div(p.k, bk);
 
   // Lookahead: launches whose panels are acquired (and pinned) before they are
-  // enqueued, so copies run ahead of compute. At most 3 frames per launch are
-  // pinned, so keep 3*(lookahead+1) below the frame count.
+  // enqueued, so copies run ahead of compute. At most 3 frames per one-panel
+  // launch are pinned, so keep 3*(lookahead+1) below the frame count (a
+  // two-panel launch pins 5 and gets half the lookahead: 5*(lookahead/2+1)
+  // stays below it too).
   uint32_t lookahead = std::max<uint32_t>(2, 2 * prefetch_distance);
   lookahead = static_cast<uint32_t>(
       std::min<uint64_t>(lookahead, frame_count >= 6 ? frame_count / 3 - 1 : 0));
