@@ -7,7 +7,6 @@
 #include <cstring>
 #include <numeric>
 #include <thread>
-#include <utility>
 
 namespace xvram {
 
@@ -601,7 +600,10 @@ Error Runtime::select_frame(Frame*& out) {
   const auto choose = [&](std::vector<VictimCandidate>& list) -> std::optional<uint64_t> {
     if (std::optional<uint64_t> v = policy_->select_victim(list)) return v;
     bool any = false;
-    for (VictimCandidate& c : list) any = any || std::exchange(c.in_working_set, false);
+    for (VictimCandidate& c : list) {
+      any = any || c.in_working_set;
+      c.in_working_set = false;
+    }
     return any ? policy_->select_victim(list) : std::nullopt;
   };
   Frame* chosen = free_frame ? free_frame : uncreated;
