@@ -499,6 +499,7 @@ Error Runtime::wait_retired(Frame& f) {
   ++t_.event_boundaries;
   const int q = device_->event_query(f.retire_ref);
   if (q == 1) {
+    time_intervals(false); // the host is about to wait anyway
     if (int rc = device_->event_sync(f.retire_ref)) return device_failure(rc, "cache", "event_sync");
   } else if (q != 0) {
     return device_failure(q, "cache", "event_query");
@@ -1400,6 +1401,9 @@ Error Runtime::begin_operation() {
   events_in_use_.insert(events_in_use_.end(), carried_events_.begin(), carried_events_.end());
   carried_events_.clear();
   op_host_start_ = std::chrono::steady_clock::now();
+  trace_timed_ = 0;
+  op_start_seen_ = false;
+  guard_tripped_ = false;
   if (int rc = device_->event_record(op_start_, compute_)) return device_failure(rc, "operation", "record");
   for (Stream s : {h2d_, d2h_, compute2_})
     if (int rc = device_->stream_wait_event(s, op_start_)) return device_failure(rc, "operation", "wait");
@@ -1409,6 +1413,34 @@ Error Runtime::begin_operation() {
 Error Runtime::record_kernel(Event& start, Event& stop) {
   if (Error e = take_event(start)) return e;
   return take_event(stop);
+}
+
+void Runtime::time_intervals(bool all) {
+  if (!in_operation_ && !all) return;
+  // Fills carried into the next operation are timed by that one.
+  const size_t own = carry_active_ ? carry_trace_mark_ : trace_.size();
+  if (!op_start_seen_) {
+    if (!all && device_->event_query(op_start_) != 0) return;
+    op_start_seen_ = true;
+  }
+  while (trace_timed_ < own) {
+    TraceInterval& iv = trace_[trace_timed_];
+    if (!all && device_->event_query(iv.stop) != 0) return;
+    float s = 0.f, e = 0.f;
+    if (device_->event_elapsed_ms(&s, op_start_, iv.start) != 0) s = 0.f;
+    if (device_->event_elapsed_ms(&e, op_start_, iv.stop) != 0) e = s;
+    iv.start_ms = s;
+    iv.stop_ms = e;
+    iv.timed = true;
+    if (iv.kind == 'k' || iv.kind == 't') {
+      const float d = e - s;
+      t_.last_transaction_ms = d;
+      if (config_.max_transaction_ms > 0 &&
+          static_cast<double>(d) > static_cast<double>(config_.max_transaction_ms))
+        guard_tripped_ = true;
+    }
+    ++trace_timed_;
+  }
 }
 
 // End of an operation: wait for the three streams, fold the kernel, callback
@@ -1454,47 +1486,41 @@ Error Runtime::finish_operation(uint64_t operation_id) {
   writebacks_settled();
   in_operation_ = false;
   protected_.clear();
-  bool guard_tripped = false;
   if (!first) {
-    FILE* out = nullptr;
-    if (tracing()) out = std::fopen(trace_path_.c_str(), "a");
-    // Host timestamps (ms from begin_operation): the last launch enqueued, the
-    // device drained.
-    if (out)
-      std::fprintf(out, "{\"operation_id\": %llu, \"host\": [%.3f, %.3f]",
-                   static_cast<unsigned long long>(operation_id), enqueued_ms, synced_ms);
-    const char* names[4] = {"kernels", "h2d", "d2h", "transactions"};
-    const char kinds[4] = {'k', 'h', 'd', 't'};
-    const size_t own = carrying ? carry_trace_mark_ : trace_.size();
-    for (int c = 0; c < 4; ++c) {
-      if (out) std::fprintf(out, ", \"%s\": [", names[c]);
-      bool comma = false;
-      for (size_t i = 0; i < own; ++i) {
-        const TraceInterval& iv = trace_[i];
-        if (iv.kind != kinds[c]) continue;
-        float s = 0.f, e = 0.f;
-        if (device_->event_elapsed_ms(&s, op_start_, iv.start) != 0) s = 0.f;
-        if (device_->event_elapsed_ms(&e, op_start_, iv.stop) != 0) e = s;
-        if (iv.kind == 'k' || iv.kind == 't') {
-          float d = 0.f;
-          if (device_->event_elapsed_ms(&d, iv.start, iv.stop) == 0) {
-            t_.last_transaction_ms = d;
-            if (config_.max_transaction_ms > 0 &&
-                static_cast<double>(d) > static_cast<double>(config_.max_transaction_ms))
-              guard_tripped = true;
-          }
-        }
-        if (out) {
-          std::fprintf(out, "%s[%.6f, %.6f, %llu]", comma ? ", " : "", s, e,
-                       static_cast<unsigned long long>(iv.bytes));
+    time_intervals(true);
+    if (tracing()) {
+      // One record per operation: kernel and copy intervals in ms from its
+      // start event, then the host timestamps (ms from begin_operation) of the
+      // last enqueue and of the device drained.
+      const size_t own = carrying ? carry_trace_mark_ : trace_.size();
+      std::string line;
+      line.reserve(64 + own * 40);
+      char buf[96];
+      std::snprintf(buf, sizeof buf, "{\"operation_id\": %llu, \"host\": [%.3f, %.3f]",
+                    static_cast<unsigned long long>(operation_id), enqueued_ms, synced_ms);
+      line += buf;
+      const char* names[4] = {"kernels", "h2d", "d2h", "transactions"};
+      const char kinds[4] = {'k', 'h', 'd', 't'};
+      for (int c = 0; c < 4; ++c) {
+        line += ", \"";
+        line += names[c];
+        line += "\": [";
+        bool comma = false;
+        for (size_t i = 0; i < own; ++i) {
+          const TraceInterval& iv = trace_[i];
+          if (iv.kind != kinds[c]) continue;
+          std::snprintf(buf, sizeof buf, "%s[%.6f, %.6f, %llu]", comma ? ", " : "", iv.start_ms,
+                        iv.stop_ms, static_cast<unsigned long long>(iv.bytes));
+          line += buf;
           comma = true;
         }
+        line += "]";
       }
-      if (out) std::fprintf(out, "]");
-    }
-    if (out) {
-      std::fprintf(out, "}\n");
-      std::fclose(out);
+      line += "}\n";
+      if (FILE* out = std::fopen(trace_path_.c_str(), "a")) {
+        std::fwrite(line.data(), 1, line.size(), out);
+        std::fclose(out);
+      }
     }
     t_.transactions_completed += kernels_in_operation_ + transactions_in_operation_;
     t_.algorithm_selections += kernels_in_operation_;
@@ -1525,7 +1551,7 @@ Error Runtime::finish_operation(uint64_t operation_id) {
     t_.cuda_free_bytes_minimum = std::min(t_.cuda_free_bytes_minimum, free_bytes);
     t_.cuda_free_bytes_end = free_bytes;
   }
-  if (!first && guard_tripped) {
+  if (!first && guard_tripped_) {
     launches_blocked_ = true;
     ++t_.watchdog_rejections;
     return make_error(XVRAM_STATUS_TIMEOUT, "transaction", "duration_guard",

@@ -166,6 +166,10 @@ struct TraceInterval {
   Event stop = nullptr;
   uint64_t bytes = 0;
   char kind = 'k'; // 'k' kernel, 'h' H2D, 'd' D2H, 't' transaction callback work
+  // Start and stop in ms from the operation's start event, once both events
+  // have completed (Runtime::time_intervals).
+  bool timed = false;
+  float start_ms = 0.f, stop_ms = 0.f;
 };
 
 // One access of a working-set transaction (allocation-relative bytes).
@@ -336,6 +340,12 @@ public:
 
   bool tracing() const { return !trace_path_.empty(); }
   void trace_push(const TraceInterval& interval) { trace_.push_back(interval); }
+  // Times the operation's intervals whose events have completed, in order,
+  // from the first untimed one; with `all`, every interval of the operation
+  // (its streams have drained). Kernel and callback durations feed the
+  // duration guard. Run while the host would otherwise wait, so that little is
+  // left when the operation ends.
+  void time_intervals(bool all);
 
 private:
   struct ChunkUse {
@@ -418,6 +428,9 @@ private:
   Event op_start_ = nullptr;
   // Host clock at begin_operation (the trace's host timestamps count from it).
   std::chrono::steady_clock::time_point op_host_start_{};
+  size_t trace_timed_ = 0;     // trace_[0 .. trace_timed_) are timed
+  bool op_start_seen_ = false; // op_start_ has completed (intervals can be timed)
+  bool guard_tripped_ = false; // a kernel or callback of the operation exceeded the guard
   std::vector<Event> event_pool_;
   std::vector<Event> events_in_use_;
   uint64_t op_serial_ = 0; // operations begun so far
