@@ -1,8 +1,9 @@
 """Launches over two K panels on the MI355X, through the C ABI.
 
-A 4096 x 4096 x 16384 N/T product under 64 MiB frames plans 4096 x 4096 x
-4096 tiles, four K panels per C tile, two panels per launch (the two-panel
-barrier-free kernel: one C-tile read and write per two panels). The first K
+A 4096 x 4096 x 16384 product under 64 MiB frames plans 4096 x 4096 x 4096
+tiles, four K panels per C tile, two panels per launch (the two-panel
+barrier-free kernels: one C-tile read and write per two panels; N/T runs
+sgemm_ring_kernel, the other forms sgemm_ring8_kernel). The first K
 pass runs as two one-panel launches (the operation's first pass is
 link-bound), the first of them as two 2048-deep slices waiting for their
 panels slice by slice; the last launch is one two-panel dispatch (beta 1 over
@@ -53,18 +54,33 @@ def session(lib):
     return xv.Session(lib, chunk_size_bytes=64 * MiB, cache_target_bytes=16 * 64 * MiB)
 
 
-def test_two_panel_pattern_every_element(traced, synth, oracle_mod):
+OPS = {"NT": (abi.OP_N, abi.OP_T), "NN": (abi.OP_N, abi.OP_N), "TN": (abi.OP_T, abi.OP_N),
+       "TT": (abi.OP_T, abi.OP_T)}
+
+
+def pattern_plan(s, synth, ops, k):
+    """A (op(A) M x k) and B (op(B) k x N) filled with the analytic pattern,
+    stored for `ops` (column-major); C M x N."""
+    a, b, c = s.allocation(M * k * 4), s.allocation(N * k * 4), s.allocation(M * N * 4)
+    a_t, b_t = ops[0] == abi.OP_T, ops[1] == abi.OP_T
+    fill_pattern(a, synth.synth_fill_pattern_a, k if a_t else M, M if a_t else k, int(a_t))
+    fill_pattern(b, synth.synth_fill_pattern_b, N if b_t else k, k if b_t else N, int(b_t))
+    am = xv.matrix(a, k, M, k) if a_t else xv.matrix(a, M, k, M)
+    bm = xv.matrix(b, N, k, N) if b_t else xv.matrix(b, k, N, k)
+    return xv.GemmPlan(s, am, bm, xv.matrix(c, M, N, M), ops[0], ops[1]), c
+
+
+@pytest.mark.parametrize("form", list(OPS))
+def test_two_panel_pattern_every_element(traced, synth, oracle_mod, form):
+    """Every form: N/T runs sgemm_ring_kernel<true>, the others the two-panel
+    instance of sgemm_ring8_kernel."""
     lib = xv.load()
     s = session(lib)
     try:
-        a, b, c = s.allocation(M * K * 4), s.allocation(N * K * 4), s.allocation(M * N * 4)
-        fill_pattern(a, synth.synth_fill_pattern_a, M, K, 0)
-        fill_pattern(b, synth.synth_fill_pattern_b, N, K, 1)
-        plan = xv.GemmPlan(s, xv.matrix(a, M, K, M), xv.matrix(b, N, K, N), xv.matrix(c, M, N, M),
-                           abi.OP_N, abi.OP_T)
+        plan, c = pattern_plan(s, synth, OPS[form], K)
         info = plan.info()
-        log(f"plan {info.tile_m}x{info.tile_n}x{info.tile_k}, {info.tile_count} tiles, working set "
-            f"{info.maximum_working_set_bytes >> 20} MiB")
+        log(f"{form}: plan {info.tile_m}x{info.tile_n}x{info.tile_k}, {info.tile_count} tiles, "
+            f"working set {info.maximum_working_set_bytes >> 20} MiB")
         assert (info.tile_m, info.tile_n, info.tile_k, info.tile_count) == (4096, 4096, 4096, 4)
         assert info.maximum_working_set_bytes == 5 * 64 * MiB  # two panels per launch
         expect = oracle_mod.pattern_expected_matrix(M, N, K).astype(np.float32)
@@ -72,7 +88,7 @@ def test_two_panel_pattern_every_element(traced, synth, oracle_mod):
             plan.execute()
             got = c.read(dtype=np.float32).reshape(N, M).T
             bad = int(np.count_nonzero(got != expect))
-            log(f"execution {run}: {bad} elements differ; kernels {kernels(traced)}")
+            log(f"{form} execution {run}: {bad} elements differ; kernels {kernels(traced)}")
             assert bad == 0
         assert kernels(traced) == [4, 4]  # 2 slices + 1 + one two-panel dispatch, each time
         plan.release()
@@ -80,35 +96,37 @@ def test_two_panel_pattern_every_element(traced, synth, oracle_mod):
         closed(s)
 
 
-def test_two_panel_ragged_second_panel(traced, synth, oracle_mod):
+@pytest.mark.parametrize("form", ["NT", "NN"])
+def test_two_panel_ragged_second_panel(traced, synth, oracle_mod, form):
     """K = 14336: panels 4096, 4096, 4096, 2048; after the first pass's two
     one-panel launches, the last launch pairs a 4096-deep panel with the
-    2048-deep one (k_split 4096, k 6144)."""
+    2048-deep one: for N/T one two-panel dispatch (k_split 4096, k 6144); for
+    N/N, whose B panels hold K inside their lines, the two panels' leading
+    dimensions differ and the launch runs one dispatch per panel."""
     k = 14336
     lib = xv.load()
     s = session(lib)
     try:
-        a, b, c = s.allocation(M * k * 4), s.allocation(N * k * 4), s.allocation(M * N * 4)
-        fill_pattern(a, synth.synth_fill_pattern_a, M, k, 0)
-        fill_pattern(b, synth.synth_fill_pattern_b, N, k, 1)
-        plan = xv.GemmPlan(s, xv.matrix(a, M, k, M), xv.matrix(b, N, k, N), xv.matrix(c, M, N, M),
-                           abi.OP_N, abi.OP_T)
+        plan, c = pattern_plan(s, synth, OPS[form], k)
         info = plan.info()
         assert (info.tile_k, info.tile_count) == (4096, 4)
         plan.execute()
         got = c.read(dtype=np.float32).reshape(N, M).T
         expect = oracle_mod.pattern_expected_matrix(M, N, k).astype(np.float32)
         bad = int(np.count_nonzero(got != expect))
-        log(f"ragged second panel: {bad} elements differ; kernels {kernels(traced)}")
+        log(f"{form} ragged second panel: {bad} elements differ; kernels {kernels(traced)}")
         assert bad == 0
-        assert kernels(traced) == [4]  # 2 slices + 1 + one two-panel dispatch of 4096 + 2048
+        assert kernels(traced) == ([4] if form == "NT" else [5])
         plan.release()
     finally:
         closed(s)
 
 
-def test_two_panel_alpha_beta_epilogue(traced, synth, oracle_mod):
+@pytest.mark.parametrize("form", ["NT", "NN"])
+def test_two_panel_alpha_beta_epilogue(traced, synth, oracle_mod, form):
     from oracle.sample import SeededOperand
+
+    b_t = form == "NT"
 
     lib = xv.load()
     s = session(lib)
@@ -122,11 +140,13 @@ def test_two_panel_alpha_beta_epilogue(traced, synth, oracle_mod):
         v = s.allocation(N * 4)
         v.write(bias)
         alpha, beta = -0.75, 0.5
-        plan = xv.GemmPlan(s, xv.matrix(a, M, K, M), xv.matrix(b, N, K, N), xv.matrix(c, M, N, M),
-                           abi.OP_N, abi.OP_T, alpha, beta,
+        bm = xv.matrix(b, N, K, N) if b_t else xv.matrix(b, K, N, K)
+        plan = xv.GemmPlan(s, xv.matrix(a, M, K, M), bm, xv.matrix(c, M, N, M),
+                           abi.OP_N, OPS[form][1], alpha, beta,
                            epilogue=xv.epilogue(v, abi.BIAS_PER_COLUMN, relu=True))
         A = SeededOperand(501, M, K, False).full().astype(np.float64)   # M x K
-        B = SeededOperand(502, N, K, True).full().astype(np.float64)    # K x N (op T)
+        B = (SeededOperand(502, N, K, True) if b_t else SeededOperand(502, K, N, False)) \
+            .full().astype(np.float64)                                   # K x N
         prev = c.read(dtype=np.float32).reshape(N, M).T.astype(np.float64)
         cols = np.arange(16) * (N // 16) + rng.integers(0, N // 16, 16)
         rows = np.arange(16) * (M // 16) + rng.integers(0, M // 16, 16)
@@ -143,7 +163,7 @@ def test_two_panel_alpha_beta_epilogue(traced, synth, oracle_mod):
                 err = np.abs(got[sel_r][:, sel_c] - ref)
                 violations += int(np.count_nonzero(err > bound))
                 worst = max(worst, float(np.max(err / (bound + 1e-300))))
-            log(f"execution {run}: {len(cols)} columns + {len(rows)} rows, violations {violations}, "
+            log(f"{form} execution {run}: {len(cols)} columns + {len(rows)} rows, violations {violations}, "
                 f"err/bound {worst:.3e}; kernels {kernels(traced)}")
             assert violations == 0
             prev = got

@@ -13,6 +13,11 @@ streams its own operand halves through a private LDS ring); the N/T cases
 above with such shapes (interior, bit-exact pattern, beta = 0 over NaN,
 out-of-core panels) run it, and the ring cases below add K tails around its
 8-pair unrolled loop and 7-pair prefetch distance, alpha/beta and the epilogue.
+Launches of the other forms with such tiles and K a multiple of 8 run
+sgemm_ring8_kernel (the same scheme with k-contiguous halves loaded straight
+into LDS in 8-deep slots): the NN, TN and TT interior and pattern cases above
+run it, and the ring8 cases add its slot tails, alpha/beta and the shapes
+that fall back to sgemm_wide_kernel.
 
 Random cases are checked element by element against the FP64 oracle on three
 column ranges (first, middle and last tile columns, every row) with the bound
@@ -134,6 +139,49 @@ def test_ring_fallback_shapes_pattern(resident, oracle_mod, m, n, k):
     prob = Problem(a_op, b_op, op_b=abi.OP_T)
     out = prob.run(resident)
     assert prob.plan_info.tile_count == 1
+    expected = oracle_mod.pattern_expected_matrix(m, n, k)
+    assert np.array_equal(out.astype(np.float64), expected)
+
+
+KC_OPS = OPS[:1] + OPS[2:]
+KC_IDS = ["NN", "TN", "TT"]
+
+
+@pytest.mark.parametrize("k", [8, 24, 32, 40, 56, 1048])
+@pytest.mark.parametrize("ops", KC_OPS, ids=KC_IDS)
+def test_ring8_k_tails_pattern(resident, oracle_mod, ops, k):
+    """Barrier-free kernel of the forms with a k-contiguous operand, bit-exact
+    pattern: fewer 8-deep slots than the ring (k = 8, 24), exactly one
+    unrolled block (32), a block plus a tail (40, 56) and a long loop with a
+    3-slot tail (1048)."""
+    m, n = 4096, 4096
+    a_op, b_op = pattern_operands(m, n, k)
+    prob = Problem(a_op, b_op, op_a=ops[0], op_b=ops[1])
+    out = prob.run(resident)
+    assert prob.plan_info.tile_count == 1
+    expected = oracle_mod.pattern_expected_matrix(m, n, k)
+    assert np.array_equal(out.astype(np.float64), expected)
+
+
+@pytest.mark.parametrize("ops", KC_OPS, ids=KC_IDS)
+def test_ring8_alpha_beta(resident, oracle_mod, ops):
+    m, n, k = 4608, 4096, 1000
+    prob = Problem(uniform(oracle_mod, m, k, 1701), uniform(oracle_mod, k, n, 1702),
+                   uniform(oracle_mod, m, n, 1703), op_a=ops[0], op_b=ops[1], alpha=-1.25,
+                   beta=0.75)
+    out = prob.run(resident)
+    sampled_check(oracle_mod, prob, out, f"ring8 alpha/beta {ops}")
+
+
+@pytest.mark.parametrize("ops,m,k", [(OPS[0], 4096, 1004), (OPS[2], 4100, 1040), (OPS[3], 4096, 1020)],
+                         ids=["NN-k%8", "TN-m%256", "TT-k%8"])
+def test_ring8_fallback_shapes_pattern(resident, oracle_mod, ops, m, k):
+    """Launches just outside that kernel's conditions (K not a multiple of 8,
+    m not a multiple of 256) run sgemm_wide_kernel: bit-exact pattern."""
+    n = 4096
+    a_op, b_op = pattern_operands(m, n, k)
+    prob = Problem(a_op, b_op, op_a=ops[0], op_b=ops[1])
+    out = prob.run(resident)
     expected = oracle_mod.pattern_expected_matrix(m, n, k)
     assert np.array_equal(out.astype(np.float64), expected)
 

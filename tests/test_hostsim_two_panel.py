@@ -1,8 +1,8 @@
 """CPU tests of launches over two K panels, over libxvram_hostsim.so.
 
-Short N/T launches of interior 256 x 256 tiles (a C tile of at least 4096 x
-4096 elements) take two K panels per launch when the schedule's H2D traffic
-does not grow: the tile kernel then reads and writes the C tile once per two
+Short launches of interior 256 x 256 tiles (a C tile of at least 4096 x 4096
+elements; K a multiple of 4 for N/T, of 8 for the other forms) take two K
+panels per launch when the schedule's H2D traffic does not grow: the tile kernel then reads and writes the C tile once per two
 panels. The simulated device enforces the gfx950 two-panel launch contract
 (xvram_amd/csrc/sgemm_launch.hpp) and computes each element's K products in
 order, so these cases check the planner's choice, the executor's acquisition
@@ -46,13 +46,17 @@ def kernels_per_operation(trace):
     return [len(json.loads(line)["kernels"]) for line in open(trace)]
 
 
-def run_nt(s, a_op, b_op, c0=None, alpha=1.0, beta=0.0, tile_k=32, epilogue=None, bias=None):
-    """C (column-major) = alpha * A * B + beta * C0 with A stored op-N and B
-    stored op-T (n x k), tile hints (4096, 4096, tile_k)."""
+def run_nt(s, a_op, b_op, c0=None, alpha=1.0, beta=0.0, tile_k=32, epilogue=None, bias=None,
+           ops=(abi.OP_N, abi.OP_T)):
+    """C (column-major) = alpha * op(A) * op(B) + beta * C0 with A and B stored
+    for `ops` (default: A op-N, m x k, and B op-T, n x k), tile hints (4096,
+    4096, tile_k)."""
     m, k = a_op.shape
     n = b_op.shape[1]
-    a_flat, lda = storage(np.ascontiguousarray(a_op), abi.COLUMN_MAJOR)
-    b_flat, ldb = storage(np.ascontiguousarray(b_op.T), abi.COLUMN_MAJOR)
+    a_stored = a_op if ops[0] == abi.OP_N else a_op.T
+    b_stored = b_op if ops[1] == abi.OP_N else b_op.T
+    a_flat, lda = storage(np.ascontiguousarray(a_stored), abi.COLUMN_MAJOR)
+    b_flat, ldb = storage(np.ascontiguousarray(b_stored), abi.COLUMN_MAJOR)
     c_flat, ldc = storage(c0 if c0 is not None else np.zeros((m, n), np.float32), abi.COLUMN_MAJOR)
     A, B, C = (s.allocation(x.nbytes) for x in (a_flat, b_flat, c_flat))
     A.write(a_flat)
@@ -63,8 +67,9 @@ def run_nt(s, a_op, b_op, c0=None, alpha=1.0, beta=0.0, tile_k=32, epilogue=None
         V = s.allocation(bias.nbytes)
         V.write(bias)
         ep = xv.epilogue(V, abi.BIAS_PER_COLUMN, relu=epilogue == "relu")
-    plan = xv.GemmPlan(s, xv.matrix(A, m, k, lda), xv.matrix(B, n, k, ldb), xv.matrix(C, m, n, ldc),
-                       abi.OP_N, abi.OP_T, alpha, beta, tile_hints=(4096, 4096, tile_k), epilogue=ep)
+    plan = xv.GemmPlan(s, xv.matrix(A, *a_stored.shape, lda), xv.matrix(B, *b_stored.shape, ldb),
+                       xv.matrix(C, m, n, ldc), ops[0], ops[1], alpha, beta,
+                       tile_hints=(4096, 4096, tile_k), epilogue=ep)
     info = plan.info()
     plan.execute()
     out = C.read(dtype=np.float32).reshape(n, ldc)[:, :m].T
@@ -85,6 +90,47 @@ def test_two_panel_launches_are_exact(sim, oracle_mod):
     assert kernels_per_operation(trace) == [4]           # one dispatch per launch
     assert t.transactions_completed == info.tile_count   # one retired tile per K panel
     assert t.bytes_h2d == (M * k + k * N) * 4            # every panel loaded once
+    assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(M, N, k))
+
+
+@pytest.mark.parametrize("ops", [(abi.OP_N, abi.OP_N), (abi.OP_T, abi.OP_N), (abi.OP_T, abi.OP_T)],
+                         ids=["NN", "TN", "TT"])
+def test_two_panel_launches_other_forms(sim, oracle_mod, ops):
+    """The same schedule for the forms with a k-contiguous operand (K a
+    multiple of 8): one dispatch per launch, bit-exact pattern, and seeded
+    U[-1,1) data within the FP64 bound on a column subset."""
+    lib, trace = sim
+    k = 192
+    a_op, b_op = pattern_operands(M, N, k)
+    with session(lib) as s:
+        out, info = run_nt(s, a_op, b_op, ops=ops)
+    assert info.tile_count == 6 and info.maximum_working_set_bytes == 5 * 64 * MiB
+    assert kernels_per_operation(trace) == [4]
+    assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(M, N, k))
+    k = 128
+    a_op = uniform(oracle_mod, M, k, 41)
+    b_op = uniform(oracle_mod, k, N, 42)
+    with session(lib) as s:
+        out, info = run_nt(s, a_op, b_op, ops=ops)
+    assert kernels_per_operation(trace) == [4, 3]
+    cols = np.arange(0, N, 101)
+    ref = a_op.astype(np.float64) @ b_op[:, cols].astype(np.float64)
+    bound = 4 * k * 2.0 ** -24 * (np.abs(a_op).astype(np.float64) @
+                                  np.abs(b_op[:, cols]).astype(np.float64)) + 1e-30
+    assert np.all(np.abs(out[:, cols].astype(np.float64) - ref) <= bound)
+
+
+def test_ragged_pair_of_a_k_contiguous_operand_runs_per_panel(sim, oracle_mod):
+    """N/N, K = 112 in 32-deep panels: B's panels hold K inside their lines, so
+    the 32-deep and 16-deep panels of the last launch have different leading
+    dimensions and that launch runs one dispatch per panel."""
+    lib, trace = sim
+    k = 112
+    a_op, b_op = pattern_operands(M, N, k)
+    with session(lib) as s:
+        out, info = run_nt(s, a_op, b_op, ops=(abi.OP_N, abi.OP_N))
+    assert info.tile_count == 4
+    assert kernels_per_operation(trace) == [4]
     assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(M, N, k))
 
 

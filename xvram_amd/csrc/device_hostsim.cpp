@@ -237,20 +237,7 @@ public:
                          l.ldb % 4 == 0 && l.ldc % 4 == 0 && l.padded;
     if (l.m <= 0 || l.n <= 0 || l.k <= 0 || !aligned) return 1; // hipErrorInvalidValue
     const bool two = l.a2 != nullptr || l.b2 != nullptr;
-    if (two) {
-      // Two K panels: the N/T interior-tile contract of the gfx950 kernel.
-      constexpr int64_t kLimit = int64_t(1) << 31;
-      const bool ok = l.a2 != nullptr && l.b2 != nullptr &&
-                      reinterpret_cast<uintptr_t>(l.a2) % 16 == 0 &&
-                      reinterpret_cast<uintptr_t>(l.b2) % 16 == 0 && !l.a_kcontig && l.b_ncontig &&
-                      l.m % 256 == 0 && l.n % 256 == 0 && l.k % 4 == 0 && l.k_split % 32 == 0 &&
-                      l.k_split > 0 && l.k_split < l.k && (l.m / 256) * (l.n / 256) >= 256 &&
-                      int64_t{l.k_split} * l.lda * 4 < kLimit &&
-                      int64_t{l.k - l.k_split} * l.lda * 4 < kLimit &&
-                      int64_t{l.k_split} * l.ldb * 4 < kLimit &&
-                      int64_t{l.k - l.k_split} * l.ldb * 4 < kLimit;
-      if (!ok) return 1; // hipErrorInvalidValue
-    }
+    if (two && !kernels::two_panel_valid(l)) return 1; // hipErrorInvalidValue
     const int64_t k1 = two ? l.k_split : l.k; // K rows read from a / b
     const auto span = [](int64_t rows, int64_t cols, int64_t ld) {
       return static_cast<uint64_t>(((cols - 1) * ld + rows) * 4);
@@ -261,8 +248,11 @@ public:
         !accessible(reinterpret_cast<uint64_t>(l.b), span(b_rows, b_cols, l.ldb)) ||
         !accessible(reinterpret_cast<uint64_t>(l.c), span(l.m, l.n, l.ldc)))
       return kSimBadAccess;
-    if (two && (!accessible(reinterpret_cast<uint64_t>(l.a2), span(l.m, l.k - k1, l.lda)) ||
-                !accessible(reinterpret_cast<uint64_t>(l.b2), span(l.n, l.k - k1, l.ldb))))
+    const int64_t k2 = l.k - k1; // K rows read from a2 / b2
+    if (two && (!accessible(reinterpret_cast<uint64_t>(l.a2),
+                            span(l.a_kcontig ? k2 : l.m, l.a_kcontig ? l.m : k2, l.lda)) ||
+                !accessible(reinterpret_cast<uint64_t>(l.b2),
+                            span(l.b_ncontig ? l.n : k2, l.b_ncontig ? k2 : l.n, l.ldb))))
       return kSimBadAccess;
     if ((l.bias_row && !accessible(reinterpret_cast<uint64_t>(l.bias_row), l.m * 4ull)) ||
         (l.bias_col && !accessible(reinterpret_cast<uint64_t>(l.bias_col), l.n * 4ull)))
@@ -281,9 +271,12 @@ public:
           acc[i] += x * y;
         }
       }
-      for (int64_t p = 0; p < l.k - k1; ++p) { // second panel (N/T only)
-        const float y = l.b2[j + p * l.ldb];
-        for (int64_t i = 0; i < l.m; ++i) acc[i] += l.a2[i + p * l.lda] * y;
+      for (int64_t p = 0; p < k2; ++p) { // second panel
+        const float y = l.b_ncontig ? l.b2[j + p * l.ldb] : l.b2[p + j * l.ldb];
+        for (int64_t i = 0; i < l.m; ++i) {
+          const float x = l.a_kcontig ? l.a2[p + i * l.lda] : l.a2[i + p * l.lda];
+          acc[i] += x * y;
+        }
       }
       for (int64_t i = 0; i < l.m; ++i) {
         float& out = l.c[i + j * l.ldc];

@@ -455,10 +455,11 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   // before their last use (32768^3 under 2 GiB of 64 MiB frames: 23 % more H2D).
   uint32_t panels = 1;
   const double one_panel_flops = launch_flops(tm, tn, bk);
-  const bool two_panel_kernel = !p.a.transposed && p.b.transposed && tm % 256 == 0 &&
-                                tn % 256 == 0 && (tm / 256) * (tn / 256) >= 256 &&
-                                p.m % tm == 0 && p.n % tn == 0 && bk % 32 == 0 &&
-                                p.k % 4 == 0 && out.panels_k >= 2;
+  const bool nt = !p.a.transposed && p.b.transposed;
+  const bool two_panel_kernel = tm % 256 == 0 && tn % 256 == 0 &&
+                                (tm / 256) * (tn / 256) >= 256 && p.m % tm == 0 &&
+                                p.n % tn == 0 && bk % 32 == 0 && p.k % (nt ? 4 : 8) == 0 &&
+                                out.panels_k >= 2;
   if (two_panel_kernel && one_panel_flops <= kTwoPanelMaxFlops &&
       (max_launch_flops == 0 || 2.0 * one_panel_flops <= static_cast<double>(max_launch_flops))) {
     const uint32_t ahead2 = std::max<uint32_t>(1, lookahead / 2);
@@ -757,10 +758,11 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     // The dispatches of this launch: K slices of each panel (sliced fill),
     // one two-panel dispatch, or one dispatch per panel.
     std::vector<KernelPiece> pieces;
-    const bool two_ok = g.panels == 2 && !acq.slice && !p.a.transposed && p.b.transposed &&
-                        g.h % 256 == 0 && g.g % 256 == 0 && (g.h / 256) * (g.g / 256) >= 256 &&
-                        g.w[0] % 32 == 0 && (g.w[0] + g.w[1]) % 4 == 0 &&
-                        lda_of(0) == lda_of(1) && ldb_of(0) == ldb_of(1);
+    const bool nt = !p.a.transposed && p.b.transposed;
+    const bool two_ok = g.panels == 2 && !acq.slice && g.h % 256 == 0 && g.g % 256 == 0 &&
+                        (g.h / 256) * (g.g / 256) >= 256 && g.w[0] % 32 == 0 &&
+                        (g.w[0] + g.w[1]) % (nt ? 4 : 8) == 0 && lda_of(0) == lda_of(1) &&
+                        ldb_of(0) == ldb_of(1);
     if (two_ok) {
       pieces.push_back(KernelPiece{0, 0, g.w[0] + g.w[1], true, -1});
     } else {

@@ -14,10 +14,11 @@
 //
 // Two K panels (optional): with a2 / b2 set, k rows [0, k_split) of op(A) and
 // op(B) come from a / b and rows [k_split, k) from a2 / b2 (same leading
-// dimensions): one launch over two separately stored panels. Only for the
-// N/T form (a_kcontig false, b_ncontig true) with m and n multiples of 256, k
-// a multiple of 4, k_split a multiple of 32 inside (0, k), at least 256 tiles
-// of 256 x 256, 16-byte aligned a2 / b2 and each panel below 2^31 bytes;
+// dimensions): one launch over two separately stored panels. Only for m and n
+// multiples of 256 with at least 256 tiles of 256 x 256, k a multiple of 4
+// (N/T: a_kcontig false, b_ncontig true) or of 8 (the other forms), k_split a
+// multiple of 32 inside (0, k), 16-byte aligned a2 / b2 and each operand panel
+// spanning less than 2^31 bytes from its base (two_panel_valid below);
 // anything else returns hipErrorInvalidValue.
 //
 // start_event / stop_event (hipEvent_t, optional) are recorded by the dispatch
@@ -52,5 +53,25 @@ struct SgemmLaunch {
 
 // Enqueues the launch on `stream` (a hipStream_t); returns a hipError_t.
 int launch_sgemm(const SgemmLaunch& launch, void* stream);
+
+// The two-panel part of the contract (a2 / b2 set); the one-panel part is
+// checked separately.
+inline bool two_panel_valid(const SgemmLaunch& l) {
+  constexpr int64_t kLimit = int64_t(1) << 31;
+  if (l.a2 == nullptr || l.b2 == nullptr || reinterpret_cast<uintptr_t>(l.a2) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(l.b2) % 16 != 0)
+    return false;
+  const bool nt = !l.a_kcontig && l.b_ncontig;
+  if (l.m % 256 != 0 || l.n % 256 != 0 || int64_t{l.m / 256} * (l.n / 256) < 256 ||
+      l.k % (nt ? 4 : 8) != 0 || l.k_split % 32 != 0 || l.k_split <= 0 || l.k_split >= l.k)
+    return false;
+  for (const int64_t kk : {int64_t{l.k_split}, int64_t{l.k - l.k_split}}) {
+    // Floats from a panel's base to the end of its last line.
+    const int64_t a = l.a_kcontig ? (l.m - 1) * l.lda + kk : kk * l.lda;
+    const int64_t b = l.b_ncontig ? kk * l.ldb : (l.n - 1) * l.ldb + kk;
+    if (a * 4 >= kLimit || b * 4 >= kLimit) return false;
+  }
+  return true;
+}
 
 } // namespace xvram::kernels

@@ -327,24 +327,11 @@ int launch_sgemm(const SgemmLaunch& launch, void* stream) {
   auto* e0 = static_cast<hipEvent_t>(launch.start_event);
   auto* e1 = static_cast<hipEvent_t>(launch.stop_event);
   if (launch.a2 != nullptr || launch.b2 != nullptr) {
-    // Two K panels: the barrier-free N/T kernel only.
-    constexpr int64_t kLimit = int64_t(1) << 31;
-    const int t = wide_tile();
-    const bool ok =
-        launch.a2 != nullptr && launch.b2 != nullptr &&
-        reinterpret_cast<uintptr_t>(launch.a2) % 16 == 0 &&
-        reinterpret_cast<uintptr_t>(launch.b2) % 16 == 0 && !launch.a_kcontig &&
-        launch.b_ncontig && launch.m % t == 0 && launch.n % t == 0 && launch.k % 4 == 0 &&
-        launch.k_split % 32 == 0 && launch.k_split > 0 && launch.k_split < launch.k &&
-        (int64_t)(launch.m / t) * (launch.n / t) >= kWideMinTiles &&
-        (int64_t)launch.k_split * launch.lda * 4 < kLimit &&
-        (int64_t)(launch.k - launch.k_split) * launch.lda * 4 < kLimit &&
-        (int64_t)launch.k_split * launch.ldb * 4 < kLimit &&
-        (int64_t)(launch.k - launch.k_split) * launch.ldb * 4 < kLimit;
-    if (!ok) return static_cast<int>(hipErrorInvalidValue);
-    p.tiles_m = launch.m / t;
-    p.tiles_n = launch.n / t;
-    return static_cast<int>(launch_wide(p, false, true, s, e0, e1));
+    // Two K panels: the barrier-free kernels only.
+    if (!two_panel_valid(launch)) return static_cast<int>(hipErrorInvalidValue);
+    p.tiles_m = launch.m / wide_tile();
+    p.tiles_n = launch.n / wide_tile();
+    return static_cast<int>(launch_wide(p, launch.a_kcontig, launch.b_ncontig, s, e0, e1));
   }
   p.k_split = 0;
   if (wide_fits(launch)) {

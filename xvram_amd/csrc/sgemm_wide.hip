@@ -35,7 +35,10 @@
 // least one tile per CU. N/T launches whose tiles are all interior and whose K
 // is a multiple of 4 run sgemm_ring_kernel instead (below): the same tile and
 // MFMA sequence with each wave streaming its own operand halves through a
-// private LDS ring, so its K loop needs no workgroup barrier.
+// private LDS ring, so its K loop needs no workgroup barrier. Launches of the
+// other three forms with interior tiles and K a multiple of 8 run
+// sgemm_ring8_kernel, the same ring scheme with k-contiguous halves loaded
+// straight into LDS as well.
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
@@ -568,6 +571,233 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
   store_c_interior<4, 2, true>(p, acc, m0 + wm, n0 + wn, lrow, lhalf);
 }
 
+// ---- barrier-free kernel for layouts with a k-contiguous operand ------------
+//
+// The ring scheme above for N/N, T/N and T/T launches. An extent-contiguous
+// half (op-N A, op-T B) is loaded as k-rows as there; a k-contiguous one
+// (op-T A, op-N B) as 32-byte pieces of its lines: lane (lrow, h) of load I
+// brings k values 4h .. 4h+3 of line 4*lrow + I of the wave's half, so one
+// load covers the 32 lines that feed MFMA block I. A slot holds 8 k values
+// of both halves of the wave:
+//   extent-contiguous: row-major 8 x 128 (k-row, element), as loaded;
+//   k-contiguous:      lane (lrow, h)'s piece of block I's line at float
+//                      256*I + 128*h + 4*lrow, as loaded.
+// The MFMAs of a slot run k-steps s = 0..3 with lane half h supplying k value
+// 4h + s (one fixed order of the slot's 8 k values, the same for both
+// operands): one ds_read_b128 of a k-contiguous half gives a lane its values
+// of one block for all four k-steps, one of an extent-contiguous half its
+// values of one k-step for all four blocks. Every fragment read and every
+// load covers 64 consecutive 16-byte LDS units in runs of 32 (no bank
+// conflicts).
+//
+// Per wave kRing8 slots of 8 KB (128 KB per workgroup). Step q multiplies
+// slot q from registers; during its first 32 MFMAs it issues slot q+kRing8's
+// eight loads into the ring slot of q, whose fragments were read half a step
+// earlier; after them it waits for slot q+1 and reads its fragments into the
+// other register set. A block of kRing8 steps loads the kRing8 slots of the
+// next block, so with k_split a multiple of 8 * kRing8 (two-panel instance,
+// as in sgemm_ring_kernel) each block's loads come from one K panel.
+//
+// Used only for launches whose tiles are all interior (m and n multiples of
+// 256) and whose K is a multiple of 8: every load then stays inside the
+// tile's lines and the K extent, so no predication is needed.
+constexpr int kRing8 = 4;     // slots per wave
+constexpr int kSlotK = 8;     // k values per slot
+constexpr int kHalf8 = 1024;  // floats of one operand half per slot (128 x 8)
+static_assert(4 * kRing8 * 2 * kHalf8 * 4 <= 160 * 1024, "rings fit the LDS");
+static_assert(8 * kRing8 <= 63, "outstanding loads fit the vmcnt counter");
+static_assert(8 * kRing8 == 32, "two-panel launches split K at multiples of 32");
+
+template <int C>
+__device__ __forceinline__ float pick(const float4& v) {
+  if constexpr (C == 0) return v.x;
+  else if constexpr (C == 1) return v.y;
+  else if constexpr (C == 2) return v.z;
+  else return v.w;
+}
+
+// Waits until at most 8 * `after` vector loads are outstanding.
+__device__ __forceinline__ void wait_slots(int after) {
+  if (after >= 3) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+  else if (after == 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else if (after == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+template <bool kAKC, bool kBKC, bool kTwo>
+__global__ __launch_bounds__(kThreads, 1) void sgemm_ring8_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) float lds[4 * kRing8 * 2 * kHalf8];
+  asm volatile("; accumulators in AGPRs" ::: "a0");
+
+  int tile_m, tile_n;
+  tile_coords<kGroupM>(p, tile_m, tile_n);
+  const int m0 = tile_m * kTile;
+  const int n0 = tile_n * kTile;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = (wave & 1) * kWave;
+  const int wn = (wave >> 1) * kWave;
+  const int lrow = lane & 31;
+  const int lhalf = lane >> 5;
+
+  float16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int slots = p.k / kSlotK;
+  const int k1 = kTwo ? p.k_split : p.k;
+  const int q_split = k1 / kSlotK;
+  // A panel's descriptor from the tile's first element: an extent-contiguous
+  // X(e, k) = x[e + k*ld] spans (kk*ld - e0) floats from x + e0 (to the end of
+  // k-row kk-1), a k-contiguous X(e, k) = x[k + e*ld] spans 255*ld + kk
+  // floats from x + e0*ld (the tile's 256 lines, kk values each).
+  const auto rsrc = [](const float* x, int64_t ld, int e0, int kk, bool kc) {
+    return kc ? panel_rsrc(x + (int64_t)e0 * ld, (uint32_t)((255 * ld + kk) * 4))
+              : panel_rsrc(x + e0, (uint32_t)(((int64_t)kk * ld - e0) * 4));
+  };
+  const RingSource lo{rsrc(p.a, p.lda, m0, k1, kAKC), rsrc(p.b, p.ldb, n0, k1, kBKC), 0};
+  RingSource hi = lo;
+  if constexpr (kTwo) {
+    const int k2 = p.k - k1;
+    hi = RingSource{rsrc(p.a2, p.lda, m0, k2, kAKC), rsrc(p.b2, p.ldb, n0, k2, kBKC), q_split};
+  }
+  // Lane offsets of load I of a half in its panel's first slot: k-row 2I + h,
+  // elements w + 4*lrow .. +3 (extent-contiguous), or line w + 4*lrow + I, k
+  // values 4h .. 4h+3 (k-contiguous). A slot advances K by 8 rows / values.
+  const auto voff = [&](int64_t ld, int w, int i, bool kc) {
+    return kc ? (uint32_t)(((int64_t)(w + 4 * lrow + i) * ld + 4 * lhalf) * 4)
+              : (uint32_t)(((int64_t)(2 * i + lhalf) * ld + w + 4 * lrow) * 4);
+  };
+  uint32_t vo_a[4], vo_b[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    vo_a[i] = voff(p.lda, wm, i, kAKC);
+    vo_b[i] = voff(p.ldb, wn, i, kBKC);
+  }
+  const uint32_t adv_a = kAKC ? kSlotK * 4 : (uint32_t)(kSlotK * 4 * p.lda);
+  const uint32_t adv_b = kBKC ? kSlotK * 4 : (uint32_t)(kSlotK * 4 * p.ldb);
+  float* ring = lds + wave * (kRing8 * 2 * kHalf8);
+  const uint32_t ring_lds = lds_byte_addr(ring);
+
+  // Load L (0..3: A, 4..7: B; load index L & 3) of slot q into ring slot S.
+  auto issue = [&]<int S, int L>(int q, Int<S>, Int<L>, const RingSource& src) {
+    constexpr int off = (S * 2 * kHalf8 + (L >> 2) * kHalf8 + (L & 3) * 256) * 4;
+    const uint32_t qq = (uint32_t)(q - src.base);
+    if constexpr (L < 4) {
+      const uint32_t so = __builtin_amdgcn_readfirstlane(adv_a * qq);
+      load_lds16<off>(ring_lds, vo_a[L & 3], src.a, so);
+    } else {
+      const uint32_t so = __builtin_amdgcn_readfirstlane(adv_b * qq);
+      load_lds16<off>(ring_lds, vo_b[L & 3], src.b, so);
+    }
+  };
+  // Fragments of ring slot S into register set R: x is the k-step of an
+  // extent-contiguous half and the block of a k-contiguous one.
+  float4 fa[2][4], fb[2][4];
+  auto read_frag = [&]<int S, int R>(Int<S>, Int<R>) {
+    const float* slot = ring + S * 2 * kHalf8;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int kc_off = 256 * x + 128 * lhalf + 4 * lrow;
+      const int ex_off = (4 * lhalf + x) * kWave + 4 * lrow;
+      fa[R][x] = *reinterpret_cast<const float4*>(slot + (kAKC ? kc_off : ex_off));
+      fb[R][x] = *reinterpret_cast<const float4*>(slot + kHalf8 + (kBKC ? kc_off : ex_off));
+    }
+  };
+  // MFMA X of a slot: k-step X / 16, row block (X / 4) % 4, column block X % 4.
+  auto mfma_one = [&]<int R, int X>(Int<R>, Int<X>) {
+    constexpr int s = X / 16, i = (X % 16) / 4, j = X % 4;
+    float ao, bo;
+    if constexpr (kAKC) ao = pick<s>(fa[R][i]);
+    else ao = pick<i>(fa[R][s]);
+    if constexpr (kBKC) bo = pick<s>(fb[R][j]);
+    else bo = pick<j>(fb[R][s]);
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(ao, bo, acc[i][j], 0, 0, 0);
+  };
+
+  // Slots 0 .. kRing8-1 in flight, then slot 0's fragments in registers.
+  auto issue_slot = [&]<int S>(Int<S>) {
+    [&]<int... L>(std::integer_sequence<int, L...>) {
+      (issue(S, Int<S>{}, Int<L>{}, lo), ...);
+    }(std::make_integer_sequence<int, 8>{});
+  };
+  [&]<int... S>(std::integer_sequence<int, S...>) {
+    ((S < slots ? (issue_slot(Int<S>{}), 0) : 0), ...);
+  }(std::make_integer_sequence<int, kRing8>{});
+  wait_slots(min(slots, kRing8) - 1);
+  read_frag(Int<0>{}, Int<0>{});
+
+  // Step q (q % kRing8 == J). `load`: issue slot q + kRing8. `after`: slots
+  // issued beyond q + 1 when slot q + 1 is waited for (-1: no slot q + 1).
+  auto step = [&]<int J, bool kTail>(int q, Int<J>, std::bool_constant<kTail>,
+                                      const RingSource& src) {
+    constexpr int cur = J & 1, nxt = cur ^ 1;
+    const bool load = !kTail || q + kRing8 < slots;
+    const int after = !kTail ? kRing8 - 1
+                      : q + 1 < slots ? min(q + kRing8, slots - 1) - (q + 1) : -1;
+    // Slot q's fragment reads (issued half a step ago) are complete before
+    // its ring slot is refilled.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    [&]<int... X>(std::integer_sequence<int, X...>) {
+      (([&] {
+         if constexpr (X % 4 == 0 && X < 32) {
+           if (load) {
+             __builtin_amdgcn_sched_barrier(0);
+             issue(q + kRing8, Int<J>{}, Int<X / 4>{}, src);
+             __builtin_amdgcn_sched_barrier(0);
+           }
+         }
+         if constexpr (X == 32) {
+           if (after >= 0) {
+             __builtin_amdgcn_sched_barrier(0);
+             if constexpr (!kTail) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+             else wait_slots(after);
+             read_frag(Int<(J + 1) % kRing8>{}, Int<nxt>{});
+             __builtin_amdgcn_sched_barrier(0);
+           }
+         }
+         mfma_one(Int<cur>{}, Int<X>{});
+       }()),
+       ...);
+    }(std::make_integer_sequence<int, 64>{});
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  static_assert(kRing8 - 1 == 3, "steady-state wait above");
+
+  const auto block = [&](int q0, const RingSource& src) {
+    [&]<int... J>(std::integer_sequence<int, J...>) {
+      (step(q0 + J, Int<J>{}, std::false_type{}, src), ...);
+    }(std::make_integer_sequence<int, kRing8>{});
+  };
+  int q = 0;
+  // Full blocks: the next block's slots all exist (q + 2 * kRing8 <= slots).
+  if constexpr (kTwo) {
+    for (; q + 2 * kRing8 <= slots && q + kRing8 < q_split; q += kRing8) block(q, lo);
+    for (; q + 2 * kRing8 <= slots; q += kRing8) block(q, hi);
+  } else {
+    for (; q + 2 * kRing8 <= slots; q += kRing8) block(q, lo);
+  }
+  for (; q < slots; q += kRing8) {
+    const RingSource& src = (kTwo && q + kRing8 >= q_split) ? hi : lo;
+    [&]<int... J>(std::integer_sequence<int, J...>) {
+      ((q + J < slots ? (step(q + J, Int<J>{}, std::true_type{}, src), 0) : 0), ...);
+    }(std::make_integer_sequence<int, kRing8>{});
+  }
+
+  // The lane id is produced again here instead of being kept live across the
+  // K loop: the epilogue needs every register, and addresses derived from a
+  // value computed before the loop were hoisted above it and spilled.
+  int lane_e;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_e));
+  store_c_interior<4, 2, true>(p, acc, m0 + wm, n0 + wn, lane_e & 31, lane_e >> 5);
+}
+
 } // namespace
 
 int wide_tile() { return kTile; }
@@ -581,11 +811,23 @@ hipError_t launch_wide(const Params& p, bool a_kcontig, bool b_ncontig, hipStrea
                        hipEvent_t start, hipEvent_t stop) {
   const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
   const dim3 block(kThreads);
-  if (!a_kcontig && b_ncontig && p.m % kTile == 0 && p.n % kTile == 0 && p.k % 4 == 0) {
+  const bool interior = p.m % kTile == 0 && p.n % kTile == 0;
+  if (interior && !a_kcontig && b_ncontig && p.k % 4 == 0) {
     if (p.a2 != nullptr)
       hipExtLaunchKernelGGL(sgemm_ring_kernel<true>, grid, block, 0, stream, start, stop, 0, p);
     else
       hipExtLaunchKernelGGL(sgemm_ring_kernel<false>, grid, block, 0, stream, start, stop, 0, p);
+  } else if (interior && p.k % kSlotK == 0) {
+    const bool two = p.a2 != nullptr;
+    if (!a_kcontig && !b_ncontig)
+      two ? hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, true>), grid, block, 0, stream, start, stop, 0, p)
+          : hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, false>), grid, block, 0, stream, start, stop, 0, p);
+    else if (a_kcontig && !b_ncontig)
+      two ? hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, true>), grid, block, 0, stream, start, stop, 0, p)
+          : hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, false>), grid, block, 0, stream, start, stop, 0, p);
+    else
+      two ? hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, true>), grid, block, 0, stream, start, stop, 0, p)
+          : hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, false>), grid, block, 0, stream, start, stop, 0, p);
   } else if (!a_kcontig && !b_ncontig)
     hipExtLaunchKernelGGL((sgemm_wide_kernel<false, false>), grid, block, 0, stream, start, stop, 0, p);
   else if (!a_kcontig && b_ncontig)
