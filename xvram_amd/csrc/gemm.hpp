@@ -149,8 +149,9 @@ struct GemmPlanData {
 constexpr double kDualLaneMaxFlops = 3.0e11;
 
 // One-panel launches of at most this many FLOPs take two K panels per launch
-// when the two-panel tile kernel accepts them (N/T, interior 256 x 256 tiles,
-// at least one per CU, panel depth a multiple of 32) and the schedule keeps
+// when a two-panel tile kernel accepts them (interior 256 x 256 tiles, at
+// least one per CU, panel depth a multiple of 32, K a multiple of 4 for N/T
+// and of 8 for the other forms) and the schedule keeps
 // its H2D traffic: each launch pays a C-tile read and write through HBM and a
 // prologue, ~20 us on a 4096 x 4096 tile (2 % of a 4096-deep launch).
 constexpr double kTwoPanelMaxFlops = 1.5e11;

@@ -277,7 +277,7 @@ hipError_t launch_variant(const Params& p, hipStream_t stream, hipEvent_t start,
 } // namespace
 
 // A launch with at least this many 256 x 256 tiles (one per CU of the chip)
-// runs a 256 x 256 kernel (sgemm_wide.hip picks the barrier-free one for N/T
+// runs a 256 x 256 kernel (sgemm_wide.hip picks a barrier-free one for
 // launches of interior tiles); smaller ones keep two 256 x 128 tiles per CU.
 constexpr int64_t kWideMinTiles = 256;
 

@@ -803,10 +803,11 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring8_kernel(Params p) {
 int wide_tile() { return kTile; }
 
 // Launches a 256 x 256 kernel for `p` (tiles_m / tiles_n already in 256s):
-// the barrier-free one for N/T launches of interior tiles only and K a
-// multiple of 4 (its two-panel instance when p.a2 is set; the caller has
-// checked that launch's contract), else sgemm_wide_kernel. start / stop
-// (optional) are recorded by the dispatch itself.
+// for launches of interior tiles only, sgemm_ring_kernel (N/T, K a multiple
+// of 4) or sgemm_ring8_kernel (the other forms, K a multiple of 8), their
+// two-panel instance when p.a2 is set (the caller has checked that launch's
+// contract); else sgemm_wide_kernel. start / stop (optional) are recorded by
+// the dispatch itself.
 hipError_t launch_wide(const Params& p, bool a_kcontig, bool b_ncontig, hipStream_t stream,
                        hipEvent_t start, hipEvent_t stop) {
   const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
