@@ -783,8 +783,8 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
       if (kp.slice >= 0) {
         for (const std::vector<Event>* ready : {&acq.a_ready[t], &acq.b_ready[t]}) {
           if (ready->empty()) continue;
-          if (int rc = rt.device().stream_wait_event(cs, (*ready)[kp.slice])) {
-            result = rt.device_failure(rc, "gemm", "stream_wait");
+          if (Error e = rt.stream_wait(cs, (*ready)[kp.slice])) {
+            result = e;
             break;
           }
         }
@@ -823,13 +823,14 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
         }
         k.relu = p.relu;
       }
-      // The launch's timing events are recorded by its dispatch; the last
+      // The launch's timing events are recorded by its dispatch (a start
+      // event only after a wait on the lane: Runtime::record_kernel); the last
       // dispatch's stop event is also the retire event of the launch's frames
       // (each marker packet between kernels would otherwise cost the compute
       // stream a few microseconds).
       TraceInterval iv;
       iv.kind = 'k';
-      if (Error e = rt.record_kernel(iv.start, iv.stop)) {
+      if (Error e = rt.record_kernel(iv, lane)) {
         result = e;
         break;
       }

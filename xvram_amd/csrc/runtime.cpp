@@ -149,6 +149,7 @@ Error Runtime::setup() {
   if (int rc = device_->stream_create(&h2d_)) return device_failure(rc, "setup", "stream");
   if (int rc = device_->stream_create(&d2h_)) return device_failure(rc, "setup", "stream");
   if (int rc = device_->event_create(&op_start_)) return device_failure(rc, "setup", "event");
+  if (int rc = device_->event_create(&op_start2_)) return device_failure(rc, "setup", "event");
   if (int rc = device_->event_create(&carry_fence_)) return device_failure(rc, "setup", "event");
   t_.flags = XVRAM_TELEMETRY_NO_PHYSICAL_ALIASES | XVRAM_TELEMETRY_STABLE_VIRTUAL_ADDRESSES;
   setup_done_ = true;
@@ -255,8 +256,9 @@ Error Runtime::close() {
   carried_trace_.clear();
   pending_writebacks_.clear();
   if (op_start_) device_->event_destroy(op_start_);
+  if (op_start2_) device_->event_destroy(op_start2_);
   if (carry_fence_) device_->event_destroy(carry_fence_);
-  op_start_ = carry_fence_ = nullptr;
+  op_start_ = op_start2_ = carry_fence_ = nullptr;
   for (Stream s : {h2d_, compute_, compute2_, d2h_})
     if (s) device_->stream_destroy(s);
   compute_ = compute2_ = h2d_ = d2h_ = nullptr;
@@ -814,13 +816,11 @@ Error Runtime::acquire_pieces(const PanelKey& key, uint64_t packed_pitch,
 // `stream` may overwrite the frame.
 Error Runtime::wait_ready(Frame& f, Stream stream) {
   if (f.writeback_done) {
-    if (int rc = device_->stream_wait_event(stream, f.writeback_done))
-      return device_failure(rc, "cache", "stream_wait");
+    if (Error e = stream_wait(stream, f.writeback_done)) return e;
     f.writeback_done = nullptr;
   }
   if (!f.ready_pending) return {};
-  if (int rc = device_->stream_wait_event(stream, f.ready))
-    return device_failure(rc, "cache", "stream_wait");
+  if (Error e = stream_wait(stream, f.ready)) return e;
   if (f.state == EntryState::h2d_in_flight) move(f, EntryState::resident_clean);
   return {};
 }
@@ -1229,7 +1229,8 @@ Error Runtime::run_transaction(const std::vector<AccessSpan>& ranges, uint64_t w
     resolved.push_back(ResolvedSpan{s, find(s.allocation_id)->va + s.offset});
   TraceInterval iv;
   iv.kind = 't';
-  if (Error e = record_kernel(iv.start, iv.stop)) return e;
+  if (Error e = take_event(iv.start)) return e;
+  if (Error e = take_event(iv.stop)) return e;
   if (int rc = device_->event_record(iv.start, compute_)) return device_failure(rc, "transaction", "record");
   bool skipped = false;
   Error body_error;
@@ -1404,15 +1405,40 @@ Error Runtime::begin_operation() {
   trace_timed_ = 0;
   op_start_seen_ = false;
   guard_tripped_ = false;
+  // Every stream is idle here (the previous operation drained them; carried
+  // fills aside), so nothing orders the copy streams after op_start_: a wait
+  // on a just-recorded event costs ~16 us of host time. Intervals are timed
+  // from op_start_ (a carried fill or a copy issued before op_start_ was
+  // processed times as negative). Each compute lane records its own start.
   if (int rc = device_->event_record(op_start_, compute_)) return device_failure(rc, "operation", "record");
-  for (Stream s : {h2d_, d2h_, compute2_})
-    if (int rc = device_->stream_wait_event(s, op_start_)) return device_failure(rc, "operation", "wait");
+  if (int rc = device_->event_record(op_start2_, compute2_)) return device_failure(rc, "operation", "record");
+  lane_last_[0] = op_start_;
+  lane_last_[1] = op_start2_;
+  lane_waited_[0] = lane_waited_[1] = false;
   return {};
 }
 
-Error Runtime::record_kernel(Event& start, Event& stop) {
-  if (Error e = take_event(start)) return e;
-  return take_event(stop);
+Error Runtime::record_kernel(TraceInterval& iv, int lane) {
+  if (lane < 0 || lane >= kLanes)
+    return make_error(XVRAM_STATUS_INTERNAL, "gemm", "launch", "no such compute lane");
+  iv.start = iv.start_ref = nullptr;
+  if (lane_waited_[lane]) {
+    if (Error e = take_event(iv.start)) return e;
+  } else {
+    iv.start_ref = lane_last_[lane];
+  }
+  if (Error e = take_event(iv.stop)) return e;
+  lane_last_[lane] = iv.stop;
+  lane_waited_[lane] = false;
+  return {};
+}
+
+Error Runtime::stream_wait(Stream stream, Event event) {
+  if (int rc = device_->stream_wait_event(stream, event))
+    return device_failure(rc, "cache", "stream_wait");
+  for (int lane = 0; lane < kLanes; ++lane)
+    if (stream == compute_stream(lane)) lane_waited_[lane] = true;
+  return {};
 }
 
 void Runtime::time_intervals(bool all) {
@@ -1420,14 +1446,18 @@ void Runtime::time_intervals(bool all) {
   // Fills carried into the next operation are timed by that one.
   const size_t own = carry_active_ ? carry_trace_mark_ : trace_.size();
   if (!op_start_seen_) {
-    if (!all && device_->event_query(op_start_) != 0) return;
+    if (!all && (device_->event_query(op_start_) != 0 || device_->event_query(op_start2_) != 0))
+      return;
     op_start_seen_ = true;
   }
   while (trace_timed_ < own) {
     TraceInterval& iv = trace_[trace_timed_];
     if (!all && device_->event_query(iv.stop) != 0) return;
+    // A kernel without a start event started when its start_ref completed
+    // (an earlier event on the same stream, so it has completed too).
+    const Event start = iv.start ? iv.start : iv.start_ref;
     float s = 0.f, e = 0.f;
-    if (device_->event_elapsed_ms(&s, op_start_, iv.start) != 0) s = 0.f;
+    if (start != op_start_ && device_->event_elapsed_ms(&s, op_start_, start) != 0) s = 0.f;
     if (device_->event_elapsed_ms(&e, op_start_, iv.stop) != 0) e = s;
     iv.start_ms = s;
     iv.stop_ms = e;
@@ -1545,12 +1575,9 @@ Error Runtime::finish_operation(uint64_t operation_id) {
     if (i < own_events || !carrying) event_pool_.push_back(events_in_use_[i]);
   }
   events_in_use_.clear();
-  uint64_t free_bytes = 0, total_bytes = 0;
-  if (!first && device_->mem_info(&free_bytes, &total_bytes) == 0) {
-    ++t_.budget_sample_count;
-    t_.cuda_free_bytes_minimum = std::min(t_.cuda_free_bytes_minimum, free_bytes);
-    t_.cuda_free_bytes_end = free_bytes;
-  }
+  // Free device memory is sampled at setup and by refresh_budget (at most once
+  // per budget_poll_ms; reference src/residency/runtime.cpp:3213-3232), not
+  // per operation.
   if (!first && guard_tripped_) {
     launches_blocked_ = true;
     ++t_.watchdog_rejections;
