@@ -783,7 +783,7 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
       if (kp.slice >= 0) {
         for (const std::vector<Event>* ready : {&acq.a_ready[t], &acq.b_ready[t]}) {
           if (ready->empty()) continue;
-          if (Error e = rt.stream_wait(cs, (*ready)[kp.slice])) {
+          if (Error e = rt.stream_wait(cs, (*ready)[kp.slice], (*ready)[kp.slice])) {
             result = e;
             break;
           }
@@ -823,8 +823,8 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
         }
         k.relu = p.relu;
       }
-      // The launch's timing events are recorded by its dispatch (a start
-      // event only after a wait on the lane: Runtime::record_kernel); the last
+      // The launch's stop event is recorded by its dispatch (its start is
+      // derived from the events it follows: Runtime::record_kernel); the last
       // dispatch's stop event is also the retire event of the launch's frames
       // (each marker packet between kernels would otherwise cost the compute
       // stream a few microseconds).

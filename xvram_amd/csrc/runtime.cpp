@@ -710,6 +710,7 @@ Error Runtime::fill_entry(Frame& f, const PanelKey& key, uint64_t packed_pitch, 
     trace_.push_back(iv);
     // The piece's stop event (an operation-owned event) marks it landed.
     if (piece_ready) piece_ready->push_back(iv.stop);
+    f.ready_stamp = iv.stop;
   }
   if (int rc = device_->event_record(f.ready, h2d_)) return device_failure(rc, "cache", "record");
   f.ready_pending = true;
@@ -816,11 +817,14 @@ Error Runtime::acquire_pieces(const PanelKey& key, uint64_t packed_pitch,
 // `stream` may overwrite the frame.
 Error Runtime::wait_ready(Frame& f, Stream stream) {
   if (f.writeback_done) {
-    if (Error e = stream_wait(stream, f.writeback_done)) return e;
+    // An operation-owned event (the write-back's stop event).
+    if (Error e = stream_wait(stream, f.writeback_done, f.writeback_done)) return e;
     f.writeback_done = nullptr;
   }
   if (!f.ready_pending) return {};
-  if (Error e = stream_wait(stream, f.ready)) return e;
+  // A pending fill was issued in this operation or carried into it, so its
+  // stamp is one of this operation's events.
+  if (Error e = stream_wait(stream, f.ready, f.ready_stamp)) return e;
   if (f.state == EntryState::h2d_in_flight) move(f, EntryState::resident_clean);
   return {};
 }
@@ -1415,6 +1419,8 @@ Error Runtime::begin_operation() {
   lane_last_[0] = op_start_;
   lane_last_[1] = op_start2_;
   lane_waited_[0] = lane_waited_[1] = false;
+  lane_deps_[0].clear();
+  lane_deps_[1].clear();
   return {};
 }
 
@@ -1422,22 +1428,28 @@ Error Runtime::record_kernel(TraceInterval& iv, int lane) {
   if (lane < 0 || lane >= kLanes)
     return make_error(XVRAM_STATUS_INTERNAL, "gemm", "launch", "no such compute lane");
   iv.start = iv.start_ref = nullptr;
+  iv.deps.clear();
   if (lane_waited_[lane]) {
     if (Error e = take_event(iv.start)) return e;
   } else {
     iv.start_ref = lane_last_[lane];
+    iv.deps.swap(lane_deps_[lane]);
   }
   if (Error e = take_event(iv.stop)) return e;
   lane_last_[lane] = iv.stop;
   lane_waited_[lane] = false;
+  lane_deps_[lane].clear();
   return {};
 }
 
-Error Runtime::stream_wait(Stream stream, Event event) {
+Error Runtime::stream_wait(Stream stream, Event event, Event stamp) {
   if (int rc = device_->stream_wait_event(stream, event))
     return device_failure(rc, "cache", "stream_wait");
-  for (int lane = 0; lane < kLanes; ++lane)
-    if (stream == compute_stream(lane)) lane_waited_[lane] = true;
+  for (int lane = 0; lane < kLanes; ++lane) {
+    if (stream != compute_stream(lane)) continue;
+    if (stamp) lane_deps_[lane].push_back(stamp);
+    else lane_waited_[lane] = true;
+  }
   return {};
 }
 
@@ -1453,11 +1465,16 @@ void Runtime::time_intervals(bool all) {
   while (trace_timed_ < own) {
     TraceInterval& iv = trace_[trace_timed_];
     if (!all && device_->event_query(iv.stop) != 0) return;
-    // A kernel without a start event started when its start_ref completed
-    // (an earlier event on the same stream, so it has completed too).
+    // A kernel without a start event started when the last of its start_ref
+    // (an earlier event on the same stream) and its deps (events its stream
+    // waited for) completed; all of them completed before its stop did.
     const Event start = iv.start ? iv.start : iv.start_ref;
     float s = 0.f, e = 0.f;
     if (start != op_start_ && device_->event_elapsed_ms(&s, op_start_, start) != 0) s = 0.f;
+    for (Event d : iv.deps) {
+      float t = 0.f;
+      if (device_->event_elapsed_ms(&t, op_start_, d) == 0) s = std::max(s, t);
+    }
     if (device_->event_elapsed_ms(&e, op_start_, iv.stop) != 0) e = s;
     iv.start_ms = s;
     iv.stop_ms = e;

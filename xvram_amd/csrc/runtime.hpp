@@ -126,6 +126,9 @@ struct Frame {
   bool dirty = false;
   uint64_t last_use = 0;
   Event ready = nullptr; // recorded on the H2D stream after a fill
+  // The fill's last copy's stop event (operation-owned, recorded just before
+  // `ready` on the same stream): when the fill landed, for timing.
+  Event ready_stamp = nullptr;
   bool ready_pending = false;
   Event retire = nullptr; // this frame's own event for its last consumer
   // The event that marks the last consumer: `retire`, or the stop event of the
@@ -164,10 +167,12 @@ struct Frame {
 struct TraceInterval {
   Event start = nullptr;
   Event stop = nullptr;
-  // A kernel dispatched with no start event (nothing was waited for since the
-  // previous work on its stream) starts when `start_ref` completed: the
-  // previous kernel's stop event on that stream, or the operation's start.
+  // A kernel dispatched with no start event starts when the last of
+  // `start_ref` (the previous kernel's stop event on its stream, or the
+  // stream's operation start) and the events its stream waited for since
+  // (`deps`, operation-owned) completed.
   Event start_ref = nullptr;
+  std::vector<Event> deps;
   uint64_t bytes = 0;
   char kind = 'k'; // 'k' kernel, 'h' H2D, 'd' D2H, 't' transaction callback work
   // Start and stop in ms from the operation's start event, once both events
@@ -329,14 +334,16 @@ public:
   Error carry_fill(const PanelKey& key, uint64_t packed_pitch, bool& issued);
 
   // Kernel bookkeeping used by the executor. record_kernel takes the stop
-  // event of a kernel about to be dispatched on compute lane `lane`, and a
-  // start event only when the lane's stream waited for something since its
-  // previous kernel (a start event in the dispatch costs ~16 us of host time
-  // and ~5 us of device time per kernel); otherwise the kernel starts when
-  // the previous kernel on the lane (or the operation's start) completed.
+  // event of a kernel about to be dispatched on compute lane `lane`; its
+  // start is derived from the events it follows (TraceInterval::start_ref,
+  // deps), and a start event is taken only when the lane waited for an event
+  // with no operation-owned stamp (a start event in the dispatch costs ~16 us
+  // of host time and ~5 us of device time per kernel).
   Error record_kernel(TraceInterval& iv, int lane);
-  // stream_wait_event that also marks a compute lane as having waited.
-  Error stream_wait(Stream stream, Event event);
+  // stream_wait_event(stream, event). For a compute lane, `stamp` is an
+  // operation-owned event that completes with `event` (nullptr: none known,
+  // the lane's next kernel takes a start event).
+  Error stream_wait(Stream stream, Event event, Event stamp);
   Error take_event(Event& out);
   void note_kernel_launched(uint64_t tiles = 1) { kernels_in_operation_ += tiles; }
 
@@ -443,7 +450,8 @@ private:
   size_t trace_timed_ = 0;     // trace_[0 .. trace_timed_) are timed
   bool op_start_seen_ = false; // op_start_ and op_start2_ have completed (intervals can be timed)
   Event lane_last_[2] = {nullptr, nullptr}; // last kernel stop per lane (its start event at first)
-  bool lane_waited_[2] = {false, false};    // a wait was enqueued since lane_last_
+  bool lane_waited_[2] = {false, false};    // a wait without a stamp since lane_last_
+  std::vector<Event> lane_deps_[2];         // stamps of the waits since lane_last_
   bool guard_tripped_ = false; // a kernel or callback of the operation exceeded the guard
   std::vector<Event> event_pool_;
   std::vector<Event> events_in_use_;
