@@ -24,7 +24,9 @@
 // start_event / stop_event (hipEvent_t, optional) are recorded by the dispatch
 // itself (hipExtLaunchKernelGGL): no separate marker packets run between
 // kernels, and stop_event completes when the kernel does, so it can serve as
-// the retire event of every panel the launch reads or writes.
+// the retire event of every panel the launch reads or writes. A start event
+// costs the dispatch ~16 us of host time and ~5 us of device time; the
+// executor passes none and derives starts from the events a launch follows.
 #pragma once
 
 #include <cstdint>
