@@ -7,7 +7,9 @@ out of core (small frames, so the planner tiles C and splits K and the panels
 stream through a few frames). A quarter of the cases are large enough that
 their launches run a 256 x 256 kernel; the rest run the 256 x 128 kernel,
 many with ragged edges in every dimension. Six more cases are N/T with m and n
-multiples of 256, so their large launches run the barrier-free N/T kernel. With beta = 0, C is filled with NaN
+multiples of 256, so their large launches run the barrier-free N/T kernel, and
+six are N/N, T/N or T/T with such m and n and K a multiple of 8 (the
+barrier-free kernel of those forms). With beta = 0, C is filled with NaN
 first (it must never be read).
 
 Every element is compared with the FP64 oracle (the reference's CPU GEMM,
@@ -74,7 +76,28 @@ def make_ring_cases(count=6, seed=2027):
     return cases
 
 
-CASES = make_cases() + make_ring_cases()
+def make_ring8_cases(count=6, seed=2028):
+    """N/N, T/N and T/T with m and n multiples of 256 from 4096 and K a multiple
+    of 8, every storage layout (a row-major C turns the product into its
+    transpose, so the canonical form of a case may be any of the four): the
+    4096 x 4096 (and resident) launches run a barrier-free kernel, mostly
+    sgemm_ring8_kernel."""
+    rng = np.random.default_rng(seed)
+    forms = [OPS[0], OPS[2], OPS[3]]
+    cases = []
+    for i in range(count):
+        resident = i % 2 == 0
+        cases.append(dict(
+            m=256 * int(rng.integers(16, 21)), n=256 * int(rng.integers(16, 21)),
+            k=8 * int(rng.integers(1, 150)), ops=forms[i % 3],
+            layouts=tuple(int(v) for v in rng.integers(0, 2, 3)),
+            ld_pad=tuple(int(v) for v in rng.integers(0, 8, 3)),
+            alpha=float(rng.choice([1.0, -0.75, 2.5])), beta=float(rng.choice([0.0, 1.0, 0.5])),
+            cache=(0, 0) if resident else (64, 12), seed=7000 + 3 * i))
+    return cases
+
+
+CASES = make_cases() + make_ring_cases() + make_ring8_cases()
 
 
 def case_id(c):
