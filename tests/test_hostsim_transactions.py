@@ -331,6 +331,37 @@ def test_duration_guard_blocks_later_launches(sim):
         assert e2.value.status == abi.INVALID_ARGUMENT
 
 
+def test_duration_guard_on_gemm_kernels(sim, oracle_mod):
+    """The guard also covers tile kernels (dispatched without a start event:
+    a kernel's start is derived from the events its lane follows). On the
+    simulated device a 128 x 128 x 1024 launch computes on the host for far
+    longer than 1 ms: the operation completes, then fails with TIMEOUT, and
+    later launches are refused."""
+    m, n, k = 128, 128, 1024
+    a_op = uniform(oracle_mod, m, k, 61)
+    b_op = uniform(oracle_mod, k, n, 62)
+    with xv.Session(sim, chunk_size_bytes=1 << 20, workspace_cap_bytes=0,
+                    device_headroom_bytes=0, max_transaction_ms=1) as s:
+        A, B, C = s.allocation(m * k * 4), s.allocation(k * n * 4), s.allocation(m * n * 4)
+        A.write(np.asfortranarray(a_op).reshape(-1, order="F"))
+        B.write(np.asfortranarray(b_op).reshape(-1, order="F"))
+        plan = xv.GemmPlan(s, xv.matrix(A, m, k, m), xv.matrix(B, k, n, k), xv.matrix(C, m, n, m))
+        assert plan.info().tile_count == 1
+        with pytest.raises(xv.XvramError) as e:
+            plan.execute()
+        assert e.value.status == abi.TIMEOUT
+        t = s.telemetry()
+        assert t.watchdog_rejections == 1 and t.last_transaction_ms >= 1
+        out = C.read(dtype=np.float32).reshape(n, m).T
+        ref = a_op.astype(np.float64) @ b_op.astype(np.float64)
+        bound = 4 * k * 2.0 ** -24 * (np.abs(a_op).astype(np.float64) @ np.abs(b_op).astype(np.float64))
+        assert np.all(np.abs(out - ref) <= bound)  # the work completed before the guard tripped
+        with pytest.raises(xv.XvramError) as e2:
+            plan.execute()
+        assert e2.value.status == abi.INVALID_ARGUMENT
+        plan.release()
+
+
 @pytest.mark.parametrize("max_ms,split", [(0, False), (1, True)])
 def test_planner_keeps_launches_under_the_guard(sim, max_ms, split):
     """Plans are sized against max_transaction_ms (at a deliberately low assumed
