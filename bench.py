@@ -67,13 +67,14 @@ WORKLOADS = {
     "c4_32768_nt_2g": (32768, 32768, 32768, OP_N, OP_T, 2 * GiB, 64 * MiB,
                        "FP32 SGEMM N/T 32768^3, 3 x 4 GiB operands, 2 GiB VRAM budget"),
 }
-# Config 3, the resident sweep: N/N and N/T at 4096^3, 8192^3, 16384^3, one launch
-# each (frames large enough for whole operands, budget unrestricted).
+# Config 3, the resident sweep: N/N and N/T at 4096^3, 8192^3, 16384^3 (and the
+# T/N and T/T forms beside them), one launch each (frames large enough for whole
+# operands, budget unrestricted).
 for _s, _frame in ((4096, 64 * MiB), (8192, 256 * MiB), (16384, 1024 * MiB)):
-    for _ob, _name in ((OP_N, "nn"), (OP_T, "nt")):
-        WORKLOADS[f"resident_{_s}_{_name}"] = (
-            _s, _s, _s, OP_N, _ob, 0, _frame,
-            f"FP32 SGEMM N/{'NT'[_ob]} {_s}^3, fully resident (one launch)")
+    for _oa, _ob in ((OP_N, OP_N), (OP_N, OP_T), (OP_T, OP_N), (OP_T, OP_T)):
+        WORKLOADS[f"resident_{_s}_{'nt'[_oa]}{'nt'[_ob]}"] = (
+            _s, _s, _s, _oa, _ob, 0, _frame,
+            f"FP32 SGEMM {'NT'[_oa]}/{'NT'[_ob]} {_s}^3, fully resident (one launch)")
 DEFAULT = "ns65536_nt_16g"
 # Config 5: 8 x [Y = ReLU(X W^T + b)], X 256 x 16384 ~ N(0,1), W 16384 x 16384 and
 # b ~ N(0, 1/16384), 2 GiB budget of 64 MiB frames; one step = one 8-layer forward.

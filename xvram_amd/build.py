@@ -30,7 +30,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
-HOST_SOURCES = ["api.cpp", "session.cpp", "runtime.cpp", "gemm.cpp", "policy.cpp"]
+HOST_SOURCES = ["api.cpp", "errors.cpp", "session.cpp", "runtime.cpp", "gemm.cpp", "policy.cpp"]
 HIP_SOURCES = ["sgemm_mfma.hip", "sgemm_wide.hip"]
 COMMON_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-fvisibility=hidden", "-DXVRAM_BUILDING_LIBRARY",
                 f"-I{INCLUDE}", f"-I{CSRC}", "-Wall", "-Wextra", "-Wno-unused-parameter"]

@@ -1,247 +1,247 @@
-// api.cpp — the C-ABI boundary: xvram_get_api and the v1 function table.
+// api.cpp — the C-ABI boundary: xvram_get_api and the v1, v2 and extension
+// function tables.
 //
-// Replaces src/sdk/api.cpp of the reference. Kept identical because callers
-// depend on it: argument validation order and the status each failure maps
-// to (api.cpp:124-344), struct_size preservation on outputs (:459-475), the
-// exception firewall (:109-122: bad_alloc -> HOST_OUT_OF_MEMORY, anything
-// else -> INTERNAL), per-session last-error recording (:18-47), handle
-// ownership (allocation handles may outlive their session, :644-661) and the
-// synchronous wrappers = submit + wait + release (:782-806, :876-900).
+// Stands in for the reference's SDK entry layer (src/sdk/api.cpp). What a
+// caller can observe is interface and is kept: which argument mistakes are
+// reported, in which order and with which status (api.cpp:124-344); outputs
+// that keep the caller's struct_size (:459-475); exceptions that never cross
+// the boundary (bad_alloc -> HOST_OUT_OF_MEMORY, anything else -> INTERNAL,
+// :109-122); a per-session last-error record; allocation handles that may
+// outlive their session (:644-661); synchronous forms = submit + wait +
+// release (:782-806, :876-900).
+//
+// The structure is this build's own:
+//  * a handle is the Session itself plus the object it names (`Bound`); the
+//    Session keeps the last-error record and the closed flag;
+//  * each descriptor is checked against an ordered table of rules, the first
+//    broken rule deciding the error;
+//  * every entry point runs its body through `guarded`, which turns
+//    exceptions into statuses and records failures on the session.
 #include <xvram/xvram.h>
 
-#include <atomic>
+#include <algorithm>
+#include <cstdio>
 #include <cstring>
 #include <memory>
-#include <mutex>
 #include <new>
+#include <utility>
 #include <vector>
 
 #include "common.hpp"
 #include "session.hpp"
 
-namespace xvram {
-namespace {
+namespace xvram::abi {
 
-struct SessionState {
-  SessionState(std::shared_ptr<Session> s, uint64_t chunk, uint64_t workspace)
-      : backend(std::move(s)), chunk_bytes(chunk), workspace_cap_bytes(workspace) {}
-  void record(const Error& e) noexcept {
-    if (!e) return;
-    try {
-      std::lock_guard<std::mutex> lock(mutex);
-      last_error = e;
-    } catch (...) {
-    }
-  }
-  Error error() const {
-    std::lock_guard<std::mutex> lock(mutex);
-    return last_error;
-  }
-  std::shared_ptr<Session> backend;
-  uint64_t chunk_bytes = 0;
-  uint64_t workspace_cap_bytes = 0;
-  mutable std::mutex mutex;
-  Error last_error;
-  std::atomic<bool> closed{false};
+// A handle: the session that issued it (kept alive by the handle) and the
+// object it names.
+template <class Object>
+struct Bound {
+  std::shared_ptr<Session> session;
+  std::shared_ptr<Object> object;
 };
 
-} // namespace
-} // namespace xvram
+} // namespace xvram::abi
 
 struct xvram_session_t {
-  std::shared_ptr<xvram::SessionState> state;
+  std::shared_ptr<xvram::Session> session;
 };
-struct xvram_allocation_t {
-  std::shared_ptr<xvram::SessionState> owner;
-  std::shared_ptr<xvram::AllocationRecord> backend;
-};
-struct xvram_operation_t {
-  std::shared_ptr<xvram::SessionState> owner;
-  std::shared_ptr<xvram::Operation> backend;
-};
-struct xvram_gemm_plan_t {
-  std::shared_ptr<xvram::SessionState> owner;
-  std::shared_ptr<xvram::GemmPlanRecord> backend;
-};
+struct xvram_allocation_t : xvram::abi::Bound<xvram::AllocationRecord> {};
+struct xvram_operation_t : xvram::abi::Bound<xvram::Operation> {};
+struct xvram_gemm_plan_t : xvram::abi::Bound<xvram::GemmPlanRecord> {};
 
-namespace xvram {
-
-// ---- status helpers ----------------------------------------------------------
-
-const char* status_name(xvram_status s) noexcept {
-  switch (s) {
-  case XVRAM_STATUS_SUCCESS: return "success";
-  case XVRAM_STATUS_INVALID_ARGUMENT: return "invalid_argument";
-  case XVRAM_STATUS_INCOMPATIBLE_ABI: return "incompatible_abi";
-  case XVRAM_STATUS_UNSUPPORTED: return "unsupported";
-  case XVRAM_STATUS_UNAVAILABLE: return "unavailable";
-  case XVRAM_STATUS_HOST_OUT_OF_MEMORY: return "host_out_of_memory";
-  case XVRAM_STATUS_DEVICE_OUT_OF_MEMORY: return "device_out_of_memory";
-  case XVRAM_STATUS_BUDGET_PRESSURE: return "budget_pressure";
-  case XVRAM_STATUS_BUSY: return "busy";
-  case XVRAM_STATUS_NOT_READY: return "not_ready";
-  case XVRAM_STATUS_TIMEOUT: return "timeout";
-  case XVRAM_STATUS_CORRUPTION: return "corruption";
-  case XVRAM_STATUS_CALLBACK_FAILED: return "callback_failed";
-  case XVRAM_STATUS_CUDA_ERROR: return "cuda_error";
-  case XVRAM_STATUS_CUBLAS_ERROR: return "cublas_error";
-  case XVRAM_STATUS_POISONED: return "poisoned";
-  case XVRAM_STATUS_CLEANUP_FAILED: return "cleanup_failed";
-  case XVRAM_STATUS_CLOSED: return "closed";
-  case XVRAM_STATUS_CANCELLED: return "cancelled";
-  case XVRAM_STATUS_INTERNAL: return "internal";
-  default: return "unknown";
-  }
-}
-
+namespace xvram::abi {
 namespace {
 
-template <size_t N>
-void copy_text(char (&dst)[N], const std::string& src) noexcept {
-  const size_t n = std::min(src.size(), N - 1);
-  std::memset(dst, 0, N);
-  if (n) std::memcpy(dst, src.data(), n);
+constexpr const char* kStage = "abi";
+
+Error bad_argument(const char* entry, const char* what) {
+  return make_error(XVRAM_STATUS_INVALID_ARGUMENT, kStage, entry, what);
 }
 
-} // namespace
-
-void write_error_info(const Error& e, xvram_error_info_v1& out) noexcept {
-  const uint32_t caller_size = out.struct_size;
-  out = XVRAM_ERROR_INFO_V1_INIT;
-  out.struct_size = caller_size;
-  out.status = e.status;
-  out.native_domain = e.native_domain;
-  out.native_code = e.native_code;
-  copy_text(out.stage, e.stage);
-  copy_text(out.operation, e.operation);
-  copy_text(out.native_name, e.native_name);
-  copy_text(out.message, e.message);
+Error too_old(const char* entry, const char* what) {
+  return make_error(XVRAM_STATUS_INCOMPATIBLE_ABI, kStage, entry, what);
 }
 
-Error exception_error(std::string_view operation) noexcept {
-  Error e;
+Error no_host_memory(const char* entry) {
+  return make_error(XVRAM_STATUS_HOST_OUT_OF_MEMORY, kStage, entry,
+                    "no host memory left for the handle");
+}
+
+// ---- the firewall ----------------------------------------------------------
+
+// Runs an entry point's body. An escaping exception becomes a status
+// (exception_error), and a failure is recorded as the session's last error
+// when the call names a session.
+template <class Body>
+xvram_status guarded(Session* session, const char* entry, Body&& body) noexcept {
+  Error outcome;
   try {
-    throw;
-  } catch (const std::bad_alloc&) {
-    e.status = XVRAM_STATUS_HOST_OUT_OF_MEMORY;
-    try {
-      e.message = "host allocation failed";
-    } catch (...) {
-    }
-  } catch (const std::exception& ex) {
-    e.status = XVRAM_STATUS_INTERNAL;
-    try {
-      e.message = ex.what();
-    } catch (...) {
-    }
+    outcome = body();
   } catch (...) {
-    e.status = XVRAM_STATUS_INTERNAL;
-    try {
-      e.message = "unknown C++ exception at ABI boundary";
-    } catch (...) {
-    }
+    outcome = exception_error(entry);
   }
-  try {
-    e.stage = "sdk";
-    e.operation.assign(operation);
-  } catch (...) {
-  }
-  return e;
+  if (outcome && session != nullptr) session->note_failure(outcome);
+  return outcome.status;
 }
 
-namespace {
-
-xvram_status publish(const std::shared_ptr<SessionState>& state, const Error& e) noexcept {
-  if (e && state) state->record(e);
-  return e.status;
+// Writes a whole output record but keeps the struct_size the caller put there
+// (a caller with a newer, larger struct keeps its own size).
+template <class T>
+void deliver(T* out, T value) noexcept {
+  value.struct_size = out->struct_size;
+  *out = value;
 }
 
-template <typename F>
-xvram_status boundary(const std::shared_ptr<SessionState>& state, std::string_view operation,
-                      F&& f) noexcept {
-  try {
-    return publish(state, f());
-  } catch (const std::bad_alloc&) {
-    return publish(state, make_error(XVRAM_STATUS_HOST_OUT_OF_MEMORY, "sdk", operation,
-                                     "host allocation failed"));
-  } catch (...) {
-    return publish(state, exception_error(operation));
-  }
+// ---- descriptor rules ------------------------------------------------------
+
+template <class T>
+bool versioned(const T* p) noexcept {
+  return p != nullptr && p->struct_size >= sizeof(T);
 }
 
-template <typename S>
-bool has_v1_size(const S* s) noexcept {
-  return s != nullptr && s->struct_size >= sizeof(S);
+template <class W, size_t N>
+bool zeroed(const W (&words)[N]) noexcept {
+  return std::all_of(words, words + N, [](W w) { return w == 0; });
 }
 
-bool all_zero(const uint64_t* v, size_t n) {
-  for (size_t i = 0; i < n; ++i)
-    if (v[i] != 0) return false;
-  return true;
-}
+// One rule of a descriptor check; a value that breaks it is INVALID_ARGUMENT
+// with `complaint` as the message.
+template <class T>
+struct Rule {
+  bool (*holds)(const T&);
+  const char* complaint;
+};
 
-bool valid_access_mode(xvram_access_mode m) {
-  return m == XVRAM_ACCESS_READ || m == XVRAM_ACCESS_READ_WRITE || m == XVRAM_ACCESS_WRITE_ONLY;
-}
-
-// src/sdk/api.cpp:173-207.
-Error validate_session_config(const xvram_session_config_v1* c) {
-  if (!has_v1_size(c)) return incompatible("session_create", "session config is null or smaller than v1");
-  if (c->flags != 0 || c->reserved0 != 0 || !all_zero(c->reserved, 4))
-    return invalid("session_create", "unknown flags or non-zero reserved field");
-  if (c->context_mode != XVRAM_CONTEXT_ISOLATED && c->context_mode != XVRAM_CONTEXT_ATTACH_CURRENT)
-    return invalid("session_create", "invalid context mode");
-  if (c->cache_policy != XVRAM_CACHE_POLICY_CLOCK && c->cache_policy != XVRAM_CACHE_POLICY_LRU)
-    return invalid("session_create", "invalid cache policy");
-  if (c->device_ordinal < 0) return invalid("session_create", "device ordinal must be non-negative");
-  if (c->chunk_size_bytes == 0) return invalid("session_create", "chunk size must be non-zero");
-  if (c->staging_slots < 2 || c->staging_slots > 8)
-    return invalid("session_create", "staging slot count must be in [2, 8]");
-  if (c->prefetch_distance > 8) return invalid("session_create", "prefetch distance must be in [0, 8]");
-  const uint64_t int64_max = static_cast<uint64_t>(INT64_MAX);
-  if (c->budget_poll_ms == 0 || c->budget_poll_ms > int64_max || c->max_transaction_ms > int64_max)
-    return invalid("session_create", "budget and transaction durations are out of range");
+template <class T, size_t N>
+Error first_broken(const Rule<T> (&rules)[N], const T& value, const char* entry) {
+  for (const Rule<T>& rule : rules)
+    if (!rule.holds(value)) return bad_argument(entry, rule.complaint);
   return {};
 }
 
-// src/sdk/api.cpp:236-276.
-Error collect_accesses(const std::shared_ptr<SessionState>& owner, const xvram_access_range_v1* ranges,
-                       uint64_t count, const char* operation, std::vector<Session::Access>& out) {
-  if (count == 0) return invalid(operation, "at least one access range is required");
-  if (ranges == nullptr) return invalid(operation, "range array is null");
-  if (count > out.max_size()) return invalid(operation, "range count is too large");
+constexpr uint64_t kLongestMs = static_cast<uint64_t>(INT64_MAX);
+
+using SessionConfig = xvram_session_config_v1;
+const Rule<SessionConfig> kSessionConfigRules[] = {
+    {[](const SessionConfig& c) { return c.flags == 0 && c.reserved0 == 0 && zeroed(c.reserved); },
+     "flags, reserved0 and reserved[] must be zero"},
+    {[](const SessionConfig& c) { return c.context_mode <= XVRAM_CONTEXT_ATTACH_CURRENT; },
+     "context_mode is neither ISOLATED nor ATTACH_CURRENT"},
+    {[](const SessionConfig& c) { return c.cache_policy <= XVRAM_CACHE_POLICY_LRU; },
+     "cache_policy is neither CLOCK nor LRU"},
+    {[](const SessionConfig& c) { return c.device_ordinal >= 0; }, "device_ordinal is negative"},
+    {[](const SessionConfig& c) { return c.chunk_size_bytes != 0; }, "chunk_size_bytes is zero"},
+    {[](const SessionConfig& c) { return c.staging_slots >= 2 && c.staging_slots <= 8; },
+     "staging_slots lies outside 2..8"},
+    {[](const SessionConfig& c) { return c.prefetch_distance <= 8; },
+     "prefetch_distance is larger than 8"},
+    {[](const SessionConfig& c) {
+       return c.budget_poll_ms != 0 && c.budget_poll_ms <= kLongestMs &&
+              c.max_transaction_ms <= kLongestMs;
+     },
+     "budget_poll_ms must lie in 1..INT64_MAX and max_transaction_ms at most INT64_MAX"},
+};
+
+Error check_session_config(const SessionConfig* c, const char* entry) {
+  if (!versioned(c)) return too_old(entry, "the session config is missing or older than v1");
+  return first_broken(kSessionConfigRules, *c, entry);
+}
+
+using SessionConfig2 = xvram_session_config_v2;
+const Rule<SessionConfig2> kSessionConfig2Rules[] = {
+    {[](const SessionConfig2& c) { return c.compression_mode <= XVRAM_COMPRESSION_CAPACITY; },
+     "compression_mode is not a known mode"},
+    {[](const SessionConfig2& c) { return c.compression_codec <= XVRAM_COMPRESSION_CODEC_LZ4; },
+     "compression_codec is not a known codec"},
+    {[](const SessionConfig2& c) {
+       return c.compression_workspace_cap_bytes != 0 && c.codec_slots >= 2 && c.codec_slots <= 8 &&
+              c.codec_workers >= 1 && c.codec_workers <= 8;
+     },
+     "compression_workspace_cap_bytes must be non-zero, codec_slots 2..8, codec_workers 1..8"},
+};
+
+Error check_session_config_v2(const SessionConfig2* c) {
+  constexpr const char* entry = "session_create_v2";
+  if (!versioned(c)) return too_old(entry, "the v2 session config is missing or older than v2");
+  if (c->flags != 0 || !zeroed(c->reserved))
+    return bad_argument(entry, "flags and reserved[] of the v2 config must be zero");
+  if (Error e = check_session_config(&c->v1, "session_create")) return e;
+  return first_broken(kSessionConfig2Rules, *c, entry);
+}
+
+using AllocationDesc = xvram_allocation_desc_v1;
+const Rule<AllocationDesc> kAllocationRules[] = {
+    {[](const AllocationDesc& d) { return d.size_bytes != 0; }, "size_bytes is zero"},
+    {[](const AllocationDesc& d) {
+       return (d.flags & ~uint32_t{XVRAM_ALLOCATION_FLAG_ZERO_INITIALIZE}) == 0 &&
+              d.reserved0 == 0 && zeroed(d.reserved);
+     },
+     "unknown allocation flags, or reserved fields not zero"},
+    {[](const AllocationDesc& d) { return d.priority <= XVRAM_ALLOCATION_STREAMING; },
+     "priority is not NORMAL, HOT or STREAMING"},
+    {[](const AllocationDesc& d) { return (d.alignment_bytes & (d.alignment_bytes - 1)) == 0; },
+     "alignment_bytes is neither zero nor a power of two"},
+};
+
+using Matrix = xvram_matrix_v1;
+const Rule<Matrix> kMatrixRules[] = {
+    {[](const Matrix& m) {
+       return m.data_type <= XVRAM_DATA_FP64 && m.layout <= XVRAM_MATRIX_COLUMN_MAJOR &&
+              m.reserved0 == 0 && zeroed(m.reserved);
+     },
+     "a matrix has an unknown data type or layout, or non-zero reserved fields"},
+    {[](const Matrix& m) { return m.rows != 0 && m.columns != 0 && m.leading_dimension != 0; },
+     "a matrix has zero rows, columns or leading dimension"},
+};
+
+using GemmDesc = xvram_gemm_desc_v1;
+const Rule<GemmDesc> kGemmRules[] = {
+    {[](const GemmDesc& d) { return d.flags == 0 && d.reserved0 == 0 && zeroed(d.reserved); },
+     "GEMM flags, reserved0 and reserved[] must be zero"},
+    {[](const GemmDesc& d) {
+       return d.operation_a <= XVRAM_MATRIX_OP_T && d.operation_b <= XVRAM_MATRIX_OP_T &&
+              d.compute_mode <= XVRAM_COMPUTE_FP64;
+     },
+     "operation_a/operation_b is not N or T, or compute_mode is unknown"},
+};
+
+using AccessRange = xvram_access_range_v1;
+const Rule<AccessRange> kAccessRules[] = {
+    {[](const AccessRange& r) { return r.mode <= XVRAM_ACCESS_WRITE_ONLY && r.reserved0 == 0; },
+     "an access range has an unknown mode or a non-zero reserved0"},
+    {[](const AccessRange& r) { return r.length_bytes != 0; }, "an access range is empty"},
+    {[](const AccessRange& r) { return r.offset_bytes <= UINT64_MAX - r.length_bytes; },
+     "an access range ends beyond 2^64"},
+};
+
+// The access list of a prefetch or transaction: at least one range, every
+// range naming a live handle of `session`.
+Error gather_accesses(Session* session, const AccessRange* ranges, uint64_t count,
+                      const char* entry, std::vector<Session::Access>& out) {
+  if (count == 0) return bad_argument(entry, "range_count is zero");
+  if (ranges == nullptr) return bad_argument(entry, "ranges is NULL");
+  if (count > out.max_size()) return bad_argument(entry, "range_count is too large");
   out.reserve(static_cast<size_t>(count));
   for (uint64_t i = 0; i < count; ++i) {
-    const xvram_access_range_v1& r = ranges[i];
-    if (r.allocation == nullptr || !r.allocation->backend)
-      return invalid(operation, "access range contains a null allocation");
-    if (r.allocation->owner.get() != owner.get())
-      return invalid(operation, "all access ranges must belong to the session");
-    if (!valid_access_mode(r.mode) || r.reserved0 != 0)
-      return invalid(operation, "access range has an invalid mode or reserved field");
-    if (r.length_bytes == 0) return invalid(operation, "access range length must be non-zero");
-    if (r.offset_bytes > UINT64_MAX - r.length_bytes)
-      return invalid(operation, "access range overflows uint64");
-    out.push_back(Session::Access{r.allocation->backend, r.offset_bytes, r.length_bytes, r.mode});
+    const AccessRange& r = ranges[i];
+    if (r.allocation == nullptr || !r.allocation->object)
+      return bad_argument(entry, "an access range names no allocation");
+    if (r.allocation->session.get() != session)
+      return bad_argument(entry, "an access range names an allocation of another session");
+    if (Error e = first_broken(kAccessRules, r, entry)) return e;
+    out.push_back(Session::Access{r.allocation->object, r.offset_bytes, r.length_bytes, r.mode});
   }
   return {};
 }
 
-// src/sdk/api.cpp:278-302.
-Error convert_matrix(const std::shared_ptr<SessionState>& owner, const xvram_matrix_v1& in,
-                     MatrixSpec& out) {
-  if (in.struct_size < sizeof(xvram_matrix_v1))
-    return incompatible("gemm_plan_create", "matrix descriptor is smaller than v1");
-  if (in.allocation == nullptr || !in.allocation->backend)
-    return invalid("gemm_plan_create", "matrix allocation is null");
-  if (in.allocation->owner.get() != owner.get())
-    return invalid("gemm_plan_create", "matrix allocation belongs to another session");
-  const bool type_ok = in.data_type <= XVRAM_DATA_FP64;
-  const bool layout_ok = in.layout == XVRAM_MATRIX_ROW_MAJOR || in.layout == XVRAM_MATRIX_COLUMN_MAJOR;
-  if (!type_ok || !layout_ok || in.reserved0 != 0 || !all_zero(in.reserved, 2))
-    return invalid("gemm_plan_create", "matrix descriptor has invalid enum or reserved fields");
-  if (in.rows == 0 || in.columns == 0 || in.leading_dimension == 0)
-    return invalid("gemm_plan_create", "matrix dimensions and leading dimension must be non-zero");
+Error read_matrix(Session* session, const Matrix& in, MatrixSpec& out) {
+  constexpr const char* entry = "gemm_plan_create";
+  if (in.struct_size < sizeof(Matrix)) return too_old(entry, "a matrix descriptor is older than v1");
+  if (in.allocation == nullptr || !in.allocation->object)
+    return bad_argument(entry, "a matrix names no allocation");
+  if (in.allocation->session.get() != session)
+    return bad_argument(entry, "a matrix names an allocation of another session");
+  if (Error e = first_broken(kMatrixRules, in, entry)) return e;
   out.offset_bytes = in.offset_bytes;
   out.rows = in.rows;
   out.columns = in.columns;
@@ -251,16 +251,81 @@ Error convert_matrix(const std::shared_ptr<SessionState>& owner, const xvram_mat
   return {};
 }
 
-// ---- entries -----------------------------------------------------------------
+// The extension's epilogue descriptor (no reference counterpart).
+Error read_epilogue(Session* session, const xvram_amd_epilogue_v1& in, EpilogueSpec& out,
+                    std::shared_ptr<AllocationRecord>& bias) {
+  constexpr const char* entry = "gemm_plan_create";
+  if (in.struct_size < sizeof(xvram_amd_epilogue_v1))
+    return too_old(entry, "the epilogue descriptor is older than v1");
+  if (in.flags != 0 || !zeroed(in.reserved))
+    return bad_argument(entry, "epilogue flags and reserved[] must be zero");
+  if (in.bias != nullptr) {
+    if (!in.bias->object || in.bias->session.get() != session)
+      return bad_argument(entry, "the bias names an allocation of another session");
+    bias = in.bias->object;
+  }
+  if (in.bias_axis != XVRAM_AMD_BIAS_NONE && !bias)
+    return bad_argument(entry, "a bias axis is given without a bias allocation");
+  if (in.bias_axis == XVRAM_AMD_BIAS_NONE && bias)
+    return bad_argument(entry, "a bias allocation is given without a bias axis");
+  out.bias_offset_bytes = in.bias_offset_bytes;
+  out.bias_axis = in.bias_axis;
+  out.activation = in.activation;
+  return {};
+}
 
-const char* XVRAM_CALL status_name_entry(xvram_status s) noexcept { return status_name(s); }
+// ---- handles -----------------------------------------------------------------
 
-xvram_status XVRAM_CALL session_create_entry(const xvram_session_config_v1* config,
-                                             xvram_session* out) noexcept {
+bool live(const xvram_session_t* h) { return h != nullptr && h->session; }
+template <class Object>
+bool live(const Bound<Object>* h) {
+  return h != nullptr && h->session && h->object;
+}
+
+Error hand_out_operation(const std::shared_ptr<Session>& session, std::shared_ptr<Operation> op,
+                         xvram_operation* out, const char* entry) {
+  auto* handle = new (std::nothrow) xvram_operation_t{{session, op}};
+  if (handle == nullptr) {
+    (void)op->cancel(); // queued work nobody can wait for; a running one drains normally
+    return no_host_memory(entry);
+  }
+  *out = handle;
+  return {};
+}
+
+// The synchronous form of a submission: submit, wait, release the operation.
+// A wait that runs out returns TIMEOUT and leaves the operation running.
+template <class Submit>
+xvram_status run_to_end(Submit&& submit, uint64_t timeout_ms, const char* entry) {
+  xvram_operation handle = nullptr;
+  if (const xvram_status s = submit(&handle); s != XVRAM_STATUS_SUCCESS) return s;
+  std::unique_ptr<xvram_operation_t> owned(handle);
+  return guarded(owned->session.get(), entry, [&]() -> Error {
+    Operation& op = *owned->object;
+    if (!op.settled_within(timeout_ms))
+      return make_error(XVRAM_STATUS_TIMEOUT, "operation", "wait",
+                        "the operation did not finish within the timeout");
+    if (Error e = op.failure()) return e;
+    const xvram_operation_info_v1 info = op.snapshot();
+    if (info.result == XVRAM_STATUS_SUCCESS) return {};
+    return make_error(info.result, "operation", entry, "the operation failed");
+  });
+}
+
+// ---- entry points ------------------------------------------------------------
+
+namespace entry {
+
+const char* XVRAM_CALL status_name(xvram_status status) noexcept {
+  return xvram::status_name(status);
+}
+
+xvram_status XVRAM_CALL session_create(const xvram_session_config_v1* config,
+                                       xvram_session* out) noexcept {
   if (out == nullptr) return XVRAM_STATUS_INVALID_ARGUMENT;
   *out = nullptr;
-  return boundary({}, "session_create", [&]() -> Error {
-    if (Error e = validate_session_config(config)) return e;
+  return guarded(nullptr, "session_create", [&]() -> Error {
+    if (Error e = check_session_config(config, "session_create")) return e;
     xvram_session_config_v1 effective = *config;
     if (config->context_mode == XVRAM_CONTEXT_ATTACH_CURRENT) {
       // Reference src/sdk/runtime.cpp:1369-1383: the session runs on what is
@@ -278,47 +343,24 @@ xvram_status XVRAM_CALL session_create_entry(const xvram_session_config_v1* conf
       return e;
     }
     if (session->chunk_size_bytes() == 0)
-      return make_error(XVRAM_STATUS_INTERNAL, "sdk", "session_create",
-                        "backend reported a zero effective chunk size");
-    auto state = std::make_shared<SessionState>(session, session->chunk_size_bytes(),
-                                                config->workspace_cap_bytes);
-    auto* handle = new (std::nothrow) xvram_session_t{std::move(state)};
-    if (handle == nullptr)
-      return make_error(XVRAM_STATUS_HOST_OUT_OF_MEMORY, "sdk", "session_create",
-                        "failed to allocate session handle");
+      return make_error(XVRAM_STATUS_INTERNAL, kStage, "session_create",
+                        "the runtime set up a zero frame size");
+    auto* handle = new (std::nothrow) xvram_session_t{std::move(session)};
+    if (handle == nullptr) return no_host_memory("session_create");
     *out = handle;
     return {};
   });
 }
 
-// src/sdk/api.cpp:209-233.
-Error validate_session_config_v2(const xvram_session_config_v2* c) {
-  if (!has_v1_size(c))
-    return incompatible("session_create_v2", "session config is null or smaller than v2");
-  if (c->flags != 0 || !all_zero(c->reserved, 8))
-    return invalid("session_create_v2", "unknown flags or non-zero reserved field");
-  if (Error e = validate_session_config(&c->v1)) return e;
-  if (c->compression_mode != XVRAM_COMPRESSION_DISABLED &&
-      c->compression_mode != XVRAM_COMPRESSION_ADAPTIVE &&
-      c->compression_mode != XVRAM_COMPRESSION_CAPACITY)
-    return invalid("session_create_v2", "invalid compression mode");
-  if (c->compression_codec != XVRAM_COMPRESSION_CODEC_AUTO &&
-      c->compression_codec != XVRAM_COMPRESSION_CODEC_LZ4)
-    return invalid("session_create_v2", "invalid compression codec");
-  if (c->compression_workspace_cap_bytes == 0 || c->codec_slots < 2 || c->codec_slots > 8 ||
-      c->codec_workers == 0 || c->codec_workers > 8)
-    return invalid("session_create_v2", "invalid compression workspace, slots, or workers");
-  return {};
-}
-
-// src/sdk/api.cpp:399-447 and sdk/runtime.cpp:1393-1397: a DISABLED session is
-// exactly a v1 session; compression modes are not provided on this device path.
-xvram_status XVRAM_CALL session_create_v2_entry(const xvram_session_config_v2* config,
-                                                xvram_session* out) noexcept {
+// A v2 session with compression DISABLED is exactly a v1 session (reference
+// src/sdk/runtime.cpp:1393-1397); the host-compression modes are not
+// provided on this device path.
+xvram_status XVRAM_CALL session_create_v2(const xvram_session_config_v2* config,
+                                          xvram_session* out) noexcept {
   if (out == nullptr) return XVRAM_STATUS_INVALID_ARGUMENT;
   *out = nullptr;
-  const xvram_status checked = boundary({}, "session_create_v2", [&]() -> Error {
-    if (Error e = validate_session_config_v2(config)) return e;
+  const xvram_status checked = guarded(nullptr, "session_create_v2", [&]() -> Error {
+    if (Error e = check_session_config_v2(config)) return e;
     if (config->compression_mode != XVRAM_COMPRESSION_DISABLED)
       return make_error(XVRAM_STATUS_UNSUPPORTED, "session", "session_create_v2",
                         "host compression is not provided on this device path; use "
@@ -326,307 +368,227 @@ xvram_status XVRAM_CALL session_create_v2_entry(const xvram_session_config_v2* c
     return {};
   });
   if (checked != XVRAM_STATUS_SUCCESS) return checked;
-  return session_create_entry(&config->v1, out);
+  return session_create(&config->v1, out);
 }
 
-xvram_status XVRAM_CALL session_get_telemetry_v2_entry(xvram_session s,
-                                                       xvram_session_telemetry_v2* out) noexcept {
-  if (s == nullptr || !s->state || !has_v1_size(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(s->state, "session_get_telemetry_v2", [&]() -> Error {
-    const uint32_t caller = out->struct_size;
-    xvram_session_telemetry_v2 local{};
-    local.struct_size = sizeof(local);
-    if (Error e = s->state->backend->telemetry_v2(local)) return e;
-    local.struct_size = caller;
-    *out = local;
+xvram_status XVRAM_CALL session_get_error(xvram_session s, xvram_error_info_v1* out) noexcept {
+  if (!live(s) || !versioned(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  return guarded(s->session.get(), "session_get_error", [&]() -> Error {
+    write_error_info(s->session->last_failure(), *out);
     return {};
   });
 }
 
-xvram_status XVRAM_CALL session_get_error_entry(xvram_session s, xvram_error_info_v1* out) noexcept {
-  if (s == nullptr || !s->state || !has_v1_size(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(s->state, "session_get_error", [&]() -> Error {
-    write_error_info(s->state->error(), *out);
+xvram_status XVRAM_CALL session_get_telemetry(xvram_session s,
+                                              xvram_session_telemetry_v1* out) noexcept {
+  if (!live(s) || !versioned(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  return guarded(s->session.get(), "session_get_telemetry", [&]() -> Error {
+    xvram_session_telemetry_v1 t{};
+    if (Error e = s->session->telemetry(t)) return e;
+    deliver(out, t);
     return {};
   });
 }
 
-xvram_status XVRAM_CALL session_get_telemetry_entry(xvram_session s,
-                                                    xvram_session_telemetry_v1* out) noexcept {
-  if (s == nullptr || !s->state || !has_v1_size(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(s->state, "session_get_telemetry", [&]() -> Error {
-    const uint32_t caller = out->struct_size;
-    xvram_session_telemetry_v1 local{};
-    local.struct_size = sizeof(local);
-    if (Error e = s->state->backend->telemetry(local)) return e;
-    local.struct_size = caller;
-    *out = local;
+xvram_status XVRAM_CALL session_get_telemetry_v2(xvram_session s,
+                                                 xvram_session_telemetry_v2* out) noexcept {
+  if (!live(s) || !versioned(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  return guarded(s->session.get(), "session_get_telemetry_v2", [&]() -> Error {
+    xvram_session_telemetry_v2 t{};
+    if (Error e = s->session->telemetry_v2(t)) return e;
+    deliver(out, t);
     return {};
   });
 }
 
-xvram_status XVRAM_CALL session_drain_entry(xvram_session s, uint64_t timeout_ms) noexcept {
-  if (s == nullptr || !s->state) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(s->state, "session_drain", [&]() { return s->state->backend->drain(timeout_ms); });
+xvram_status XVRAM_CALL session_drain(xvram_session s, uint64_t timeout_ms) noexcept {
+  if (!live(s)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  return guarded(s->session.get(), "session_drain",
+                 [&]() { return s->session->drain(timeout_ms); });
 }
 
-xvram_status XVRAM_CALL session_close_entry(xvram_session s, uint64_t timeout_ms) noexcept {
-  if (s == nullptr || !s->state) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(s->state, "session_close", [&]() -> Error {
-    if (s->state->closed.load(std::memory_order_acquire)) return {};
-    Error e = s->state->backend->close(timeout_ms);
-    if (!e) s->state->closed.store(true, std::memory_order_release);
-    return e;
-  });
+xvram_status XVRAM_CALL session_close(xvram_session s, uint64_t timeout_ms) noexcept {
+  if (!live(s)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  return guarded(s->session.get(), "session_close",
+                 [&]() { return s->session->close(timeout_ms); });
 }
 
-void XVRAM_CALL session_release_entry(xvram_session s) noexcept {
+// Closes without a bound when the caller has not, then frees the handle;
+// other handles keep the closed session's records alive until released.
+void XVRAM_CALL session_release(xvram_session s) noexcept {
   if (s == nullptr) return;
-  try {
-    if (s->state && !s->state->closed.load(std::memory_order_acquire)) {
-      Error e = s->state->backend->close(XVRAM_TIMEOUT_INFINITE);
-      if (!e) s->state->closed.store(true, std::memory_order_release);
-      else s->state->record(e);
-    }
-  } catch (...) {
-  }
+  if (s->session) (void)guarded(s->session.get(), "session_release", [&]() {
+    return s->session->close(XVRAM_TIMEOUT_INFINITE);
+  });
   delete s;
 }
 
-xvram_status XVRAM_CALL allocation_create_entry(xvram_session s, const xvram_allocation_desc_v1* d,
-                                                xvram_allocation* out) noexcept {
+xvram_status XVRAM_CALL allocation_create(xvram_session s, const xvram_allocation_desc_v1* d,
+                                          xvram_allocation* out) noexcept {
   if (out == nullptr) return XVRAM_STATUS_INVALID_ARGUMENT;
   *out = nullptr;
-  if (s == nullptr || !s->state) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(s->state, "allocation_create", [&]() -> Error {
-    if (!has_v1_size(d))
-      return incompatible("allocation_create", "allocation descriptor is null or smaller than v1");
-    if (d->size_bytes == 0) return invalid("allocation_create", "allocation size must be non-zero");
-    if ((d->flags & ~static_cast<uint32_t>(XVRAM_ALLOCATION_FLAG_ZERO_INITIALIZE)) != 0 ||
-        d->reserved0 != 0 || !all_zero(d->reserved, 2))
-      return invalid("allocation_create", "unknown flags or non-zero reserved field");
-    if (d->priority > XVRAM_ALLOCATION_STREAMING)
-      return invalid("allocation_create", "invalid allocation priority");
-    if (d->alignment_bytes != 0 && (d->alignment_bytes & (d->alignment_bytes - 1)) != 0)
-      return invalid("allocation_create", "alignment must be zero or a power of two");
-    if (d->alignment_bytes > s->state->chunk_bytes ||
-        (d->alignment_bytes != 0 && s->state->chunk_bytes % d->alignment_bytes != 0))
-      return invalid("allocation_create", "alignment must divide the effective runtime chunk size");
-    std::shared_ptr<AllocationRecord> rec;
-    if (Error e = s->state->backend->allocate(*d, rec)) return e;
-    auto* handle = new (std::nothrow) xvram_allocation_t{s->state, rec};
+  if (!live(s)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  constexpr const char* entry = "allocation_create";
+  return guarded(s->session.get(), entry, [&]() -> Error {
+    if (!versioned(d)) return too_old(entry, "the allocation descriptor is missing or older than v1");
+    if (Error e = first_broken(kAllocationRules, *d, entry)) return e;
+    const uint64_t frame = s->session->chunk_size_bytes();
+    if (d->alignment_bytes > frame || (d->alignment_bytes != 0 && frame % d->alignment_bytes != 0))
+      return bad_argument(entry, "alignment_bytes does not divide the session's frame size");
+    std::shared_ptr<AllocationRecord> record;
+    if (Error e = s->session->allocate(*d, record)) return e;
+    auto* handle = new (std::nothrow) xvram_allocation_t{{s->session, record}};
     if (handle == nullptr) {
-      try {
-        (void)s->state->backend->release(*rec);
-      } catch (...) {
-      }
-      return make_error(XVRAM_STATUS_HOST_OUT_OF_MEMORY, "sdk", "allocation_create",
-                        "failed to allocate handle");
+      // The host backing exists already: give it back rather than leak it.
+      record->released = true;
+      (void)s->session->release(*record);
+      return no_host_memory(entry);
     }
     *out = handle;
     return {};
   });
 }
 
-xvram_status XVRAM_CALL allocation_get_info_entry(xvram_allocation a,
-                                                  xvram_allocation_info_v1* out) noexcept {
-  if (a == nullptr || !a->owner || !a->backend || !has_v1_size(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(a->owner, "allocation_get_info", [&]() -> Error {
-    if (a->backend->released)
-      return make_error(XVRAM_STATUS_CLOSED, "allocation", "info", "allocation is released");
-    const uint32_t caller = out->struct_size;
-    xvram_allocation_info_v1 local{};
-    local.struct_size = caller;
-    local.allocation_id = a->backend->id;
-    local.size_bytes = a->backend->bytes;
-    local.alignment_bytes = a->backend->desc.alignment_bytes;
-    local.priority = a->backend->desc.priority;
-    local.flags = 0;
-    // Transactions see each allocation at one device VA reserved on first use
-    // and kept until release.
-    local.stable_virtual_address = 1;
-    *out = local;
+xvram_status XVRAM_CALL allocation_get_info(xvram_allocation a,
+                                            xvram_allocation_info_v1* out) noexcept {
+  if (!live(a) || !versioned(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  return guarded(a->session.get(), "allocation_get_info", [&]() -> Error {
+    const AllocationRecord& r = *a->object;
+    if (r.released)
+      return make_error(XVRAM_STATUS_CLOSED, "allocation", "info", "the allocation was released");
+    xvram_allocation_info_v1 info{};
+    info.allocation_id = r.id;
+    info.size_bytes = r.bytes;
+    info.alignment_bytes = r.desc.alignment_bytes;
+    info.priority = r.desc.priority;
+    // Transactions see each allocation at one device VA, reserved on first
+    // use and kept until release.
+    info.stable_virtual_address = 1;
+    deliver(out, info);
     return {};
   });
 }
 
-Error live_allocation(xvram_allocation a, const char* op, std::shared_ptr<Session>& session) {
-  session = a->backend->owner.lock();
-  if (!session || a->backend->released)
-    return make_error(XVRAM_STATUS_CLOSED, "allocation", op, "allocation is released");
-  return {};
-}
-
-xvram_status XVRAM_CALL allocation_write_entry(xvram_allocation a, uint64_t offset, const void* src,
-                                               uint64_t bytes) noexcept {
-  if (a == nullptr || !a->owner || !a->backend || (bytes != 0 && src == nullptr))
-    return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(a->owner, "allocation_write", [&]() -> Error {
-    std::shared_ptr<Session> session;
-    if (Error e = live_allocation(a, "write", session)) return e;
-    if (bytes == 0) return {};
-    return session->write(*a->backend, offset, src, bytes);
+// Host copies into and out of an allocation's authoritative host store.
+template <class Copy>
+xvram_status host_copy(xvram_allocation a, const char* entry, const char* verb, Copy&& copy) {
+  return guarded(a->session.get(), entry, [&]() -> Error {
+    std::shared_ptr<Session> owner = a->object->owner.lock();
+    if (!owner || a->object->released)
+      return make_error(XVRAM_STATUS_CLOSED, "allocation", verb, "the allocation was released");
+    return copy(*owner);
   });
 }
 
-xvram_status XVRAM_CALL allocation_read_entry(xvram_allocation a, uint64_t offset, void* dst,
-                                              uint64_t bytes) noexcept {
-  if (a == nullptr || !a->owner || !a->backend || (bytes != 0 && dst == nullptr))
-    return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(a->owner, "allocation_read", [&]() -> Error {
-    std::shared_ptr<Session> session;
-    if (Error e = live_allocation(a, "read", session)) return e;
-    if (bytes == 0) return {};
-    return session->read(*a->backend, offset, dst, bytes);
+xvram_status XVRAM_CALL allocation_write(xvram_allocation a, uint64_t offset, const void* src,
+                                         uint64_t bytes) noexcept {
+  if (!live(a) || (bytes != 0 && src == nullptr)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  return host_copy(a, "allocation_write", "write", [&](Session& owner) -> Error {
+    return bytes == 0 ? Error{} : owner.write(*a->object, offset, src, bytes);
   });
 }
 
-xvram_status XVRAM_CALL allocation_release_entry(xvram_allocation a) noexcept {
-  if (a == nullptr || !a->owner || !a->backend) return XVRAM_STATUS_INVALID_ARGUMENT;
-  if (a->owner->closed.load(std::memory_order_acquire)) {
+xvram_status XVRAM_CALL allocation_read(xvram_allocation a, uint64_t offset, void* dst,
+                                        uint64_t bytes) noexcept {
+  if (!live(a) || (bytes != 0 && dst == nullptr)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  return host_copy(a, "allocation_read", "read", [&](Session& owner) -> Error {
+    return bytes == 0 ? Error{} : owner.read(*a->object, offset, dst, bytes);
+  });
+}
+
+// After a successful session close every allocation is gone with the
+// runtime, so releasing a handle is then local and always succeeds. Before
+// that, the first release frees the host store; the handle is freed only on
+// success, so a failed release can be retried.
+xvram_status XVRAM_CALL allocation_release(xvram_allocation a) noexcept {
+  if (!live(a)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  if (a->session->closed()) {
     delete a;
     return XVRAM_STATUS_SUCCESS;
   }
-  const xvram_status result = boundary(a->owner, "allocation_release", [&]() -> Error {
-    bool expected = false;
-    if (!a->backend->released.compare_exchange_strong(expected, true)) return {};
-    auto session = a->backend->owner.lock();
-    if (!session) return {};
-    Error e = session->release(*a->backend);
+  const xvram_status status = guarded(a->session.get(), "allocation_release", [&]() -> Error {
+    AllocationRecord& r = *a->object;
+    if (r.released.exchange(true)) return {};
+    Error e = a->session->release(r);
     if (e.status == XVRAM_STATUS_CLOSED) return {};
-    if (e) a->backend->released.store(false);
+    if (e) r.released = false;
     return e;
   });
-  if (result == XVRAM_STATUS_SUCCESS) delete a;
-  return result;
+  if (status == XVRAM_STATUS_SUCCESS) delete a;
+  return status;
 }
 
-xvram_status XVRAM_CALL operation_wait_entry(xvram_operation op, uint64_t timeout_ms,
-                                             xvram_operation_info_v1* out) noexcept;
-void XVRAM_CALL operation_release_entry(xvram_operation op) noexcept;
-
-Error wrap_operation(const std::shared_ptr<SessionState>& owner, std::shared_ptr<Operation> backend,
-                     xvram_operation* out) {
-  if (!backend)
-    return make_error(XVRAM_STATUS_INTERNAL, "sdk", "operation_create",
-                      "backend returned success without an operation");
-  auto* handle = new (std::nothrow) xvram_operation_t{owner, backend};
-  if (handle == nullptr) {
-    try {
-      (void)backend->cancel();
-    } catch (...) {
-    }
-    return make_error(XVRAM_STATUS_HOST_OUT_OF_MEMORY, "sdk", "operation_create",
-                      "failed to allocate operation handle");
-  }
-  *out = handle;
-  return {};
-}
-
-xvram_status XVRAM_CALL prefetch_submit_entry(xvram_session s, const xvram_prefetch_desc_v1* d,
-                                              xvram_operation* out) noexcept {
+xvram_status XVRAM_CALL prefetch_submit(xvram_session s, const xvram_prefetch_desc_v1* d,
+                                        xvram_operation* out) noexcept {
   if (out == nullptr) return XVRAM_STATUS_INVALID_ARGUMENT;
   *out = nullptr;
-  if (s == nullptr || !s->state) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(s->state, "prefetch_submit", [&]() -> Error {
-    if (!has_v1_size(d)) return incompatible("prefetch_submit", "prefetch descriptor is null or smaller than v1");
-    if (d->flags != 0 || !all_zero(d->reserved, 2))
-      return invalid("prefetch_submit", "unknown flags or non-zero reserved field");
-    if (Error e = validate_deadline(d->deadline_ms, "prefetch_submit")) return e;
+  if (!live(s)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  constexpr const char* entry = "prefetch_submit";
+  return guarded(s->session.get(), entry, [&]() -> Error {
+    if (!versioned(d)) return too_old(entry, "the prefetch descriptor is missing or older than v1");
+    if (d->flags != 0 || !zeroed(d->reserved))
+      return bad_argument(entry, "prefetch flags and reserved[] must be zero");
+    if (Error e = check_deadline_ms(d->deadline_ms, entry)) return e;
     std::vector<Session::Access> accesses;
-    if (Error e = collect_accesses(s->state, d->ranges, d->range_count, "prefetch_submit", accesses))
+    if (Error e = gather_accesses(s->session.get(), d->ranges, d->range_count, entry, accesses))
       return e;
     std::shared_ptr<Operation> op;
-    if (Error e = s->state->backend->submit_prefetch(std::move(accesses), d->deadline_ms, op)) return e;
-    return wrap_operation(s->state, std::move(op), out);
+    if (Error e = s->session->submit_prefetch(std::move(accesses), d->deadline_ms, op)) return e;
+    return hand_out_operation(s->session, std::move(op), out, entry);
   });
 }
 
-xvram_status XVRAM_CALL transaction_submit_entry(xvram_session s, const xvram_transaction_desc_v1* d,
-                                                 xvram_operation* out) noexcept {
+xvram_status XVRAM_CALL transaction_submit(xvram_session s, const xvram_transaction_desc_v1* d,
+                                           xvram_operation* out) noexcept {
   if (out == nullptr) return XVRAM_STATUS_INVALID_ARGUMENT;
   *out = nullptr;
-  if (s == nullptr || !s->state) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(s->state, "transaction_submit", [&]() -> Error {
-    if (!has_v1_size(d))
-      return incompatible("transaction_submit", "transaction descriptor is null or smaller than v1");
-    if (d->flags != 0 || !all_zero(d->reserved, 2))
-      return invalid("transaction_submit", "unknown flags or non-zero reserved field");
-    if (d->callback == nullptr) return invalid("transaction_submit", "transaction callback is null");
-    if (d->workspace_bytes > s->state->workspace_cap_bytes)
-      return invalid("transaction_submit", "transaction workspace exceeds the session cap");
-    if (Error e = validate_deadline(d->deadline_ms, "transaction_submit")) return e;
+  if (!live(s)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  constexpr const char* entry = "transaction_submit";
+  return guarded(s->session.get(), entry, [&]() -> Error {
+    if (!versioned(d))
+      return too_old(entry, "the transaction descriptor is missing or older than v1");
+    if (d->flags != 0 || !zeroed(d->reserved))
+      return bad_argument(entry, "transaction flags and reserved[] must be zero");
+    if (d->callback == nullptr) return bad_argument(entry, "callback is NULL");
+    if (d->workspace_bytes > s->session->config().workspace_cap_bytes)
+      return bad_argument(entry, "workspace_bytes exceeds the session's workspace_cap_bytes");
+    if (Error e = check_deadline_ms(d->deadline_ms, entry)) return e;
     std::vector<Session::Access> accesses;
-    if (Error e = collect_accesses(s->state, d->ranges, d->range_count, "transaction_submit", accesses))
+    if (Error e = gather_accesses(s->session.get(), d->ranges, d->range_count, entry, accesses))
       return e;
     std::shared_ptr<Operation> op;
-    if (Error e = s->state->backend->submit_transaction(std::move(accesses), d->workspace_bytes,
-                                                        d->deadline_ms, d->callback, d->user_data, op))
+    if (Error e = s->session->submit_transaction(std::move(accesses), d->workspace_bytes,
+                                                 d->deadline_ms, d->callback, d->user_data, op))
       return e;
-    return wrap_operation(s->state, std::move(op), out);
+    return hand_out_operation(s->session, std::move(op), out, entry);
   });
 }
 
-xvram_status XVRAM_CALL transaction_execute_entry(xvram_session s, const xvram_transaction_desc_v1* d,
-                                                  uint64_t timeout_ms) noexcept {
-  xvram_operation op = nullptr;
-  const xvram_status submit = transaction_submit_entry(s, d, &op);
-  if (submit != XVRAM_STATUS_SUCCESS) return submit;
-  xvram_operation_info_v1 info = XVRAM_OPERATION_INFO_V1_INIT;
-  const xvram_status wait = operation_wait_entry(op, timeout_ms, &info);
-  if (wait != XVRAM_STATUS_SUCCESS) {
-    operation_release_entry(op);
-    return wait;
-  }
-  xvram_status result = info.result;
-  if (result != XVRAM_STATUS_SUCCESS) {
-    result = boundary(op->owner, "transaction_execute", [&]() -> Error {
-      Error e = op->backend->error();
-      return e ? e : make_error(info.result, "transaction", "execute", "transaction operation failed");
-    });
-  }
-  operation_release_entry(op);
-  return result;
+xvram_status XVRAM_CALL transaction_execute(xvram_session s, const xvram_transaction_desc_v1* d,
+                                            uint64_t timeout_ms) noexcept {
+  return run_to_end([&](xvram_operation* op) { return transaction_submit(s, d, op); }, timeout_ms,
+                    "transaction_execute");
 }
 
-// gemm_plan_create, with an optional fused epilogue (extension table).
+// gemm_plan_create, with the extension's epilogue when `epilogue` is given.
 xvram_status create_plan(xvram_session s, const xvram_gemm_desc_v1* d,
                          const xvram_amd_epilogue_v1* epilogue, xvram_gemm_plan* out) noexcept {
   if (out == nullptr) return XVRAM_STATUS_INVALID_ARGUMENT;
   *out = nullptr;
-  if (s == nullptr || !s->state) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(s->state, "gemm_plan_create", [&]() -> Error {
-    if (!has_v1_size(d)) return incompatible("gemm_plan_create", "GEMM descriptor is null or smaller than v1");
-    std::shared_ptr<AllocationRecord> bias;
-    EpilogueSpec ep;
-    if (epilogue != nullptr) {
-      if (epilogue->struct_size < sizeof(xvram_amd_epilogue_v1))
-        return incompatible("gemm_plan_create", "epilogue descriptor is smaller than v1");
-      if (epilogue->flags != 0 || !all_zero(epilogue->reserved, 2))
-        return invalid("gemm_plan_create", "unknown epilogue flags or non-zero reserved field");
-      if (epilogue->bias != nullptr) {
-        if (!epilogue->bias->backend || epilogue->bias->owner.get() != s->state.get())
-          return invalid("gemm_plan_create", "bias allocation belongs to another session");
-        bias = epilogue->bias->backend;
-      }
-      ep.bias_offset_bytes = epilogue->bias_offset_bytes;
-      ep.bias_axis = epilogue->bias_axis;
-      ep.activation = epilogue->activation;
-      if (ep.bias_axis != XVRAM_AMD_BIAS_NONE && !bias)
-        return invalid("gemm_plan_create", "bias axis given without a bias allocation");
-      if (ep.bias_axis == XVRAM_AMD_BIAS_NONE && bias)
-        return invalid("gemm_plan_create", "a bias allocation needs a bias axis");
-    }
-    if (d->flags != 0 || d->reserved0 != 0 || !all_zero(d->reserved, 3))
-      return invalid("gemm_plan_create", "unknown GEMM flags or non-zero reserved field");
-    const bool ops_ok = d->operation_a <= XVRAM_MATRIX_OP_T && d->operation_b <= XVRAM_MATRIX_OP_T;
-    if (!ops_ok || d->compute_mode > XVRAM_COMPUTE_FP64)
-      return invalid("gemm_plan_create", "invalid GEMM operation or compute mode");
-    if (Error e = validate_deadline(d->deadline_ms, "gemm_plan_create")) return e;
+  if (!live(s)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  constexpr const char* entry = "gemm_plan_create";
+  return guarded(s->session.get(), entry, [&]() -> Error {
+    if (!versioned(d)) return too_old(entry, "the GEMM descriptor is missing or older than v1");
+    if (Error e = first_broken(kGemmRules, *d, entry)) return e;
+    if (Error e = check_deadline_ms(d->deadline_ms, entry)) return e;
     GemmSpec spec;
-    if (Error e = convert_matrix(s->state, d->a, spec.a)) return e;
-    if (Error e = convert_matrix(s->state, d->b, spec.b)) return e;
-    if (Error e = convert_matrix(s->state, d->c, spec.c)) return e;
+    const std::pair<const Matrix*, MatrixSpec*> operands[] = {
+        {&d->a, &spec.a}, {&d->b, &spec.b}, {&d->c, &spec.c}};
+    for (const auto& [in, spec_out] : operands)
+      if (Error e = read_matrix(s->session.get(), *in, *spec_out)) return e;
+    std::shared_ptr<AllocationRecord> bias;
+    if (epilogue != nullptr)
+      if (Error e = read_epilogue(s->session.get(), *epilogue, spec.epilogue, bias)) return e;
     spec.operation_a = d->operation_a;
     spec.operation_b = d->operation_b;
     spec.compute_mode = d->compute_mode;
@@ -635,31 +597,26 @@ xvram_status create_plan(xvram_session s, const xvram_gemm_desc_v1* d,
     spec.tile_m_hint = d->tile_m_hint;
     spec.tile_n_hint = d->tile_n_hint;
     spec.tile_k_hint = d->tile_k_hint;
-    spec.epilogue = ep;
-    std::shared_ptr<GemmPlanRecord> rec;
-    if (Error e = s->state->backend->create_gemm_plan(spec, d->a.allocation->backend,
-                                                      d->b.allocation->backend,
-                                                      d->c.allocation->backend, d->deadline_ms, rec,
-                                                      bias))
+    std::shared_ptr<GemmPlanRecord> plan;
+    if (Error e = s->session->create_gemm_plan(spec, d->a.allocation->object,
+                                               d->b.allocation->object, d->c.allocation->object,
+                                               d->deadline_ms, plan, bias))
       return e;
-    auto* handle = new (std::nothrow) xvram_gemm_plan_t{s->state, rec};
-    if (handle == nullptr)
-      return make_error(XVRAM_STATUS_HOST_OUT_OF_MEMORY, "sdk", "gemm_plan_create",
-                        "failed to allocate plan handle");
+    auto* handle = new (std::nothrow) xvram_gemm_plan_t{{s->session, plan}};
+    if (handle == nullptr) return no_host_memory(entry);
     *out = handle;
     return {};
   });
 }
 
-xvram_status XVRAM_CALL gemm_plan_create_entry(xvram_session s, const xvram_gemm_desc_v1* d,
-                                               xvram_gemm_plan* out) noexcept {
+xvram_status XVRAM_CALL gemm_plan_create(xvram_session s, const xvram_gemm_desc_v1* d,
+                                         xvram_gemm_plan* out) noexcept {
   return create_plan(s, d, nullptr, out);
 }
 
-xvram_status XVRAM_CALL gemm_plan_create_epilogue_entry(xvram_session s,
-                                                        const xvram_gemm_desc_v1* d,
-                                                        const xvram_amd_epilogue_v1* epilogue,
-                                                        xvram_gemm_plan* out) noexcept {
+xvram_status XVRAM_CALL gemm_plan_create_epilogue(xvram_session s, const xvram_gemm_desc_v1* d,
+                                                  const xvram_amd_epilogue_v1* epilogue,
+                                                  xvram_gemm_plan* out) noexcept {
   if (epilogue == nullptr) {
     if (out != nullptr) *out = nullptr;
     return XVRAM_STATUS_INVALID_ARGUMENT;
@@ -667,248 +624,200 @@ xvram_status XVRAM_CALL gemm_plan_create_epilogue_entry(xvram_session s,
   return create_plan(s, d, epilogue, out);
 }
 
-xvram_status XVRAM_CALL gemm_plan_get_info_entry(xvram_gemm_plan p, xvram_gemm_plan_info_v1* out) noexcept {
-  if (p == nullptr || !p->owner || !p->backend || !has_v1_size(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(p->owner, "gemm_plan_get_info", [&]() -> Error {
-    const uint32_t caller = out->struct_size;
-    xvram_gemm_plan_info_v1 local = XVRAM_GEMM_PLAN_INFO_V1_INIT;
-    const GemmPlanData& plan = p->backend->plan;
-    uint64_t m, n, k;
-    problem_dims(p->backend->spec, m, n, k);
-    local.m = m;
-    local.n = n;
-    local.k = k;
+xvram_status XVRAM_CALL gemm_plan_get_info(xvram_gemm_plan p,
+                                           xvram_gemm_plan_info_v1* out) noexcept {
+  if (!live(p) || !versioned(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  return guarded(p->session.get(), "gemm_plan_get_info", [&]() -> Error {
+    const GemmPlanRecord& record = *p->object;
+    const GemmPlanData& plan = record.plan;
+    xvram_gemm_plan_info_v1 info = XVRAM_GEMM_PLAN_INFO_V1_INIT;
+    problem_dims(record.spec, info.m, info.n, info.k);
     // Tile extents in the caller's orientation (m/n swap back for row-major C).
-    local.tile_m = plan.problem.swapped ? plan.tn : plan.tm;
-    local.tile_n = plan.problem.swapped ? plan.tm : plan.tn;
-    local.tile_k = plan.bk;
+    info.tile_m = plan.problem.swapped ? plan.tn : plan.tm;
+    info.tile_n = plan.problem.swapped ? plan.tm : plan.tn;
+    info.tile_k = plan.bk;
     // One launch's working set: its C tile and an A and a B panel frame per
     // K panel it covers.
-    auto session = p->backend->owner.lock();
-    local.maximum_working_set_bytes =
-        session ? (1 + 2 * uint64_t{plan.panels_per_launch}) * session->chunk_size_bytes() : 0;
-    local.workspace_bytes = 0;
+    info.maximum_working_set_bytes =
+        (1 + 2 * uint64_t{plan.panels_per_launch}) * p->session->chunk_size_bytes();
+    info.workspace_bytes = 0;
     // Tiles of the plan's geometry (reference planner.cpp:163 tile_count):
     // C tiles x K panels, however many K panels one launch covers.
-    local.tile_count = plan.tiles_m * plan.tiles_n * plan.panels_k;
-    local.effective_compute_mode = XVRAM_COMPUTE_FP32_STRICT;
-    local.uses_cublas_lt = 0;
-    local.struct_size = caller;
-    *out = local;
+    info.tile_count = record.tile_count();
+    info.effective_compute_mode = XVRAM_COMPUTE_FP32_STRICT;
+    info.uses_cublas_lt = 0;
+    deliver(out, info);
     return {};
   });
 }
 
-xvram_status XVRAM_CALL gemm_submit_entry(xvram_gemm_plan p, xvram_operation* out) noexcept {
+xvram_status XVRAM_CALL gemm_submit(xvram_gemm_plan p, xvram_operation* out) noexcept {
   if (out == nullptr) return XVRAM_STATUS_INVALID_ARGUMENT;
   *out = nullptr;
-  if (p == nullptr || !p->owner || !p->backend) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(p->owner, "gemm_submit", [&]() -> Error {
-    auto session = p->backend->owner.lock();
-    if (!session) return make_error(XVRAM_STATUS_CLOSED, "gemm", "submit", "session is closed");
+  if (!live(p)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  return guarded(p->session.get(), "gemm_submit", [&]() -> Error {
     std::shared_ptr<Operation> op;
-    if (Error e = session->submit_gemm(p->backend, op)) return e;
-    return wrap_operation(p->owner, std::move(op), out);
+    if (Error e = p->session->submit_gemm(p->object, op)) return e;
+    return hand_out_operation(p->session, std::move(op), out, "gemm_submit");
   });
 }
 
-xvram_status XVRAM_CALL gemm_execute_entry(xvram_gemm_plan p, uint64_t timeout_ms) noexcept {
-  xvram_operation op = nullptr;
-  const xvram_status submit = gemm_submit_entry(p, &op);
-  if (submit != XVRAM_STATUS_SUCCESS) return submit;
-  xvram_operation_info_v1 info = XVRAM_OPERATION_INFO_V1_INIT;
-  const xvram_status wait = operation_wait_entry(op, timeout_ms, &info);
-  if (wait != XVRAM_STATUS_SUCCESS) {
-    operation_release_entry(op);
-    return wait;
-  }
-  xvram_status result = info.result;
-  if (result != XVRAM_STATUS_SUCCESS) {
-    result = boundary(op->owner, "gemm_execute", [&]() -> Error {
-      Error e = op->backend->error();
-      return e ? e : make_error(info.result, "gemm", "execute", "GEMM operation failed");
-    });
-  }
-  operation_release_entry(op);
-  return result;
+xvram_status XVRAM_CALL gemm_execute(xvram_gemm_plan p, uint64_t timeout_ms) noexcept {
+  return run_to_end([&](xvram_operation* op) { return gemm_submit(p, op); }, timeout_ms,
+                    "gemm_execute");
 }
 
-void XVRAM_CALL gemm_plan_release_entry(xvram_gemm_plan p) noexcept {
-  try {
-    delete p;
-  } catch (...) {
-  }
-}
+void XVRAM_CALL gemm_plan_release(xvram_gemm_plan p) noexcept { delete p; }
 
-xvram_status XVRAM_CALL operation_poll_entry(xvram_operation op, xvram_operation_info_v1* out) noexcept {
-  if (op == nullptr || !op->owner || !op->backend || !has_v1_size(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(op->owner, "operation_poll", [&]() -> Error {
-    const uint32_t caller = out->struct_size;
-    xvram_operation_info_v1 local = XVRAM_OPERATION_INFO_V1_INIT;
-    Error e = op->backend->poll(local);
-    local.struct_size = caller;
-    *out = local;
-    return e;
-  });
-}
-
-xvram_status XVRAM_CALL operation_wait_entry(xvram_operation op, uint64_t timeout_ms,
-                                             xvram_operation_info_v1* out) noexcept {
-  if (op == nullptr || !op->owner || !op->backend || !has_v1_size(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(op->owner, "operation_wait", [&]() -> Error {
-    const uint32_t caller = out->struct_size;
-    xvram_operation_info_v1 local = XVRAM_OPERATION_INFO_V1_INIT;
-    Error e = op->backend->wait(timeout_ms, local);
-    local.struct_size = caller;
-    *out = local;
-    return e;
-  });
-}
-
-xvram_status XVRAM_CALL operation_cancel_entry(xvram_operation op) noexcept {
-  if (op == nullptr || !op->owner || !op->backend) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(op->owner, "operation_cancel", [&]() { return op->backend->cancel(); });
-}
-
-xvram_status XVRAM_CALL operation_get_error_entry(xvram_operation op, xvram_error_info_v1* out) noexcept {
-  if (op == nullptr || !op->owner || !op->backend || !has_v1_size(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
-  return boundary(op->owner, "operation_get_error", [&]() -> Error {
-    write_error_info(op->backend->error(), *out);
+xvram_status XVRAM_CALL operation_poll(xvram_operation op, xvram_operation_info_v1* out) noexcept {
+  if (!live(op) || !versioned(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  return guarded(op->session.get(), "operation_poll", [&]() -> Error {
+    deliver(out, op->object->snapshot());
     return {};
   });
 }
 
-void XVRAM_CALL operation_release_entry(xvram_operation op) noexcept {
+// Fills `out` whether or not the operation finished; TIMEOUT when it did not.
+xvram_status XVRAM_CALL operation_wait(xvram_operation op, uint64_t timeout_ms,
+                                       xvram_operation_info_v1* out) noexcept {
+  if (!live(op) || !versioned(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  return guarded(op->session.get(), "operation_wait", [&]() -> Error {
+    const bool settled = op->object->settled_within(timeout_ms);
+    deliver(out, op->object->snapshot());
+    if (settled) return {};
+    return make_error(XVRAM_STATUS_TIMEOUT, "operation", "wait",
+                      "the operation did not finish within the timeout");
+  });
+}
+
+xvram_status XVRAM_CALL operation_cancel(xvram_operation op) noexcept {
+  if (!live(op)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  return guarded(op->session.get(), "operation_cancel", [&]() { return op->object->cancel(); });
+}
+
+xvram_status XVRAM_CALL operation_get_error(xvram_operation op, xvram_error_info_v1* out) noexcept {
+  if (!live(op) || !versioned(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
+  return guarded(op->session.get(), "operation_get_error", [&]() -> Error {
+    write_error_info(op->object->failure(), *out);
+    return {};
+  });
+}
+
+void XVRAM_CALL operation_release(xvram_operation op) noexcept { delete op; }
+
+xvram_status XVRAM_CALL device_get_info(int32_t ordinal, xvram_amd_device_info_v1* out) noexcept {
+  if (!versioned(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
   try {
-    delete op;
-  } catch (...) {
-  }
-}
-
-const xvram_api_v1& api_v1() noexcept {
-  static const xvram_api_v1 api = [] {
-    xvram_api_v1 v{};
-    v.struct_size = sizeof(v);
-    v.abi_version = XVRAM_ABI_VERSION_1;
-    v.status_name = &status_name_entry;
-    v.session_create = &session_create_entry;
-    v.session_get_error = &session_get_error_entry;
-    v.session_get_telemetry = &session_get_telemetry_entry;
-    v.session_drain = &session_drain_entry;
-    v.session_close = &session_close_entry;
-    v.session_release = &session_release_entry;
-    v.allocation_create = &allocation_create_entry;
-    v.allocation_get_info = &allocation_get_info_entry;
-    v.allocation_write = &allocation_write_entry;
-    v.allocation_read = &allocation_read_entry;
-    v.allocation_release = &allocation_release_entry;
-    v.prefetch_submit = &prefetch_submit_entry;
-    v.transaction_submit = &transaction_submit_entry;
-    v.transaction_execute = &transaction_execute_entry;
-    v.gemm_plan_create = &gemm_plan_create_entry;
-    v.gemm_plan_get_info = &gemm_plan_get_info_entry;
-    v.gemm_submit = &gemm_submit_entry;
-    v.gemm_execute = &gemm_execute_entry;
-    v.gemm_plan_release = &gemm_plan_release_entry;
-    v.operation_poll = &operation_poll_entry;
-    v.operation_wait = &operation_wait_entry;
-    v.operation_cancel = &operation_cancel_entry;
-    v.operation_get_error = &operation_get_error_entry;
-    v.operation_release = &operation_release_entry;
-    return v;
-  }();
-  return api;
-}
-
-// src/sdk/api.cpp:1002-1013: the v1 table first (its struct_size and
-// abi_version describing the v2 table), then the two v2 entries.
-const xvram_api_v2& api_v2() {
-  static const xvram_api_v2 api = [] {
-    xvram_api_v2 v{};
-    v.v1 = api_v1();
-    v.v1.struct_size = sizeof(v);
-    v.v1.abi_version = XVRAM_ABI_VERSION_2;
-    v.session_create_v2 = &session_create_v2_entry;
-    v.session_get_telemetry_v2 = &session_get_telemetry_v2_entry;
-    return v;
-  }();
-  return api;
-}
-
-xvram_status XVRAM_CALL device_get_info_entry(int32_t ordinal,
-                                              xvram_amd_device_info_v1* out) noexcept {
-  if (!has_v1_size(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
-  try {
-    DeviceInfo info;
-    if (int rc = describe_device(ordinal, info)) {
+    DeviceInfo d;
+    if (const int rc = describe_device(ordinal, d))
       return rc == 101 /* hipErrorInvalidDevice */ ? XVRAM_STATUS_INVALID_ARGUMENT
                                                    : XVRAM_STATUS_CUDA_ERROR;
-    }
-    const uint32_t caller = out->struct_size;
-    xvram_amd_device_info_v1 local{};
-    local.struct_size = caller;
-    local.ordinal = ordinal;
-    copy_text(local.name, info.name);
-    copy_text(local.arch, info.arch);
-    copy_text(local.pci_bus_id, info.pci_bus_id);
-    local.total_memory_bytes = info.total_memory;
-    local.free_memory_bytes = info.free_memory;
-    local.granularity_minimum_bytes = info.granularity_minimum;
-    local.granularity_recommended_bytes = info.granularity_recommended;
-    local.compute_major = static_cast<uint32_t>(info.compute_major);
-    local.compute_minor = static_cast<uint32_t>(info.compute_minor);
-    local.multiprocessor_count = static_cast<uint32_t>(info.multiprocessors);
-    local.vmm_supported = info.vmm_supported ? 1u : 0u;
-    local.driver_version = info.driver_version;
-    local.runtime_version = info.runtime_version;
-    *out = local;
+    xvram_amd_device_info_v1 info{};
+    info.ordinal = ordinal;
+    std::snprintf(info.name, sizeof info.name, "%s", d.name.c_str());
+    std::snprintf(info.arch, sizeof info.arch, "%s", d.arch.c_str());
+    std::snprintf(info.pci_bus_id, sizeof info.pci_bus_id, "%s", d.pci_bus_id.c_str());
+    info.total_memory_bytes = d.total_memory;
+    info.free_memory_bytes = d.free_memory;
+    info.granularity_minimum_bytes = d.granularity_minimum;
+    info.granularity_recommended_bytes = d.granularity_recommended;
+    info.compute_major = static_cast<uint32_t>(d.compute_major);
+    info.compute_minor = static_cast<uint32_t>(d.compute_minor);
+    info.multiprocessor_count = static_cast<uint32_t>(d.multiprocessors);
+    info.vmm_supported = d.vmm_supported ? 1u : 0u;
+    info.driver_version = d.driver_version;
+    info.runtime_version = d.runtime_version;
+    deliver(out, info);
     return XVRAM_STATUS_SUCCESS;
   } catch (...) {
     return exception_error("device_get_info").status;
   }
 }
 
-const xvram_amd_ext_v1& ext_v1() {
-  static const xvram_amd_ext_v1 ext = [] {
-    xvram_amd_ext_v1 v{};
-    v.struct_size = sizeof(v);
-    v.ext_version = XVRAM_AMD_EXT_VERSION_1;
-    v.gemm_plan_create_epilogue = &gemm_plan_create_epilogue_entry;
-    v.device_get_info = &device_get_info_entry;
-    return v;
-  }();
-  return ext;
+} // namespace entry
+
+// ---- the tables ----------------------------------------------------------------
+
+// The v1 table with its header describing a table of `size` bytes, version
+// `version` (the v2 table embeds v1 first, headed with v2's size and version).
+xvram_api_v1 table_v1(uint32_t size, uint32_t version) {
+  return xvram_api_v1{
+      .struct_size = size,
+      .abi_version = version,
+      .status_name = entry::status_name,
+      .session_create = entry::session_create,
+      .session_get_error = entry::session_get_error,
+      .session_get_telemetry = entry::session_get_telemetry,
+      .session_drain = entry::session_drain,
+      .session_close = entry::session_close,
+      .session_release = entry::session_release,
+      .allocation_create = entry::allocation_create,
+      .allocation_get_info = entry::allocation_get_info,
+      .allocation_write = entry::allocation_write,
+      .allocation_read = entry::allocation_read,
+      .allocation_release = entry::allocation_release,
+      .prefetch_submit = entry::prefetch_submit,
+      .transaction_submit = entry::transaction_submit,
+      .transaction_execute = entry::transaction_execute,
+      .gemm_plan_create = entry::gemm_plan_create,
+      .gemm_plan_get_info = entry::gemm_plan_get_info,
+      .gemm_submit = entry::gemm_submit,
+      .gemm_execute = entry::gemm_execute,
+      .gemm_plan_release = entry::gemm_plan_release,
+      .operation_poll = entry::operation_poll,
+      .operation_wait = entry::operation_wait,
+      .operation_cancel = entry::operation_cancel,
+      .operation_get_error = entry::operation_get_error,
+      .operation_release = entry::operation_release,
+      .reserved = {},
+  };
+}
+
+const xvram_api_v1 kApiV1 = table_v1(sizeof(xvram_api_v1), XVRAM_ABI_VERSION_1);
+
+const xvram_api_v2 kApiV2 = {
+    .v1 = table_v1(sizeof(xvram_api_v2), XVRAM_ABI_VERSION_2),
+    .session_create_v2 = entry::session_create_v2,
+    .session_get_telemetry_v2 = entry::session_get_telemetry_v2,
+    .reserved = {},
+};
+
+// This build's extension table (no reference counterpart), reached through
+// the one export so the library's symbol set stays the reference's.
+const xvram_amd_ext_v1 kExtV1 = {
+    .struct_size = sizeof(xvram_amd_ext_v1),
+    .ext_version = XVRAM_AMD_EXT_VERSION_1,
+    .gemm_plan_create_epilogue = entry::gemm_plan_create_epilogue,
+    .device_get_info = entry::device_get_info,
+    .reserved = {},
+};
+
+struct TableRef {
+  const void* table;
+  size_t size;
+};
+
+// NULL for a version this library does not serve.
+TableRef table_for(uint32_t version) {
+  switch (version) {
+  case XVRAM_ABI_VERSION_1: return {&kApiV1, sizeof kApiV1};
+  case XVRAM_ABI_VERSION_2: return {&kApiV2, sizeof kApiV2};
+  case XVRAM_AMD_EXT_ABI_VERSION_1: return {&kExtV1, sizeof kExtV1};
+  default: return {nullptr, 0};
+  }
 }
 
 } // namespace
-} // namespace xvram
+} // namespace xvram::abi
 
+// The library's one export (reference include/xvram/xvram.h:532-533): an
+// unknown version is INCOMPATIBLE_ABI; a known one needs a buffer at least
+// as large as its table, else INVALID_ARGUMENT.
 extern "C" XVRAM_API xvram_status XVRAM_CALL xvram_get_api(uint32_t requested_abi_version,
                                                            uint32_t caller_api_size, void* out_api) {
-  // One table per version; the same argument rules for each (reference
-  // src/sdk/api.cpp:967-1035).
-  const void* table = nullptr;
-  size_t size = 0;
-  switch (requested_abi_version) {
-  case XVRAM_ABI_VERSION_1:
-    table = &xvram::api_v1();
-    size = sizeof(xvram_api_v1);
-    break;
-  case XVRAM_ABI_VERSION_2:
-    table = &xvram::api_v2();
-    size = sizeof(xvram_api_v2);
-    break;
-  case XVRAM_AMD_EXT_ABI_VERSION_1:
-    // This build's extension table (no reference counterpart), reached
-    // through the one export so the library's symbol set stays the
-    // reference's.
-    table = &xvram::ext_v1();
-    size = sizeof(xvram_amd_ext_v1);
-    break;
-  default:
-    return XVRAM_STATUS_INCOMPATIBLE_ABI;
-  }
-  if (out_api == nullptr || caller_api_size < size) return XVRAM_STATUS_INVALID_ARGUMENT;
-  std::memcpy(out_api, table, size);
+  const xvram::abi::TableRef t = xvram::abi::table_for(requested_abi_version);
+  if (t.table == nullptr) return XVRAM_STATUS_INCOMPATIBLE_ABI;
+  if (out_api == nullptr || caller_api_size < t.size) return XVRAM_STATUS_INVALID_ARGUMENT;
+  std::memcpy(out_api, t.table, t.size);
   return XVRAM_STATUS_SUCCESS;
 }

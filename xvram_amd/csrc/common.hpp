@@ -9,6 +9,7 @@
 #include <cstdint>
 #include <cstring>
 #include <limits>
+#include <optional>
 #include <string>
 #include <string_view>
 
@@ -40,23 +41,17 @@ inline Error make_error(xvram_status status, std::string_view stage, std::string
   return e;
 }
 
-inline Error invalid(std::string_view operation, std::string_view message) {
-  return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "sdk", operation, message);
-}
-
-inline Error incompatible(std::string_view operation, std::string_view message) {
-  return make_error(XVRAM_STATUS_INCOMPATIBLE_ABI, "sdk", operation, message);
-}
-
-// Status names, identical strings to the reference (src/sdk/status.cpp:83-128).
+// The status names of the ABI (the strings are interface: reference
+// src/sdk/status.cpp:83-128 returns the same name for each code).
 const char* status_name(xvram_status status) noexcept;
 
 // Copies `error` into a public record, preserving the caller's struct_size
-// (src/sdk/status.cpp:130-141).
+// (reference src/sdk/status.cpp:130-141).
 void write_error_info(const Error& error, xvram_error_info_v1& output) noexcept;
 
-// Maps the active exception to an Error (bad_alloc -> HOST_OUT_OF_MEMORY,
-// anything else -> INTERNAL), as the reference boundary does.
+// Maps the exception being handled to an Error: bad_alloc ->
+// HOST_OUT_OF_MEMORY, anything else -> INTERNAL (the reference ABI boundary's
+// mapping, src/sdk/api.cpp:109-122). Call only inside a catch block.
 Error exception_error(std::string_view operation) noexcept;
 
 inline bool checked_add(uint64_t a, uint64_t b, uint64_t& out) {
@@ -74,43 +69,41 @@ inline bool checked_mul(uint64_t a, uint64_t b, uint64_t& out) {
 inline uint64_t round_up(uint64_t v, uint64_t m) { return (v + m - 1) / m * m; }
 inline uint64_t ceil_div(uint64_t v, uint64_t d) { return (v + d - 1) / d; }
 
-// A submission-relative deadline (src/sdk/deadline.hpp:14-63): zero disables
-// it; expiry is now >= submitted + deadline_ms; an unrepresentable deadline is
-// rejected at submission.
+// The submission-relative deadline of an operation (a descriptor's
+// deadline_ms): due that many milliseconds after submission, never for 0.
+// Once it has passed the operation starts no more device work: the worker
+// checks it when it takes the operation off the queue and before each launch.
 class Deadline {
 public:
-  static bool create(uint64_t deadline_ms, Clock::time_point submitted, Deadline& out) {
-    out = Deadline{};
-    out.submitted_ = submitted;
-    if (deadline_ms == 0) return true;
-    const auto remaining = Clock::time_point::max() - submitted;
-    const auto remaining_ms = std::chrono::duration_cast<std::chrono::milliseconds>(remaining).count();
-    if (remaining_ms < 0 || deadline_ms > static_cast<uint64_t>(remaining_ms)) return false;
-    out.at_ = submitted + std::chrono::duration_cast<Clock::duration>(
-                              std::chrono::milliseconds(static_cast<int64_t>(deadline_ms)));
-    out.has_ = true;
-    return true;
+  Deadline() = default;
+  // nullopt when submission + ms lies beyond the steady clock's range.
+  static std::optional<Deadline> after(uint64_t ms, Clock::time_point submitted) {
+    using Ms = std::chrono::milliseconds;
+    Deadline d;
+    d.submitted_ = submitted;
+    if (ms == 0) return d;
+    const int64_t room = std::chrono::duration_cast<Ms>(Clock::time_point::max() - submitted).count();
+    if (room < 0 || ms > static_cast<uint64_t>(room)) return std::nullopt;
+    d.due_ = submitted + std::chrono::duration_cast<Clock::duration>(Ms(static_cast<int64_t>(ms)));
+    return d;
   }
-  bool expired(Clock::time_point now = Clock::now()) const { return has_ && now >= at_; }
+  bool passed(Clock::time_point now = Clock::now()) const { return due_ && now >= *due_; }
   Clock::time_point submitted() const { return submitted_; }
-  Error timeout_error(const char* stage, const char* operation) const {
-    return make_error(XVRAM_STATUS_TIMEOUT, stage, operation,
-                      "operation missed its submission-relative deadline before a safe launch "
-                      "boundary");
+  Error missed(const char* stage, const char* where) const {
+    return make_error(XVRAM_STATUS_TIMEOUT, stage, where,
+                      "deadline_ms passed before the operation reached its next launch boundary");
   }
 
 private:
   Clock::time_point submitted_{};
-  Clock::time_point at_{};
-  bool has_ = false;
+  std::optional<Clock::time_point> due_;
 };
 
-inline Error validate_deadline(uint64_t deadline_ms, const char* operation) {
-  Deadline ignored;
-  if (!Deadline::create(deadline_ms, Clock::now(), ignored))
-    return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "deadline", operation,
-                      "deadline_ms cannot be represented by the monotonic clock");
-  return {};
+// INVALID_ARGUMENT when a descriptor's deadline_ms cannot be represented.
+inline Error check_deadline_ms(uint64_t ms, const char* operation) {
+  if (Deadline::after(ms, Clock::now())) return {};
+  return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "deadline", operation,
+                    "deadline_ms lies beyond the range of the monotonic clock");
 }
 
 } // namespace xvram

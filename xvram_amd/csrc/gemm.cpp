@@ -717,6 +717,7 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
   };
 
   Error result;
+  uint64_t tiles_done = 0; // C tiles x K panels enqueued so far (progress units)
   for (size_t idx = 0; idx < total && !result; ++idx) {
     if (hooks.boundary) {
       if (Error e = hooks.boundary("before_tile")) {
@@ -866,7 +867,8 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
         break;
       }
     }
-    if (hooks.progress) hooks.progress(idx + 1, total);
+    tiles_done += l.panels;
+    if (hooks.progress) hooks.progress(tiles_done, plan.tiles_m * plan.tiles_n * plan.panels_k);
     while (next < total && next <= idx + plan.lookahead) {
       if (Error e = acquire_launch(next++)) {
         result = e;

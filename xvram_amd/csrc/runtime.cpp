@@ -422,7 +422,7 @@ Error Runtime::map_frame_at(Frame& f, uint64_t address) {
       if (Error e = refresh_budget(0, workspace_bytes_, true)) return e;
       if (f.index >= capacity_)
         return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "cache", "mem_create_retry",
-                          "live budget shrink removed the frame selected for allocation");
+                          "a budget shrink took the frame this allocation was about to use");
       rc = device_->mem_create(frame_bytes_, &handle);
     }
     if (rc == 2)

@@ -5,104 +5,136 @@
 
 namespace xvram {
 
-// ---- Operation (reference RuntimeOperation, src/sdk/runtime.cpp:146-279) ----
+// ---- Operation --------------------------------------------------------------
+
+namespace {
+
+// Internal phases of an operation whose terminal record is being written: a
+// snapshot taken meanwhile still shows the phase it is leaving.
+constexpr uint32_t kLeavingQueued = 0x100;
+constexpr uint32_t kLeavingRunning = 0x101;
+
+bool terminal(uint32_t phase) {
+  return phase == XVRAM_OPERATION_COMPLETED || phase == XVRAM_OPERATION_FAILED ||
+         phase == XVRAM_OPERATION_CANCELLED;
+}
+
+uint32_t visible(uint32_t phase) {
+  if (phase == kLeavingQueued) return XVRAM_OPERATION_QUEUED;
+  if (phase == kLeavingRunning) return XVRAM_OPERATION_RUNNING;
+  return phase;
+}
+
+double ms_between(Clock::time_point from, Clock::time_point to) {
+  return std::chrono::duration<double, std::milli>(to - from).count();
+}
+
+} // namespace
 
 Operation::Operation(uint64_t id, uint64_t units_total, Deadline deadline)
-    : deadline_(deadline), id_(id) {
-  info_ = XVRAM_OPERATION_INFO_V1_INIT;
-  info_.operation_id = id;
-  info_.units_total = units_total;
-}
+    : id_(id), units_total_(units_total), deadline_(deadline),
+      settled_(settled_promise_.get_future().share()) {}
 
-Error Operation::poll(xvram_operation_info_v1& out) {
-  std::lock_guard<std::mutex> lock(mutex_);
-  out = info_;
-  return {};
-}
-
-Error Operation::wait(uint64_t timeout_ms, xvram_operation_info_v1& out) {
-  std::unique_lock<std::mutex> lock(mutex_);
-  const auto terminal = [&]() {
-    return info_.state == XVRAM_OPERATION_COMPLETED || info_.state == XVRAM_OPERATION_CANCELLED ||
-           info_.state == XVRAM_OPERATION_FAILED;
-  };
-  bool completed = true;
-  if (!terminal()) {
-    if (timeout_ms == XVRAM_TIMEOUT_INFINITE) {
-      done_.wait(lock, terminal);
-    } else {
-      completed = done_.wait_for(lock, std::chrono::milliseconds(timeout_ms), terminal);
-    }
+xvram_operation_info_v1 Operation::snapshot() const {
+  xvram_operation_info_v1 info = XVRAM_OPERATION_INFO_V1_INIT;
+  info.operation_id = id_;
+  info.units_total = units_total_;
+  const uint32_t phase = phase_.load(std::memory_order_acquire);
+  info.state = visible(phase);
+  info.units_completed = std::min(units_done_.load(std::memory_order_relaxed), units_total_);
+  if (terminal(phase)) {
+    // A terminal phase is stored only after the record is complete.
+    std::lock_guard<std::mutex> lock(record_mutex_);
+    info.result = result_;
+    info.elapsed_ms = elapsed_ms_;
+    info.bytes_h2d = traffic_.bytes_h2d;
+    info.bytes_d2h = traffic_.bytes_d2h;
+    info.cache_hits = traffic_.cache_hits;
+    info.cache_misses = traffic_.cache_misses;
+    if (phase == XVRAM_OPERATION_COMPLETED) info.units_completed = units_total_;
   }
-  out = info_;
-  return completed ? Error{}
-                   : make_error(XVRAM_STATUS_TIMEOUT, "operation", "wait",
-                                "operation did not finish before the timeout");
+  return info;
+}
+
+bool Operation::settled_within(uint64_t timeout_ms) const {
+  if (timeout_ms == XVRAM_TIMEOUT_INFINITE) {
+    settled_.wait();
+    return true;
+  }
+  // Waits longer than the clock can express are waits without bound.
+  constexpr uint64_t kLongest = uint64_t{1} << 40; // ~35 years
+  if (timeout_ms >= kLongest) {
+    settled_.wait();
+    return true;
+  }
+  return settled_.wait_for(std::chrono::milliseconds(timeout_ms)) == std::future_status::ready;
 }
 
 Error Operation::cancel() {
-  std::lock_guard<std::mutex> lock(mutex_);
-  if (info_.state == XVRAM_OPERATION_QUEUED) {
-    cancel_requested_ = true;
+  uint32_t expected = XVRAM_OPERATION_QUEUED;
+  if (phase_.compare_exchange_strong(expected, kLeavingQueued, std::memory_order_acq_rel)) {
+    publish(XVRAM_OPERATION_CANCELLED,
+            make_error(XVRAM_STATUS_CANCELLED, "operation", "cancel",
+                       "cancelled before the worker started it"),
+            0.0, {});
     return {};
   }
-  if (info_.state == XVRAM_OPERATION_RUNNING)
+  if (visible(expected) == XVRAM_OPERATION_RUNNING)
     return make_error(XVRAM_STATUS_BUSY, "operation", "cancel",
-                      "a running device operation cannot be cancelled safely");
-  return {};
+                      "the operation has device work in flight; wait for it instead");
+  return {}; // already terminal: nothing to cancel
 }
 
-Error Operation::error() const {
-  std::lock_guard<std::mutex> lock(mutex_);
+Error Operation::failure() const {
+  if (!terminal(phase_.load(std::memory_order_acquire))) return {};
+  std::lock_guard<std::mutex> lock(record_mutex_);
   return error_;
 }
 
-bool Operation::begin() {
-  std::lock_guard<std::mutex> lock(mutex_);
-  if (cancel_requested_) {
-    info_.state = XVRAM_OPERATION_CANCELLED;
-    info_.result = XVRAM_STATUS_CANCELLED;
-    error_ = make_error(XVRAM_STATUS_CANCELLED, "operation", "cancel", "operation cancelled");
-    done_.notify_all();
+bool Operation::cancelled() const {
+  return phase_.load(std::memory_order_acquire) == XVRAM_OPERATION_CANCELLED;
+}
+
+bool Operation::claim() {
+  const Clock::time_point now = Clock::now();
+  uint32_t expected = XVRAM_OPERATION_QUEUED;
+  if (deadline_.passed(now)) {
+    if (!phase_.compare_exchange_strong(expected, kLeavingQueued, std::memory_order_acq_rel))
+      return false; // cancelled meanwhile
+    publish(XVRAM_OPERATION_FAILED, deadline_.missed("operation", "queue_deadline"),
+            ms_between(deadline_.submitted(), now), {});
     return false;
   }
-  const auto now = Clock::now();
-  if (deadline_.expired(now)) {
-    info_.state = XVRAM_OPERATION_FAILED;
-    info_.result = XVRAM_STATUS_TIMEOUT;
-    error_ = deadline_.timeout_error("operation", "queue_deadline");
-    info_.elapsed_ms = std::chrono::duration<double, std::milli>(now - deadline_.submitted()).count();
-    done_.notify_all();
-    return false;
-  }
-  info_.state = XVRAM_OPERATION_RUNNING;
   started_ = now;
-  return true;
+  return phase_.compare_exchange_strong(expected, XVRAM_OPERATION_RUNNING,
+                                        std::memory_order_acq_rel);
 }
 
-Error Operation::deadline_error(const char* stage, const char* operation) const {
-  return deadline_.expired() ? deadline_.timeout_error(stage, operation) : Error{};
+Error Operation::deadline_check(const char* stage, const char* where) const {
+  return deadline_.passed() ? deadline_.missed(stage, where) : Error{};
 }
 
-void Operation::finish(const Error& error, const xvram_session_telemetry_v1& before,
-                       const xvram_session_telemetry_v1& after) {
-  std::lock_guard<std::mutex> lock(mutex_);
-  error_ = error;
-  info_.result = error.status;
-  info_.state = error ? XVRAM_OPERATION_FAILED : XVRAM_OPERATION_COMPLETED;
-  if (!error) info_.units_completed = info_.units_total;
-  info_.elapsed_ms = std::chrono::duration<double, std::milli>(Clock::now() - started_).count();
-  info_.bytes_h2d = after.bytes_h2d - before.bytes_h2d;
-  info_.bytes_d2h = after.bytes_d2h - before.bytes_d2h;
-  info_.cache_hits = after.cache_hits - before.cache_hits;
-  info_.cache_misses = after.cache_misses - before.cache_misses;
-  done_.notify_all();
+void Operation::progress(uint64_t units_done) {
+  units_done_.store(std::min(units_done, units_total_), std::memory_order_relaxed);
 }
 
-void Operation::advance(uint64_t completed) {
-  std::lock_guard<std::mutex> lock(mutex_);
-  if (info_.state == XVRAM_OPERATION_RUNNING)
-    info_.units_completed = std::min(completed, info_.units_total);
+void Operation::settle(const Error& result, const OperationTraffic& traffic) {
+  const xvram_operation_state end = result ? XVRAM_OPERATION_FAILED : XVRAM_OPERATION_COMPLETED;
+  phase_.store(kLeavingRunning, std::memory_order_relaxed);
+  publish(end, result, ms_between(started_, Clock::now()), traffic);
+}
+
+void Operation::publish(xvram_operation_state end, const Error& result, double elapsed_ms,
+                        const OperationTraffic& traffic) {
+  {
+    std::lock_guard<std::mutex> lock(record_mutex_);
+    result_ = result.status;
+    error_ = result;
+    elapsed_ms_ = elapsed_ms;
+    traffic_ = traffic;
+  }
+  phase_.store(end, std::memory_order_release);
+  settled_promise_.set_value();
 }
 
 // ---- Session --------------------------------------------------------------
@@ -126,31 +158,43 @@ RuntimeConfig runtime_config(const xvram_session_config_v1& c) {
 } // namespace
 
 Session::Session(const xvram_session_config_v1& config)
-    : config_(config), runtime_(runtime_config(config)) {
-  close_operation_ = std::make_shared<Operation>(0, 1, Deadline{});
-  telemetry_ = xvram_session_telemetry_v1{};
+    : config_(config), runtime_(runtime_config(config)),
+      exited_(exit_promise_.get_future().share()),
+      shutdown_(std::make_shared<Operation>(0, 1, Deadline{})) {
   telemetry_.struct_size = sizeof(telemetry_);
 }
 
-Session::~Session() { (void)close(XVRAM_TIMEOUT_INFINITE); }
-
-Error Session::start() {
+Session::~Session() {
   try {
-    worker_ = std::thread([this]() { worker_main(); });
+    (void)close(XVRAM_TIMEOUT_INFINITE);
   } catch (...) {
-    Error e = exception_error("worker_start");
-    std::lock_guard<std::mutex> lock(queue_mutex_);
-    setup_error_ = e;
-    setup_finished_ = true;
-    worker_exited_ = true;
-    return e;
+    // A destructor cannot report; the runtime's own destructor still frees.
   }
-  std::unique_lock<std::mutex> lock(queue_mutex_);
-  setup_cv_.wait(lock, [&]() { return setup_finished_; });
-  return setup_error_;
 }
 
-void Session::refresh_telemetry() {
+Error Session::start() {
+  std::future<Error> setup = setup_promise_.get_future();
+  try {
+    thread_ = std::thread(&Session::worker, this);
+    worker_started_ = true;
+  } catch (...) {
+    Error e = exception_error("worker_start");
+    std::lock_guard<std::mutex> lock(jobs_mutex_);
+    setup_failed_ = true;
+    setup_error_ = e;
+    exit_promise_.set_value();
+    return e;
+  }
+  Error e = setup.get();
+  if (e) {
+    std::lock_guard<std::mutex> lock(jobs_mutex_);
+    setup_failed_ = true;
+    setup_error_ = e;
+  }
+  return e;
+}
+
+void Session::publish_telemetry() {
   xvram_session_telemetry_v1 t{};
   runtime_.telemetry(t);
   std::lock_guard<std::mutex> lock(telemetry_mutex_);
@@ -175,99 +219,92 @@ Error Session::telemetry_v2(xvram_session_telemetry_v2& out) const {
   return {};
 }
 
-void Session::worker_main() {
+// The worker: set the runtime up (on this thread, which keeps the device
+// current from here on), report the outcome to start(), then run jobs in
+// submission order until the shutdown job, which close() queues last.
+void Session::worker() {
   Error setup;
   try {
     setup = runtime_.setup();
   } catch (...) {
     setup = exception_error("worker_setup");
   }
-  {
-    std::lock_guard<std::mutex> lock(queue_mutex_);
-    setup_error_ = setup;
-    chunk_bytes_ = runtime_.frame_bytes();
-    setup_finished_ = true;
-  }
-  refresh_telemetry();
-  setup_cv_.notify_all();
+  chunk_bytes_ = runtime_.frame_bytes();
+  publish_telemetry();
+  setup_promise_.set_value(setup);
   if (setup) {
     (void)runtime_.close();
-    std::lock_guard<std::mutex> lock(queue_mutex_);
-    worker_exited_ = true;
-    exit_cv_.notify_all();
+    exit_promise_.set_value();
     return;
   }
-  for (;;) {
-    WorkItem item;
+  for (bool running = true; running;) {
+    Job job;
     {
-      std::unique_lock<std::mutex> lock(queue_mutex_);
-      queue_cv_.wait(lock, [&]() { return stop_worker_ || close_requested_ || !queue_.empty(); });
-      if (stop_worker_ && queue_.empty()) break;
-      if (!queue_.empty()) {
-        item = std::move(queue_.front());
-        queue_.pop_front();
-      } else {
-        item = WorkItem{close_operation_, {}, true};
-        close_requested_ = false;
-      }
+      std::unique_lock<std::mutex> lock(jobs_mutex_);
+      jobs_ready_.wait(lock, [this]() { return !jobs_.empty(); });
+      job = std::move(jobs_.front());
+      jobs_.pop_front();
     }
-    if (!item.operation->begin()) continue;
-    xvram_session_telemetry_v1 before{}, after{};
-    runtime_.telemetry(before);
-    Error result;
-    try {
-      result = item.shutdown ? runtime_.close() : item.action(*item.operation);
-    } catch (...) {
-      result = exception_error("worker_action");
-    }
-    runtime_.telemetry(after);
-    refresh_telemetry();
-    item.operation->finish(result, before, after);
-    if (item.shutdown) {
-      std::lock_guard<std::mutex> lock(queue_mutex_);
-      stop_worker_ = true;
-    }
+    running = !job.shutdown;
+    execute(job);
   }
-  std::lock_guard<std::mutex> lock(queue_mutex_);
-  worker_exited_ = true;
-  exit_cv_.notify_all();
+  exit_promise_.set_value();
 }
 
-Error Session::enqueue(Action action, uint64_t units, uint64_t deadline_ms,
-                       std::shared_ptr<Operation>& out, std::shared_ptr<GemmPlanRecord> gemm) {
-  Deadline deadline;
-  if (!Deadline::create(deadline_ms, Clock::now(), deadline))
-    return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "deadline", "submit",
-                      "deadline_ms cannot be represented by the monotonic clock");
-  auto op = std::make_shared<Operation>(next_operation_id_.fetch_add(1), units, deadline);
-  {
-    std::lock_guard<std::mutex> lock(queue_mutex_);
-    if (closing_) return make_error(XVRAM_STATUS_CLOSED, "session", "submit", "session is closing");
-    queue_.push_back(WorkItem{op, std::move(action), false, std::move(gemm)});
+void Session::execute(Job& job) {
+  if (!job.operation->claim()) return;
+  xvram_session_telemetry_v1 before{}, after{};
+  runtime_.telemetry(before);
+  Error result;
+  try {
+    result = job.shutdown ? runtime_.close() : job.body(*job.operation);
+  } catch (...) {
+    result = exception_error(job.shutdown ? "session_shutdown" : "worker_job");
   }
-  queue_cv_.notify_one();
+  runtime_.telemetry(after);
+  publish_telemetry();
+  job.operation->settle(result, OperationTraffic{after.bytes_h2d - before.bytes_h2d,
+                                                 after.bytes_d2h - before.bytes_d2h,
+                                                 after.cache_hits - before.cache_hits,
+                                                 after.cache_misses - before.cache_misses});
+}
+
+Error Session::enqueue(std::function<Error(Operation&)> body, uint64_t units, uint64_t deadline_ms,
+                       std::shared_ptr<Operation>& out, std::shared_ptr<GemmPlanRecord> gemm) {
+  const std::optional<Deadline> deadline = Deadline::after(deadline_ms, Clock::now());
+  if (!deadline) return check_deadline_ms(deadline_ms, "submit");
+  auto op = std::make_shared<Operation>(operation_ids_.fetch_add(1), units, *deadline);
+  {
+    std::lock_guard<std::mutex> lock(jobs_mutex_);
+    if (sealed_ || setup_failed_)
+      return make_error(XVRAM_STATUS_CLOSED, "session", "submit",
+                        "the session is closed or closing; nothing more can be queued");
+    jobs_.push_back(Job{op, std::move(body), std::move(gemm), false});
+  }
+  jobs_ready_.notify_one();
   out = std::move(op);
   return {};
 }
 
-Error Session::invoke_sync(std::function<Error()> action, uint64_t timeout_ms) {
+Error Session::run_on_worker(std::function<Error()> body, uint64_t timeout_ms) {
   std::shared_ptr<Operation> op;
-  if (Error e = enqueue(
-          [action = std::move(action)](Operation& o) -> Error {
-            if (Error d = o.deadline_error("operation", "pre_launch_deadline")) return d;
-            return action();
-          },
-          1, 0, op))
-    return e;
-  xvram_operation_info_v1 info{};
-  if (Error e = op->wait(timeout_ms, info)) return e;
-  return op->error();
+  Error e = enqueue(
+      [body = std::move(body)](Operation& o) -> Error {
+        if (Error d = o.deadline_check("operation", "pre_launch_deadline")) return d;
+        return body();
+      },
+      1, 0, op);
+  if (e) return e;
+  if (!op->settled_within(timeout_ms))
+    return make_error(XVRAM_STATUS_TIMEOUT, "operation", "wait",
+                      "the session worker did not finish the call within the timeout");
+  return op->failure();
 }
 
 Error Session::allocate(const xvram_allocation_desc_v1& desc,
                         std::shared_ptr<AllocationRecord>& out) {
   std::shared_ptr<AllocationRecord> created;
-  Error e = invoke_sync([&]() -> Error {
+  Error e = run_on_worker([&]() -> Error {
     if (desc.alignment_bytes > runtime_.frame_bytes())
       return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "allocation", "alignment",
                         "allocation alignment exceeds the runtime chunk alignment");
@@ -288,15 +325,15 @@ Error Session::allocate(const xvram_allocation_desc_v1& desc,
 }
 
 Error Session::write(AllocationRecord& a, uint64_t offset, const void* src, uint64_t bytes) {
-  return invoke_sync([&]() { return runtime_.write(a.id, offset, src, bytes); });
+  return run_on_worker([&]() { return runtime_.write(a.id, offset, src, bytes); });
 }
 
 Error Session::read(AllocationRecord& a, uint64_t offset, void* dst, uint64_t bytes) {
-  return invoke_sync([&]() { return runtime_.read(a.id, offset, dst, bytes); });
+  return run_on_worker([&]() { return runtime_.read(a.id, offset, dst, bytes); });
 }
 
 Error Session::release(AllocationRecord& a) {
-  return invoke_sync([&]() { return runtime_.release(a.id); });
+  return run_on_worker([&]() { return runtime_.release(a.id); });
 }
 
 // Plan creation (reference RuntimeSession::create_gemm_plan,
@@ -312,7 +349,7 @@ Error Session::create_gemm_plan(const GemmSpec& spec_in, std::shared_ptr<Allocat
     return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "gemm", "create_plan",
                       "GEMM allocation is invalid or released");
   std::shared_ptr<GemmPlanRecord> record;
-  Error e = invoke_sync([&]() -> Error {
+  Error e = run_on_worker([&]() -> Error {
     if (a->released || b->released || c->released || (bias && bias->released))
       return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "gemm", "create_plan",
                         "GEMM allocation was released before planning");
@@ -354,47 +391,46 @@ Error Session::create_gemm_plan(const GemmSpec& spec_in, std::shared_ptr<Allocat
   return {};
 }
 
+// A GEMM operation counts its progress in tiles of the plan's geometry (C
+// tiles x K panels, gemm_plan_info_v1.tile_count), as the reference's does
+// (src/sdk/runtime.cpp:1227): units_completed reaches tile_count on success
+// however many K panels each launch covers.
 Error Session::submit_gemm(const std::shared_ptr<GemmPlanRecord>& plan,
                            std::shared_ptr<Operation>& out) {
-  const uint64_t units = plan->plan.launches.size();
   return enqueue(
       [this, plan](Operation& op) -> Error {
-        if (Error d = op.deadline_error("gemm", "pre_launch_deadline")) return d;
-        if (plan->a->released || plan->b->released || plan->c->released ||
-            (plan->bias && plan->bias->released))
+        if (Error d = op.deadline_check("gemm", "pre_launch_deadline")) return d;
+        if (!plan->operands_live())
           return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "gemm", "execute",
-                            "a GEMM allocation was released");
+                            "an operand allocation of the plan was released");
         GemmHooks hooks;
         hooks.boundary = [&](const char*) -> Error {
-          return op.deadline_error("gemm", "tile_deadline");
+          return op.deadline_check("gemm", "tile_deadline");
         };
-        hooks.progress = [&](uint64_t done, uint64_t) { op.advance(done); };
+        hooks.progress = [&](uint64_t tiles_done, uint64_t) { op.progress(tiles_done); };
         // Operations run one at a time, so the link would idle while this
         // one's last launches and write-backs finish and the next one starts:
         // start the next queued GEMM's first panel fills behind this one's
         // work instead. prefetch_distance = 0 turns this off.
         hooks.tail = [this]() -> Error {
           if (config_.prefetch_distance == 0) return {};
-          const std::shared_ptr<GemmPlanRecord> next = next_queued_gemm();
+          const std::shared_ptr<GemmPlanRecord> next = gemm_queued_next();
           if (!next) return {};
           return carry_gemm_head(runtime_, next->plan, uint64_t{next->plan.lookahead} + 1);
         };
         return execute_gemm(runtime_, plan->plan, op.id(), hooks);
       },
-      units, plan->deadline_ms, out, plan);
+      plan->tile_count(), plan->deadline_ms, out, plan);
 }
 
-std::shared_ptr<GemmPlanRecord> Session::next_queued_gemm() const {
+std::shared_ptr<GemmPlanRecord> Session::gemm_queued_next() const {
   std::shared_ptr<GemmPlanRecord> next;
   {
-    std::lock_guard<std::mutex> lock(queue_mutex_);
-    if (queue_.empty()) return nullptr;
-    next = queue_.front().gemm;
+    std::lock_guard<std::mutex> lock(jobs_mutex_);
+    if (jobs_.empty()) return nullptr;
+    next = jobs_.front().gemm;
   }
-  if (!next || next->a->released || next->b->released || next->c->released ||
-      (next->bias && next->bias->released))
-    return nullptr;
-  return next;
+  return next && next->operands_live() ? next : nullptr;
 }
 
 namespace {
@@ -429,7 +465,7 @@ Error Session::submit_prefetch(std::vector<Access> accesses, uint64_t deadline_m
   if (Error e = convert_accesses(accesses, spans, "prefetch")) return e;
   return enqueue(
       [this, spans = std::move(spans), accesses = std::move(accesses)](Operation& op) -> Error {
-        if (Error d = op.deadline_error("operation", "pre_launch_deadline")) return d;
+        if (Error d = op.deadline_check("operation", "pre_launch_deadline")) return d;
         return runtime_.run_prefetch(spans, op.id());
       },
       1, deadline_ms, out);
@@ -447,14 +483,14 @@ Error Session::submit_transaction(std::vector<Access> accesses, uint64_t workspa
                       "transaction workspace exceeds the session workspace cap");
   std::vector<AccessSpan> spans;
   if (Error e = convert_accesses(accesses, spans, "transaction")) return e;
-  const uint64_t transaction_id = next_transaction_id_.fetch_add(1);
+  const uint64_t transaction_id = transaction_ids_.fetch_add(1);
   return enqueue(
       [this, spans = std::move(spans), accesses = std::move(accesses), workspace_bytes, callback,
        user_data, transaction_id](Operation& op) -> Error {
-        if (Error d = op.deadline_error("operation", "pre_launch_deadline")) return d;
+        if (Error d = op.deadline_check("operation", "pre_launch_deadline")) return d;
         TransactionBody body = [&](const std::vector<ResolvedSpan>& ranges, uint64_t ws_address,
                                    uint64_t ws_bytes, Stream stream, bool& skipped) -> Error {
-          if (Error d = op.deadline_error("operation", "post_residency_deadline")) {
+          if (Error d = op.deadline_check("operation", "post_residency_deadline")) {
             skipped = true;
             return d;
           }
@@ -484,7 +520,7 @@ Error Session::submit_transaction(std::vector<Access> accesses, uint64_t workspa
           e.operation = bounded_text(native.operation);
           e.native_name = bounded_text(native.native_name);
           e.message = bounded_text(native.message);
-          if (e.message.empty()) e.message = "transaction callback failed";
+          if (e.message.empty()) e.message = "the transaction callback returned a failure status";
           return e;
         };
         return runtime_.run_transaction(spans, workspace_bytes, body, op.id());
@@ -499,64 +535,76 @@ Error Session::telemetry(xvram_session_telemetry_v1& out) const {
 }
 
 Error Session::drain(uint64_t timeout_ms) {
-  return invoke_sync([this]() { return runtime_.drain(); }, timeout_ms);
+  return run_on_worker([this]() { return runtime_.drain(); }, timeout_ms);
 }
 
-bool Session::wait_worker_exit(uint64_t timeout_ms) {
-  std::unique_lock<std::mutex> lock(queue_mutex_);
-  const auto exited = [this]() { return worker_exited_; };
-  if (worker_exited_) return true;
-  if (timeout_ms == XVRAM_TIMEOUT_INFINITE) {
-    exit_cv_.wait(lock, exited);
-    return true;
-  }
-  return exit_cv_.wait_for(lock, std::chrono::milliseconds(timeout_ms), exited);
+bool Session::join_worker(uint64_t timeout_ms) {
+  if (!worker_started_) return true;
+  if (timeout_ms != XVRAM_TIMEOUT_INFINITE &&
+      exited_.wait_for(std::chrono::milliseconds(timeout_ms)) != std::future_status::ready)
+    return false;
+  std::call_once(join_once_, [this]() {
+    if (thread_.joinable()) thread_.join();
+  });
+  return true;
 }
 
-// Close (reference RuntimeSession::close, src/sdk/runtime.cpp:637-679): queue
-// a shutdown after the pending work, wait for it, join the worker.
+// Close (reference RuntimeSession::close, src/sdk/runtime.cpp:637-679): the
+// shutdown job is queued once, behind everything already submitted; its
+// operation's result is the close result. A session whose set-up failed has
+// no runtime to close: its worker has already ended.
 Error Session::close(uint64_t timeout_ms) {
-  const auto started = Clock::now();
-  const auto remaining = [&]() -> uint64_t {
+  if (closed()) return {};
+  const Clock::time_point begun = Clock::now();
+  const auto left = [&]() -> uint64_t {
     if (timeout_ms == XVRAM_TIMEOUT_INFINITE) return XVRAM_TIMEOUT_INFINITE;
-    const auto el = std::chrono::duration_cast<std::chrono::milliseconds>(Clock::now() - started);
-    const uint64_t e = el.count() < 0 ? 0 : static_cast<uint64_t>(el.count());
-    return e >= timeout_ms ? 0 : timeout_ms - e;
+    const auto spent = std::chrono::duration_cast<std::chrono::milliseconds>(Clock::now() - begun);
+    const uint64_t used = spent.count() > 0 ? static_cast<uint64_t>(spent.count()) : 0;
+    return used >= timeout_ms ? 0 : timeout_ms - used;
   };
-  Error setup;
-  bool has_worker;
+  bool setup_failed = false;
+  Error setup_error;
   {
-    std::lock_guard<std::mutex> lock(queue_mutex_);
-    has_worker = worker_.joinable();
-    if (!closing_) {
-      if (!setup_error_) close_requested_ = true;
-      closing_ = true;
+    std::lock_guard<std::mutex> lock(jobs_mutex_);
+    setup_failed = setup_failed_;
+    setup_error = setup_error_;
+    if (!setup_failed && !sealed_ && worker_started_) {
+      jobs_.push_back(Job{shutdown_, {}, nullptr, true});
+      jobs_ready_.notify_one();
     }
-    setup = setup_error_;
+    sealed_ = true;
   }
-  queue_cv_.notify_all();
-  if (!has_worker) return {};
-  if (setup) {
-    if (!wait_worker_exit(remaining()))
+  if (!worker_started_) return setup_error;
+  if (setup_failed) {
+    if (!join_worker(left()))
       return make_error(XVRAM_STATUS_TIMEOUT, "session", "close",
-                        "session setup cleanup did not finish before the timeout");
-  } else {
-    xvram_operation_info_v1 info{};
-    if (Error e = close_operation_->wait(remaining(), info)) return e;
-    if (!wait_worker_exit(remaining()))
-      return make_error(XVRAM_STATUS_TIMEOUT, "session", "close",
-                        "worker did not retire after cleanup before the timeout");
+                        "the worker did not finish its failed set-up within the timeout");
+    return setup_error;
   }
-  bool join = false;
-  {
-    std::lock_guard<std::mutex> lock(queue_mutex_);
-    if (!joined_) {
-      joined_ = true;
-      join = true;
-    }
+  if (!shutdown_->settled_within(left()))
+    return make_error(XVRAM_STATUS_TIMEOUT, "session", "close",
+                      "queued work and the runtime teardown did not finish within the timeout");
+  if (!join_worker(left()))
+    return make_error(XVRAM_STATUS_TIMEOUT, "session", "close",
+                      "the worker did not exit within the timeout after the teardown");
+  Error result = shutdown_->failure();
+  if (!result) closed_.store(true, std::memory_order_release);
+  return result;
+}
+
+void Session::note_failure(const Error& error) noexcept {
+  if (!error) return;
+  try {
+    std::lock_guard<std::mutex> lock(failure_mutex_);
+    last_failure_ = error;
+  } catch (...) {
+    // Keeping the previous record is the only option when copying fails.
   }
-  if (join && worker_.joinable()) worker_.join();
-  return setup ? setup : close_operation_->error();
+}
+
+Error Session::last_failure() const {
+  std::lock_guard<std::mutex> lock(failure_mutex_);
+  return last_failure_;
 }
 
 } // namespace xvram

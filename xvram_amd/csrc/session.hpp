@@ -2,17 +2,20 @@
 // session owns the device and executes queued operations in order.
 //
 // Reference counterpart: src/sdk/runtime.cpp (RuntimeOperation :146-279,
-// RuntimeSession :319-1116, RuntimeGemmPlan :1175-1364). Semantics kept: any
-// thread may call; every call that touches the device runs on the worker;
-// submissions return operations with poll/wait/cancel (cancel succeeds only
-// while queued, BUSY while running); deadlines are submission-relative and
-// are sampled at safe boundaries; close drains the queue and tears down.
+// RuntimeSession :319-1116, RuntimeGemmPlan :1175-1364). What callers observe
+// is kept: any thread may call; every call that touches the device runs on the
+// worker; submissions return operations with poll/wait/cancel (a cancel is
+// accepted only before the operation starts, BUSY while it runs); deadlines are
+// submission-relative and are checked when the operation is taken off the
+// queue and at safe launch boundaries; close runs after the queued work and
+// tears the runtime down.
 #pragma once
 
 #include <atomic>
 #include <condition_variable>
 #include <deque>
 #include <functional>
+#include <future>
 #include <memory>
 #include <mutex>
 #include <thread>
@@ -25,31 +28,64 @@ namespace xvram {
 
 class Session;
 
+// Traffic an operation caused, from the runtime counters around its run.
+struct OperationTraffic {
+  uint64_t bytes_h2d = 0, bytes_d2h = 0, cache_hits = 0, cache_misses = 0;
+};
+
+// One submitted unit of work. Its phase is one atomic word that the caller
+// side (snapshot, settled_within, cancel) and the worker side (claim,
+// progress, settle) move with compare-and-swap:
+//
+//   queued --claim--> running --settle--> completed | failed
+//   queued --cancel--> cancelled          (at once: waiters return immediately)
+//   queued --claim, deadline passed--> failed (TIMEOUT)
+//
+// Exactly one of cancel/claim wins a queued operation. The terminal record
+// (result, error, elapsed time, traffic) is written once, by the winner, and
+// then published through a promise; every waiter holds its shared future.
 class Operation {
 public:
   Operation(uint64_t id, uint64_t units_total, Deadline deadline);
 
-  Error poll(xvram_operation_info_v1& out);
-  Error wait(uint64_t timeout_ms, xvram_operation_info_v1& out);
+  // ---- caller side ----
+  xvram_operation_info_v1 snapshot() const;
+  // True once the operation is terminal; waits at most timeout_ms
+  // (XVRAM_TIMEOUT_INFINITE: without bound).
+  bool settled_within(uint64_t timeout_ms) const;
   Error cancel();
-  Error error() const;
+  Error failure() const;
 
-  bool begin();
-  Error deadline_error(const char* stage, const char* operation) const;
-  void finish(const Error& error, const xvram_session_telemetry_v1& before,
-              const xvram_session_telemetry_v1& after);
-  void advance(uint64_t completed);
+  // ---- worker side ----
+  // Moves a queued operation to running. False when it was cancelled or its
+  // deadline had already passed (then it is settled as FAILED/TIMEOUT here).
+  bool claim();
+  // TIMEOUT error naming `stage`/`where` once the deadline has passed.
+  Error deadline_check(const char* stage, const char* where) const;
+  void progress(uint64_t units_done);
+  void settle(const Error& result, const OperationTraffic& traffic);
+  bool cancelled() const;
   uint64_t id() const { return id_; }
 
 private:
-  mutable std::mutex mutex_;
-  std::condition_variable done_;
-  xvram_operation_info_v1 info_{};
-  Error error_;
-  Deadline deadline_;
+  void publish(xvram_operation_state terminal, const Error& result, double elapsed_ms,
+               const OperationTraffic& traffic);
+
+  const uint64_t id_;
+  const uint64_t units_total_;
+  const Deadline deadline_;
+  std::atomic<uint32_t> phase_{XVRAM_OPERATION_QUEUED};
+  std::atomic<uint64_t> units_done_{0};
   Clock::time_point started_{};
-  bool cancel_requested_ = false;
-  uint64_t id_ = 0;
+
+  mutable std::mutex record_mutex_; // guards the terminal record below
+  xvram_status result_ = XVRAM_STATUS_SUCCESS;
+  Error error_;
+  double elapsed_ms_ = 0.0;
+  OperationTraffic traffic_;
+
+  std::promise<void> settled_promise_;
+  std::shared_future<void> settled_;
 };
 
 struct AllocationRecord {
@@ -67,6 +103,11 @@ struct GemmPlanRecord {
   std::shared_ptr<AllocationRecord> a, b, c;
   std::shared_ptr<AllocationRecord> bias; // fused-epilogue bias vector, if any
   uint64_t deadline_ms = 0;
+  // Tiles of the plan's geometry: C tiles x K panels (progress units).
+  uint64_t tile_count() const { return plan.tiles_m * plan.tiles_n * plan.panels_k; }
+  bool operands_live() const {
+    return !a->released && !b->released && !c->released && !(bias && bias->released);
+  }
 };
 
 class Session : public std::enable_shared_from_this<Session> {
@@ -74,6 +115,7 @@ public:
   explicit Session(const xvram_session_config_v1& config);
   ~Session();
 
+  // Starts the worker and waits for the runtime set-up it runs.
   Error start();
   uint64_t chunk_size_bytes() const { return chunk_bytes_; }
   const xvram_session_config_v1& config() const { return config_; }
@@ -106,48 +148,60 @@ public:
   Error telemetry(xvram_session_telemetry_v1& out) const;
   Error telemetry_v2(xvram_session_telemetry_v2& out) const;
   Error drain(uint64_t timeout_ms);
+  // Runs after the work already queued; a second call after a successful
+  // close returns success at once.
   Error close(uint64_t timeout_ms);
+  bool closed() const { return closed_.load(std::memory_order_acquire); }
+
+  // The last failure any ABI call on this session reported (session_get_error).
+  void note_failure(const Error& error) noexcept;
+  Error last_failure() const;
 
 private:
-  using Action = std::function<Error(Operation&)>;
-  struct WorkItem {
+  // A queued unit of work. `gemm` names the plan of a GEMM execution, so the
+  // operation running ahead of it can start its first fills (carry).
+  struct Job {
     std::shared_ptr<Operation> operation;
-    Action action;
+    std::function<Error(Operation&)> body;
+    std::shared_ptr<GemmPlanRecord> gemm;
     bool shutdown = false;
-    std::shared_ptr<GemmPlanRecord> gemm; // set for a GEMM execution
   };
 
-  Error enqueue(Action action, uint64_t units, uint64_t deadline_ms,
-                std::shared_ptr<Operation>& out,
-                std::shared_ptr<GemmPlanRecord> gemm = nullptr);
-  // The plan of the GEMM queued next, if the next queued item is one whose
-  // allocations are all live.
-  std::shared_ptr<GemmPlanRecord> next_queued_gemm() const;
-  Error invoke_sync(std::function<Error()> action, uint64_t timeout_ms = XVRAM_TIMEOUT_INFINITE);
-  void worker_main();
-  void refresh_telemetry();
-  bool wait_worker_exit(uint64_t timeout_ms);
+  Error enqueue(std::function<Error(Operation&)> body, uint64_t units, uint64_t deadline_ms,
+                std::shared_ptr<Operation>& out, std::shared_ptr<GemmPlanRecord> gemm = nullptr);
+  // Runs `body` on the worker as an operation of one unit and waits for it.
+  Error run_on_worker(std::function<Error()> body, uint64_t timeout_ms = XVRAM_TIMEOUT_INFINITE);
+  // The plan of the job queued first, if it is a GEMM whose operands are live.
+  std::shared_ptr<GemmPlanRecord> gemm_queued_next() const;
+  void worker();
+  void execute(Job& job);
+  void publish_telemetry();
+  bool join_worker(uint64_t timeout_ms);
 
   xvram_session_config_v1 config_{};
   Runtime runtime_;
   uint64_t chunk_bytes_ = 0;
 
-  std::thread worker_;
-  mutable std::mutex queue_mutex_;
-  std::condition_variable queue_cv_;
-  std::condition_variable setup_cv_;
-  std::condition_variable exit_cv_;
-  std::deque<WorkItem> queue_;
-  bool setup_finished_ = false;
-  bool stop_worker_ = false;
-  bool worker_exited_ = false;
-  bool closing_ = false;
-  bool close_requested_ = false;
-  bool joined_ = false;
+  std::thread thread_;
+  std::promise<Error> setup_promise_;
+  std::promise<void> exit_promise_;
+  std::shared_future<void> exited_;
+  std::once_flag join_once_;
+  bool worker_started_ = false; // written by start(), before the session is shared
+
+  mutable std::mutex jobs_mutex_;
+  std::condition_variable jobs_ready_;
+  std::deque<Job> jobs_;
+  bool sealed_ = false;          // no more jobs; the shutdown job is queued
+  bool setup_failed_ = false;
   Error setup_error_;
-  std::shared_ptr<Operation> close_operation_;
-  std::atomic<uint64_t> next_operation_id_{1};
-  std::atomic<uint64_t> next_transaction_id_{1};
+  std::shared_ptr<Operation> shutdown_;
+  std::atomic<bool> closed_{false};
+  std::atomic<uint64_t> operation_ids_{1};
+  std::atomic<uint64_t> transaction_ids_{1};
+
+  mutable std::mutex failure_mutex_;
+  Error last_failure_;
 
   mutable std::mutex telemetry_mutex_;
   xvram_session_telemetry_v1 telemetry_{};
