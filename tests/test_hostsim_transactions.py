@@ -362,6 +362,38 @@ def test_duration_guard_on_gemm_kernels(sim, oracle_mod):
         plan.release()
 
 
+def test_host_stall_between_dispatches_does_not_trip_the_guard(sim):
+    """A tile kernel without a start event inherits its start from the event
+    its lane last recorded (the previous kernel's stop, or the operation's
+    start marker). When the host itself stalls before a dispatch with no fill
+    to wait for (here: one event record sleeps 100 ms on the host, at each
+    record of a repeated, fully cached 96 x 40 x 96 GEMM in turn), the lane
+    may have idled meanwhile: the kernel then takes a real start event, so the
+    idle time is not counted as kernel time and a 50 ms guard does not trip.
+    (The record after the operation's start marker on lane 0 is such a stall:
+    lane 0's first kernel would otherwise inherit that marker.)"""
+    sim.dll.xvram_hostsim_delay.argtypes = [ctypes.c_int, ctypes.c_long, ctypes.c_int]
+    site_event_record = 12
+    m, n = 96, 40
+    for skip in range(0, 24):
+        sim.dll.xvram_hostsim_reset()
+        with xv.Session(sim, chunk_size_bytes=16 * KiB, cache_target_bytes=32 * 16 * KiB,
+                        workspace_cap_bytes=0, device_headroom_bytes=0,
+                        max_transaction_ms=50) as s:
+            a, b, c = s.allocation(m * m * 4), s.allocation(m * n * 4), s.allocation(m * n * 4)
+            a.write(np.ones(m * m, np.float32))
+            b.write(np.ones(m * n, np.float32))
+            plan = xv.GemmPlan(s, xv.matrix(a, m, m, m), xv.matrix(b, m, n, m),
+                               xv.matrix(c, m, n, m))
+            plan.execute()
+            assert sim.dll.xvram_hostsim_delay(site_event_record, skip, 100) == 0
+            plan.execute()
+            t = s.telemetry()
+            assert t.watchdog_rejections == 0 and t.last_transaction_ms < 50, skip
+            assert np.array_equal(c.read(dtype=np.float32), np.full(m * n, m, np.float32))
+            plan.release()
+
+
 @pytest.mark.parametrize("max_ms,split", [(0, False), (1, True)])
 def test_planner_keeps_launches_under_the_guard(sim, max_ms, split):
     """Plans are sized against max_transaction_ms (at a deliberately low assumed

@@ -295,6 +295,69 @@ def test_failed_operation_keeps_earlier_outputs(sim):
         p3.release()
 
 
+def failing_repeat(s, A, B, C, big):
+    """Runs the same product again under a 5 ms deadline; returns the failed
+    operation's info, or skips when the deadline expired before any launch."""
+    p = xv.GemmPlan(s, xv.matrix(A, big, big, big), xv.matrix(B, big, big, big),
+                    xv.matrix(C, big, big, big), deadline_ms=5)
+    op = p.submit()
+    st, info = op.wait()
+    assert st == abi.SUCCESS and info.result == abi.TIMEOUT
+    where = op.error().operation.decode()
+    op.release()
+    p.release()
+    if where != "tile_deadline":
+        pytest.skip(f"the deadline expired at {where}, before any launch")
+    assert 0 < info.units_completed < 8
+    return info
+
+
+@pytest.mark.parametrize("drained", [False, True], ids=["unwritten", "written_back"])
+def test_failed_repeat_of_a_gemm(sim, drained):
+    """The same GEMM run twice, the second run failing part way: C tiles the
+    failed run rewrote while they still held the first run's unwritten results
+    (the resident pattern: C stays cached and dirty) hold neither result.
+    Those bytes are reported lost: reading them, or a GEMM reading them,
+    fails with CORRUPTION until the caller writes them again. When the first
+    results had been written back (drain) before, nothing is lost: C reads
+    back as the first run's result."""
+    big = 512
+    a_h, b_h = ints(big, big, 26), ints(big, big, 27)
+    # 24 frames: the four 256 x 256 C tiles form one block and all stay
+    # cached, dirty, after the first run (fewer frames, and the second run
+    # writes them back before it starts, as its schedule needs the frames).
+    with session(sim, frame=256 * KiB, frames=24) as s:
+        A, B, C = put(s, a_h), put(s, b_h), s.allocation(big * big * 4)
+        p1 = xv.GemmPlan(s, xv.matrix(A, big, big, big), xv.matrix(B, big, big, big),
+                         xv.matrix(C, big, big, big))
+        run(p1)
+        if drained:
+            s.drain()
+        failing_repeat(s, A, B, C, big)
+        if drained:
+            np.testing.assert_array_equal(get(C, big, big), a_h @ b_h)
+            p1.release()
+            return
+        with pytest.raises(xv.XvramError) as e:
+            C.read()
+        assert e.value.status == abi.CORRUPTION
+        # A GEMM that reads C (beta = 1) cannot load the lost bytes either.
+        p3 = xv.GemmPlan(s, xv.matrix(A, big, big, big), xv.matrix(B, big, big, big),
+                         xv.matrix(C, big, big, big), beta=1.0)
+        op = p3.submit()
+        st, info = op.wait()
+        assert info.result == abi.CORRUPTION
+        op.release()
+        # Rewriting C makes it whole; the same GEMM then runs as before.
+        C.write(np.zeros(big * big, np.float32))
+        np.testing.assert_array_equal(get(C, big, big), np.zeros((big, big), np.float32))
+        run(p3)
+        np.testing.assert_array_equal(get(C, big, big), a_h @ b_h)
+        assert s.telemetry().poisoned == 0
+        p1.release()
+        p3.release()
+
+
 def test_background_flush_bounds_idle_dirty_frames(sim):
     """Outputs of earlier operations may not crowd the pool: once more than
     half of it is idle and dirty, the least recently used half of those are

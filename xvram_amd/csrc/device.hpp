@@ -23,6 +23,10 @@ namespace xvram {
 using Stream = void*;
 using Event = void*;
 
+// event_query's answer for work that has not completed yet (error codes are
+// positive).
+constexpr int kNotReady = -1;
+
 // What a device reports about itself (for reports and diagnostics).
 struct DeviceInfo {
   std::string name;
@@ -60,15 +64,15 @@ public:
   virtual int host_alloc(uint64_t bytes, void** pointer) = 0; // pinned
   virtual int host_free(void* pointer) = 0;
 
+  // There are no blocking waits here: the runtime polls event_query against
+  // its stall deadline, so no wait on device work is unbounded.
   virtual int stream_create(Stream* stream) = 0;
   virtual int stream_destroy(Stream stream) = 0;
-  virtual int stream_sync(Stream stream) = 0;
   virtual int event_create(Event* event) = 0;
   virtual int event_destroy(Event event) = 0;
   virtual int event_record(Event event, Stream stream) = 0;
-  // 0 = complete, 1 = not ready, otherwise an error code.
+  // 0 = complete, kNotReady = still pending, otherwise an error code.
   virtual int event_query(Event event) = 0;
-  virtual int event_sync(Event event) = 0;
   virtual int event_elapsed_ms(float* ms, Event start, Event stop) = 0;
   virtual int stream_wait_event(Stream stream, Event event) = 0;
 

@@ -103,9 +103,6 @@ public:
   int stream_destroy(Stream stream) override {
     return hipStreamDestroy(static_cast<hipStream_t>(stream));
   }
-  int stream_sync(Stream stream) override {
-    return hipStreamSynchronize(static_cast<hipStream_t>(stream));
-  }
   int event_create(Event* event) override {
     hipEvent_t ev = nullptr;
     const hipError_t e = hipEventCreateWithFlags(&ev, hipEventDefault);
@@ -119,11 +116,8 @@ public:
   int event_query(Event event) override {
     const hipError_t e = hipEventQuery(static_cast<hipEvent_t>(event));
     if (e == hipSuccess) return 0;
-    if (e == hipErrorNotReady) return 1;
+    if (e == hipErrorNotReady) return kNotReady;
     return e;
-  }
-  int event_sync(Event event) override {
-    return hipEventSynchronize(static_cast<hipEvent_t>(event));
   }
   int event_elapsed_ms(float* ms, Event start, Event stop) override {
     return hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop));

@@ -21,7 +21,9 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <set>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "device.hpp"
@@ -33,7 +35,12 @@ namespace {
 enum Site {
   kInit, kMemInfo, kVaReserve, kVaFree, kMemCreate, kMemRelease, kMemMap, kMemUnmap, kSetAccess,
   kHostAlloc, kStreamCreate, kEventCreate, kEventRecord, kEventQuery, kEventSync, kCopyH2D,
-  kCopyD2H, kLaunch, kSiteCount
+  kCopyD2H, kLaunch,
+  // Not a failure: once this site "fails", the event being recorded never
+  // completes (event_query keeps answering kNotReady), as if the work queued
+  // before it on its stream hung. Persistent: every later record hangs too.
+  kEventHang,
+  kSiteCount
 };
 
 constexpr int kSimFault = 9001;      // injected failure
@@ -43,6 +50,8 @@ constexpr int kSimOutOfMemory = 2;   // same value as hipErrorOutOfMemory
 struct Injection {
   long skip = -1; // calls to let through before failing; -1 = disabled
   bool persistent = false;
+  long delay_skip = -1; // calls to let through before one call sleeps; -1 = none
+  int delay_ms = 0;
 };
 
 struct SimState {
@@ -57,6 +66,16 @@ struct SimState {
 } g_sim;
 
 int fault(Site site) {
+  int sleep_ms = 0;
+  {
+    std::lock_guard<std::mutex> lock(g_sim.mutex);
+    Injection& inj = g_sim.sites[site];
+    if (inj.delay_skip == 0) sleep_ms = inj.delay_ms;
+    if (inj.delay_skip >= 0) --inj.delay_skip;
+  }
+  // A slow host call (a descheduled thread, a slow driver call): the host
+  // time passes, the simulated device stays idle.
+  if (sleep_ms > 0) std::this_thread::sleep_for(std::chrono::milliseconds(sleep_ms));
   std::lock_guard<std::mutex> lock(g_sim.mutex);
   Injection& inj = g_sim.sites[site];
   if (inj.skip < 0) return 0;
@@ -182,7 +201,6 @@ public:
     return 0;
   }
   int stream_destroy(Stream) override { return 0; }
-  int stream_sync(Stream) override { return 0; }
   int event_create(Event* event) override {
     if (int f = fault(kEventCreate)) return f;
     *event = reinterpret_cast<Event>(++next_object_);
@@ -192,10 +210,14 @@ public:
   int event_record(Event event, Stream) override {
     if (int f = fault(kEventRecord)) return f;
     recorded_[event] = std::chrono::steady_clock::now();
+    if (fault(kEventHang)) hung_.insert(event);
+    else hung_.erase(event);
     return 0;
   }
-  int event_query(Event) override { return fault(kEventQuery); }
-  int event_sync(Event) override { return fault(kEventSync); }
+  int event_query(Event event) override {
+    if (int f = fault(kEventQuery)) return f;
+    return hung_.count(event) ? kNotReady : 0;
+  }
   int event_elapsed_ms(float* ms, Event start, Event stop) override {
     auto a = recorded_.find(start), b = recorded_.find(stop);
     if (a == recorded_.end() || b == recorded_.end()) return kSimBadAccess;
@@ -334,6 +356,7 @@ private:
   std::map<uint64_t, uint64_t> handles_;
   std::map<uint64_t, Mapping> mappings_;
   std::map<Event, std::chrono::steady_clock::time_point> recorded_;
+  std::set<Event> hung_; // recorded while kEventHang fired: never complete
   uint64_t next_handle_ = 0;
   uint64_t next_object_ = 0x1000;
 };
@@ -372,6 +395,18 @@ extern "C" __attribute__((visibility("default"))) int xvram_hostsim_inject(int s
   std::lock_guard<std::mutex> lock(g_sim.mutex);
   g_sim.sites[site].skip = skip;
   g_sim.sites[site].persistent = persistent != 0;
+  return 0;
+}
+
+// After `skip` more calls at `site`, the next one sleeps `ms` on the host
+// before it runs (the call itself succeeds).
+extern "C" __attribute__((visibility("default"))) int xvram_hostsim_delay(int site, long skip,
+                                                                          int ms) {
+  using namespace xvram;
+  if (site < 0 || site >= kSiteCount || skip < 0 || ms < 0) return -1;
+  std::lock_guard<std::mutex> lock(g_sim.mutex);
+  g_sim.sites[site].delay_skip = skip;
+  g_sim.sites[site].delay_ms = ms;
   return 0;
 }
 

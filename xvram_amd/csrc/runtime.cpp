@@ -63,6 +63,14 @@ bool keys_overlap(const PanelKey& a, const PanelKey& b) {
   return false;
 }
 
+// Host time between two dispatches on one compute lane after which the second
+// kernel takes a start event of its own (Runtime::record_kernel): far below
+// any duration-guard limit. A host that keeps ahead of short kernels
+// dispatches them well within it; where the host waits longer between
+// dispatches, the kernels it waits for are long and a start event (~5 us of
+// device time) is small next to them.
+constexpr std::chrono::milliseconds kStartEventAfterHostGap{2};
+
 Runtime::Runtime(RuntimeConfig config) : config_(config), device_(make_device()) {
   if (const char* path = std::getenv("XVRAM_TRACE_FILE"); path != nullptr && *path != '\0')
     trace_path_ = path;
@@ -86,6 +94,46 @@ Error Runtime::poison(std::string_view stage, std::string_view operation,
   poisoned_ = true;
   t_.poisoned = 1;
   return make_error(XVRAM_STATUS_POISONED, stage, operation, message);
+}
+
+// Polls rather than blocks (hipEventSynchronize has no time limit): yields for
+// the first millisecond, then sleeps between queries.
+Error Runtime::await_event(Event event, std::string_view stage, std::string_view operation) {
+  if (quarantined_)
+    return make_error(XVRAM_STATUS_POISONED, stage, operation,
+                      "device work of this session is quarantined after a stalled or failed wait");
+  const Clock::time_point begun = Clock::now();
+  const Clock::time_point give_up = begun + std::chrono::milliseconds(config_.stall_timeout_ms);
+  for (;;) {
+    const int q = device_->event_query(event);
+    if (q == 0) return {};
+    if (q != kNotReady) {
+      quarantined_ = true;
+      return device_failure(q, stage, operation);
+    }
+    const Clock::time_point now = Clock::now();
+    if (now >= give_up) {
+      quarantined_ = true;
+      Error e = poison(stage, operation,
+                       "device work did not complete within the stall deadline; the frames, "
+                       "workspace and host buffers it may still use are quarantined");
+      e.status = XVRAM_STATUS_TIMEOUT;
+      return e;
+    }
+    if (now - begun < std::chrono::milliseconds(1)) std::this_thread::yield();
+    else std::this_thread::sleep_for(std::chrono::microseconds(20));
+  }
+}
+
+Error Runtime::await_stream(Stream stream, std::string_view stage, std::string_view operation) {
+  if (quarantined_)
+    return make_error(XVRAM_STATUS_POISONED, stage, operation,
+                      "device work of this session is quarantined after a stalled or failed wait");
+  if (int rc = device_->event_record(sync_marker_, stream)) {
+    quarantined_ = true;
+    return device_failure(rc, stage, operation);
+  }
+  return await_event(sync_marker_, stage, operation);
 }
 
 // Session setup (reference src/residency/runtime.cpp:212-596): bind the
@@ -151,6 +199,7 @@ Error Runtime::setup() {
   if (int rc = device_->event_create(&op_start_)) return device_failure(rc, "setup", "event");
   if (int rc = device_->event_create(&op_start2_)) return device_failure(rc, "setup", "event");
   if (int rc = device_->event_create(&carry_fence_)) return device_failure(rc, "setup", "event");
+  if (int rc = device_->event_create(&sync_marker_)) return device_failure(rc, "setup", "event");
   t_.flags = XVRAM_TELEMETRY_NO_PHYSICAL_ALIASES | XVRAM_TELEMETRY_STABLE_VIRTUAL_ADDRESSES;
   setup_done_ = true;
   return {};
@@ -164,7 +213,7 @@ Error Runtime::drain() {
   if (!poisoned_)
     if (Error e = flush_all()) return e;
   for (Stream s : {h2d_, compute_, compute2_, d2h_})
-    if (int rc = device_->stream_sync(s)) return device_failure(rc, "drain", "stream_sync");
+    if (Error e = await_stream(s, "drain", "stream_wait")) return e;
   writebacks_settled();
   return {};
 }
@@ -179,7 +228,7 @@ Error Runtime::flush_all() {
     issued = true;
   }
   if (issued) {
-    if (int rc = device_->stream_sync(d2h_)) return device_failure(rc, "cache", "stream_sync");
+    if (Error e = await_stream(d2h_, "cache", "writeback_wait")) return e;
     writebacks_settled();
   }
   return {};
@@ -216,8 +265,11 @@ Error Runtime::close() {
   for (Frame& f : frames_) f.pins = 0;
   if (!poisoned_)
     if (Error e = flush_all(); e && !first) first = e;
-  for (Stream s : {h2d_, compute_, compute2_, d2h_})
-    if (s) note(device_->stream_sync(s), "stream_sync");
+  for (Stream s : {h2d_, compute_, compute2_, d2h_}) {
+    if (quarantined_) break;
+    if (Error e = await_stream(s, "close", "stream_wait"); e && !first) first = e;
+  }
+  if (quarantined_) return abandon_device_resources();
   for (Frame& f : frames_) {
     if (f.keyed) {
       index_.erase(f.key);
@@ -255,10 +307,10 @@ Error Runtime::close() {
   carried_events_.clear();
   carried_trace_.clear();
   pending_writebacks_.clear();
-  if (op_start_) device_->event_destroy(op_start_);
-  if (op_start2_) device_->event_destroy(op_start2_);
-  if (carry_fence_) device_->event_destroy(carry_fence_);
-  op_start_ = op_start2_ = carry_fence_ = nullptr;
+  for (Event* e : {&op_start_, &op_start2_, &carry_fence_, &sync_marker_}) {
+    if (*e) device_->event_destroy(*e);
+    *e = nullptr;
+  }
   for (Stream s : {h2d_, compute_, compute2_, d2h_})
     if (s) device_->stream_destroy(s);
   compute_ = compute2_ = h2d_ = d2h_ = nullptr;
@@ -269,6 +321,39 @@ Error Runtime::close() {
   allocations_.clear();
   t_.resident_bytes = 0;
   return first;
+}
+
+// Teardown of a quarantined runtime (reference runtime.cpp:1575-1595,
+// 1745-1760, and the SDK's abandon at sdk/runtime.cpp:900-915): device work
+// whose completion was never observed may still read or write the frames, the
+// workspace and the pinned host buffers, so none of them is unmapped,
+// released or freed, and the streams and events stay alive. They are given up
+// until the process ends; the cache index and the allocation table are
+// dropped, so nothing in this session reaches them again. Close reports
+// CLEANUP_FAILED.
+Error Runtime::abandon_device_resources() {
+  uint64_t mapped = 0;
+  for (Frame& f : frames_) {
+    if (f.mapped_at) ++mapped;
+    if (f.keyed) index_.erase(f.key);
+    f.keyed = false;
+  }
+  frames_.clear();
+  allocations_.clear();
+  event_pool_.clear();
+  events_in_use_.clear();
+  carried_events_.clear();
+  carried_trace_.clear();
+  pending_writebacks_.clear();
+  compute_ = compute2_ = h2d_ = d2h_ = nullptr;
+  op_start_ = op_start2_ = carry_fence_ = sync_marker_ = nullptr;
+  workspace_va_ = 0;
+  arena_ = 0;
+  t_.resident_bytes = 0;
+  return make_error(XVRAM_STATUS_CLEANUP_FAILED, "close", "quarantine",
+                    "device work of this session never completed; " + std::to_string(mapped) +
+                        " mapped frames, the workspace and the pinned host buffers were "
+                        "abandoned instead of released");
 }
 
 // ---- allocations -----------------------------------------------------------
@@ -348,6 +433,9 @@ Error Runtime::release(uint64_t id) {
   device_->host_free(a->host);
   pinned_bytes_ -= a->bytes;
   allocations_.erase(id);
+  lost_.erase(std::remove_if(lost_.begin(), lost_.end(),
+                             [id](const PanelKey& k) { return k.allocation_id == id; }),
+              lost_.end());
   return {};
 }
 
@@ -362,6 +450,16 @@ Error Runtime::write(uint64_t id, uint64_t offset, const void* source, uint64_t 
   // Cached entries overlapping the range become stale: drop them first.
   if (Error e = invalidate(id, offset, end)) return e;
   parallel_copy(a->host + offset, source, bytes);
+  if (bytes > 0 && !lost_.empty()) {
+    PanelKey range;
+    range.allocation_id = id;
+    range.offset = offset;
+    range.width = bytes;
+    range.height = 1;
+    range.pitch = bytes;
+    range.kind = EntryKind::chunk;
+    forget_lost_within(range);
+  }
   return {};
 }
 
@@ -393,9 +491,10 @@ Error Runtime::read(uint64_t id, uint64_t offset, void* destination, uint64_t by
       issued = true;
     }
     if (issued) {
-      if (int rc = device_->stream_sync(d2h_)) return device_failure(rc, "allocation", "stream_sync");
+      if (Error e = await_stream(d2h_, "allocation", "writeback_wait")) return e;
       writebacks_settled();
     }
+    if (Error e = check_not_lost(range, "allocation", "read")) return e;
   }
   parallel_copy(destination, a->host + offset, bytes);
   return {};
@@ -500,17 +599,18 @@ Error Runtime::wait_retired(Frame& f) {
   if (!f.retire_pending) return {};
   ++t_.event_boundaries;
   const int q = device_->event_query(f.retire_ref);
-  if (q == 1) {
+  if (q == kNotReady) {
     time_intervals(false); // the host is about to wait anyway
-    if (int rc = device_->event_sync(f.retire_ref)) return device_failure(rc, "cache", "event_sync");
+    if (Error e = await_event(f.retire_ref, "cache", "retire_wait")) return e;
   } else if (q != 0) {
+    quarantined_ = true;
     return device_failure(q, "cache", "event_query");
   }
   // The other compute lane's last use may finish later than retire_ref.
   for (int lane = 0; lane < kLanes; ++lane) {
     if (!f.lane_pending[lane]) continue;
     if (f.lane_ref[lane] != f.retire_ref)
-      if (int rc = device_->event_sync(f.lane_ref[lane])) return device_failure(rc, "cache", "event_sync");
+      if (Error e = await_event(f.lane_ref[lane], "cache", "retire_wait")) return e;
     f.lane_pending[lane] = false;
   }
   f.retire_pending = false;
@@ -527,6 +627,7 @@ Error Runtime::evict_key(Frame& f, bool was_dirty) {
   f.keyed = false;
   f.dirty = false;
   f.unwritten = false;
+  f.overwrote_unflushed = false;
   f.ready_pending = false;
   t_.resident_bytes -= frame_bytes_;
   if (was_dirty) ++t_.dirty_evictions;
@@ -745,6 +846,8 @@ Error Runtime::acquire(const PanelKey& key, uint64_t packed_pitch, bool needs_da
     }
   }
   if (Error e = flush_overlapping(key, nullptr)) return e;
+  if (needs_data)
+    if (Error e = check_not_lost(key, "cache", "fill")) return e;
   Frame* f = nullptr;
   if (Error e = select_frame(f)) return e;
   if (Error e = map_frame_at(*f, f->slot)) return abandon_mapping(*f, e);
@@ -772,6 +875,7 @@ Error Runtime::carry_fill(const PanelKey& key, uint64_t packed_pitch, bool& issu
     if (keys_overlap(written, key)) return {};
   for (const Frame& f : frames_)
     if (f.keyed && f.dirty && keys_overlap(f.key, key)) return {};
+  if (check_not_lost(key, "cache", "carry")) return {}; // its own operation reports it
   if (!carry_active_) {
     if (int rc = device_->event_record(carry_fence_, h2d_)) return device_failure(rc, "cache", "record");
     carry_active_ = true;
@@ -803,6 +907,7 @@ Error Runtime::acquire_pieces(const PanelKey& key, uint64_t packed_pitch,
   if (covered != key.bytes())
     return make_error(XVRAM_STATUS_INTERNAL, "cache", "acquire", "pieces do not tile the panel");
   if (Error e = flush_overlapping(key, nullptr)) return e;
+  if (Error e = check_not_lost(key, "cache", "fill")) return e;
   Frame* f = nullptr;
   if (Error e = select_frame(f)) return e;
   if (Error e = map_frame_at(*f, f->slot)) return abandon_mapping(*f, e);
@@ -865,6 +970,7 @@ Error Runtime::unpin(Frame& f, bool dirty) {
   }
   f.last_use = ++tick_;
   if (!dirty) return {};
+  if (f.dirty && f.dirty_serial != op_serial_) f.overwrote_unflushed = true;
   f.dirty = true;
   f.unwritten = false;
   f.dirty_serial = op_serial_;
@@ -923,7 +1029,9 @@ Error Runtime::writeback(Frame& f, bool evict) {
   // retire event (the copy) gates any reuse.
   move(f, EntryState::resident_clean);
   f.dirty = false;
+  f.overwrote_unflushed = false;
   const PanelKey written = f.key;
+  forget_lost_within(written); // these bytes are whole again once the copy lands
   pending_writebacks_[written] = iv.stop;
   t_.bytes_d2h += written.bytes();
   ++t_.writebacks_completed;
@@ -977,7 +1085,7 @@ Error Runtime::invalidate(uint64_t allocation_id, uint64_t begin, uint64_t end) 
       return make_error(XVRAM_STATUS_BUSY, "cache", "invalidate", "entry is in use by an operation");
     if (f.dirty) {
       if (Error e = writeback_and_evict(f)) return e;
-      if (int rc = device_->stream_sync(d2h_)) return device_failure(rc, "cache", "stream_sync");
+      if (Error e = await_stream(d2h_, "cache", "writeback_wait")) return e;
       writebacks_settled();
     } else {
       if (Error e = wait_retired(f)) return e;
@@ -988,14 +1096,47 @@ Error Runtime::invalidate(uint64_t allocation_id, uint64_t begin, uint64_t end) 
   return {};
 }
 
+// A failed operation drops what it wrote: the host copy stays authoritative.
+// Entries it rewrote while they still held an earlier operation's unwritten
+// results lose those results too; their rectangles are recorded as lost.
 void Runtime::discard_dirty() {
   for (Frame& f : frames_) {
     f.pins = 0;
     if (f.keyed && ((f.dirty && f.dirty_serial == op_serial_) || f.unwritten)) {
+      if (f.dirty && f.overwrote_unflushed) lost_.push_back(f.key);
       f.dirty = false;
       (void)evict_key(f, false);
     }
   }
+}
+
+Error Runtime::check_not_lost(const PanelKey& range, const char* stage,
+                              const char* operation) const {
+  for (const PanelKey& k : lost_)
+    if (keys_overlap(k, range))
+      return make_error(XVRAM_STATUS_CORRUPTION, stage, operation,
+                        "these bytes held results of an earlier operation that a failed "
+                        "operation overwrote before they were written back; write them again");
+  return {};
+}
+
+// Lost rectangles that lie inside `rewritten` (same allocation) are whole
+// again: a contiguous rewrite covers every line of a rectangle inside its
+// byte range; a rectangle rewrite covers one with the same pitch whose lines
+// and columns lie inside it.
+void Runtime::forget_lost_within(const PanelKey& rewritten) {
+  const auto inside = [&](const PanelKey& k) {
+    if (k.allocation_id != rewritten.allocation_id) return false;
+    if (rewritten.height == 1)
+      return k.offset >= rewritten.offset && k.end() <= rewritten.offset + rewritten.width;
+    if (k.pitch != rewritten.pitch || rewritten.pitch == 0) return k == rewritten;
+    const uint64_t P = rewritten.pitch;
+    const uint64_t r0 = rewritten.offset / P, c0 = rewritten.offset % P;
+    const uint64_t kr = k.offset / P, kc = k.offset % P;
+    return kr >= r0 && kr + k.height <= r0 + rewritten.height && kc >= c0 &&
+           kc + k.width <= c0 + rewritten.width;
+  };
+  lost_.erase(std::remove_if(lost_.begin(), lost_.end(), inside), lost_.end());
 }
 
 // ---- transactions and prefetch -----------------------------------------------
@@ -1167,6 +1308,8 @@ Error Runtime::acquire_chunk(ChunkUse& use) {
     return {};
   }
   if (Error e = flush_overlapping(key, nullptr)) return e;
+  if (use.needs_data)
+    if (Error e = check_not_lost(key, "transaction", "fill")) return e;
   const uint64_t address = a->va + key.offset;
   Frame* f = nullptr;
   for (uint64_t i = 0; i < capacity_; ++i) {
@@ -1415,7 +1558,9 @@ Error Runtime::begin_operation() {
   // from op_start_ (a carried fill or a copy issued before op_start_ was
   // processed times as negative). Each compute lane records its own start.
   if (int rc = device_->event_record(op_start_, compute_)) return device_failure(rc, "operation", "record");
+  lane_dispatched_at_[0] = Clock::now();
   if (int rc = device_->event_record(op_start2_, compute2_)) return device_failure(rc, "operation", "record");
+  lane_dispatched_at_[1] = Clock::now();
   lane_last_[0] = op_start_;
   lane_last_[1] = op_start2_;
   lane_waited_[0] = lane_waited_[1] = false;
@@ -1429,7 +1574,10 @@ Error Runtime::record_kernel(TraceInterval& iv, int lane) {
     return make_error(XVRAM_STATUS_INTERNAL, "gemm", "launch", "no such compute lane");
   iv.start = iv.start_ref = nullptr;
   iv.deps.clear();
-  if (lane_waited_[lane]) {
+  const Clock::time_point now = Clock::now();
+  const bool host_gap = now - lane_dispatched_at_[lane] > kStartEventAfterHostGap;
+  lane_dispatched_at_[lane] = now;
+  if (lane_waited_[lane] || host_gap) {
     if (Error e = take_event(iv.start)) return e;
   } else {
     iv.start_ref = lane_last_[lane];
@@ -1503,14 +1651,13 @@ Error Runtime::finish_operation(uint64_t operation_id) {
   const double enqueued_ms = host_ms(); // everything is enqueued: the host waits from here
   Error first;
   for (Stream s : {compute_, compute2_, d2h_}) {
-    if (int rc = device_->stream_sync(s)) {
-      if (!first) first = device_failure(rc, "operation", "stream_sync");
-    }
+    if (Error e = await_stream(s, "operation", "stream_wait"); e && !first) first = e;
   }
   // This operation's own fills end at the carry fence; carried fills run on.
-  if (int rc = carry_active_ ? device_->event_sync(carry_fence_) : device_->stream_sync(h2d_)) {
-    if (!first) first = device_failure(rc, "operation", "stream_sync");
-  }
+  if (Error e = carry_active_ ? await_event(carry_fence_, "operation", "fill_wait")
+                              : await_stream(h2d_, "operation", "stream_wait");
+      e && !first)
+    first = e;
   const bool carrying = carry_active_ && !first;
   for (Frame& f : frames_) {
     if (carrying && f.carry_serial == op_serial_) continue; // still filling for the next one

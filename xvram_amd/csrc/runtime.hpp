@@ -61,6 +61,11 @@ struct RuntimeConfig {
   uint32_t cache_policy = XVRAM_CACHE_POLICY_CLOCK;
   uint64_t max_transaction_ms = 250;
   uint64_t budget_poll_ms = 100;
+  // How long the host waits for any one piece of device work (an event or a
+  // stream's queue) before it gives up on it: then the session is poisoned
+  // and its device resources quarantined (reference RuntimeConfig
+  // stall_timeout, src/residency/runtime.hpp:65).
+  uint64_t stall_timeout_ms = 5000;
 };
 
 struct HostAllocation {
@@ -153,6 +158,10 @@ struct Frame {
   // contents are garbage until the consumer writes them (dropped if the
   // operation fails first).
   bool unwritten = false;
+  // The operation that last wrote the entry overwrote results an earlier
+  // operation had left in it, not yet written back. If that operation fails,
+  // neither result survives: the bytes are recorded as lost.
+  bool overwrote_unflushed = false;
   // Stop event of a write-back still in flight that left the entry cached: a
   // later writer of the frame must not overtake the copy.
   Event writeback_done = nullptr;
@@ -246,6 +255,7 @@ public:
   uint64_t granularity() const { return granularity_; }
   const RuntimeConfig& config() const { return config_; }
   bool poisoned() const { return poisoned_; }
+  bool quarantined() const { return quarantined_; }
   static constexpr int kLanes = 2;
   Stream compute_stream(int lane = 0) const { return lane == 0 ? compute_ : compute2_; }
 
@@ -354,6 +364,13 @@ public:
   uint64_t host_stored_peak_bytes() const { return pinned_peak_bytes_; }
 
   Error device_failure(int code, std::string_view stage, std::string_view operation);
+  // Bounded waits: poll until the event (or everything queued on the stream
+  // so far) completes, at most stall_timeout_ms; past that, or on a device
+  // error, the runtime is quarantined and the call fails (TIMEOUT / the
+  // device error).
+  Error await_event(Event event, std::string_view stage, std::string_view operation);
+  Error await_stream(Stream stream, std::string_view stage, std::string_view operation);
+  Error abandon_device_resources();
   Error poison(std::string_view stage, std::string_view operation, std::string_view message);
 
   bool tracing() const { return !trace_path_.empty(); }
@@ -414,6 +431,19 @@ private:
   bool setup_done_ = false;
   bool closed_ = false;
   bool poisoned_ = false;
+  // Device work whose completion the host could not observe (a wait ran past
+  // the stall deadline or a query failed) may still use frames, the
+  // workspace and the pinned host buffers: close then abandons them.
+  bool quarantined_ = false;
+  // Rectangles whose latest results were lost: a failed operation rewrote
+  // entries that held an earlier operation's unwritten results, and dropped
+  // them. Reading those bytes (allocation_read, a fill) fails with
+  // CORRUPTION until the caller writes them again or a later operation's
+  // write-back covers them.
+  std::vector<PanelKey> lost_;
+  Error check_not_lost(const PanelKey& range, const char* stage, const char* operation) const;
+  void forget_lost_within(const PanelKey& rewritten);
+  Event sync_marker_ = nullptr; // recorded on a stream to wait for its queue
   bool launches_blocked_ = false;
 
   uint64_t granularity_ = 0;
@@ -451,6 +481,12 @@ private:
   bool op_start_seen_ = false; // op_start_ and op_start2_ have completed (intervals can be timed)
   Event lane_last_[2] = {nullptr, nullptr}; // last kernel stop per lane (its start event at first)
   bool lane_waited_[2] = {false, false};    // a wait without a stamp since lane_last_
+  // Host clock at each lane's last dispatch (or the operation's start). A
+  // lane the host left alone for longer than kStartEventAfterHostGap may have
+  // drained and idled, so its next kernel takes a real start event instead
+  // of inheriting the previous stop (an idle gap would otherwise count as
+  // kernel time under the duration guard).
+  Clock::time_point lane_dispatched_at_[2]{};
   std::vector<Event> lane_deps_[2];         // stamps of the waits since lane_last_
   bool guard_tripped_ = false; // a kernel or callback of the operation exceeded the guard
   std::vector<Event> event_pool_;

@@ -2,6 +2,7 @@
 #include "session.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace xvram {
 
@@ -152,6 +153,14 @@ RuntimeConfig runtime_config(const xvram_session_config_v1& c) {
   r.cache_policy = c.cache_policy;
   r.max_transaction_ms = c.max_transaction_ms == 0 ? 250 : c.max_transaction_ms;
   r.budget_poll_ms = c.budget_poll_ms;
+  // The session config has no stall deadline field (the reference's SDK
+  // uses its runtime default, 5 s); XVRAM_STALL_TIMEOUT_MS overrides it for
+  // the whole process.
+  if (const char* text = std::getenv("XVRAM_STALL_TIMEOUT_MS"); text != nullptr && *text) {
+    char* end = nullptr;
+    const unsigned long long ms = std::strtoull(text, &end, 10);
+    if (end != text && *end == '\0' && ms > 0) r.stall_timeout_ms = ms;
+  }
   return r;
 }
 
