@@ -75,6 +75,12 @@ for _s, _frame in ((4096, 64 * MiB), (8192, 256 * MiB), (16384, 1024 * MiB)):
         WORKLOADS[f"resident_{_s}_{'nt'[_oa]}{'nt'[_ob]}"] = (
             _s, _s, _s, _oa, _ob, 0, _frame,
             f"FP32 SGEMM {'NT'[_oa]}/{'NT'[_ob]} {_s}^3, fully resident (one launch)")
+# One config-5 layer with its weights resident (Y^T = W X^T as the chain's
+# T/N launch: 16384 x 256 x 16384, 1 GiB frames): 64 tiles of 256 x 256, so the
+# launch splits K into 4 ranges (a single round of 256 workgroups).
+WORKLOADS["resident_c5_layer_tn"] = (
+    16384, 256, 16384, OP_T, OP_N, 0, 1024 * MiB,
+    "FP32 SGEMM T/N 16384 x 256 x 16384 (one config-5 layer, weights resident; split K)")
 DEFAULT = "ns65536_nt_16g"
 # Config 5: 8 x [Y = ReLU(X W^T + b)], X 256 x 16384 ~ N(0,1), W 16384 x 16384 and
 # b ~ N(0, 1/16384), 2 GiB budget of 64 MiB frames; one step = one 8-layer forward.

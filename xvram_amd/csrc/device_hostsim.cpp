@@ -60,6 +60,8 @@ struct SimState {
   uint64_t free_bytes = 16ull << 30;
   uint64_t total_bytes = 16ull << 30;
   uint64_t kernel_launches = 0;
+  uint64_t split_launches = 0; // launches that split K (kernels::split_k_plan)
+  int last_splits = 0;         // K ranges of the last split launch
   int device_count = 1;       // simulated devices 0 .. device_count-1
   int current_device = 0;     // what the calling thread sees as current (-1: none)
   int last_init_ordinal = -1; // the device the last session set up on
@@ -279,14 +281,33 @@ public:
     if ((l.bias_row && !accessible(reinterpret_cast<uint64_t>(l.bias_row), l.m * 4ull)) ||
         (l.bias_col && !accessible(reinterpret_cast<uint64_t>(l.bias_col), l.n * 4ull)))
       return kSimBadAccess;
+    // A split launch writes its partials to the workspace (sgemm_launch.hpp).
+    const kernels::SplitK sk = two ? kernels::SplitK{} : kernels::split_k_plan(l);
+    const int64_t mn = int64_t{l.m} * l.n;
+    if (sk.splits > 1 && !accessible(reinterpret_cast<uint64_t>(l.workspace),
+                                     static_cast<uint64_t>(sk.splits * mn * 4)))
+      return kSimBadAccess;
     // Events attached to the dispatch are stamped around the kernel itself.
     if (l.start_event) recorded_[l.start_event] = std::chrono::steady_clock::now();
     // Column by column; each element accumulates its K products in order
-    // (p ascending, the second panel after the first), in FP32.
+    // (p ascending, the second panel after the first), in FP32. A split
+    // launch accumulates each K range into its partial, then adds the
+    // partials in range order.
     std::vector<float> acc(static_cast<size_t>(l.m));
     for (int64_t j = 0; j < l.n; ++j) {
       std::fill(acc.begin(), acc.end(), 0.f);
-      for (int64_t p = 0; p < k1; ++p) {
+      for (int s = 0; s < sk.splits && sk.splits > 1; ++s) {
+        float* part = l.workspace + s * mn + j * l.m;
+        std::fill(part, part + l.m, 0.f);
+        const int64_t p_end = std::min<int64_t>(l.k, int64_t{s + 1} * sk.depth);
+        for (int64_t p = int64_t{s} * sk.depth; p < p_end; ++p) {
+          const float y = l.b_ncontig ? l.b[j + p * l.ldb] : l.b[p + j * l.ldb];
+          for (int64_t i = 0; i < l.m; ++i)
+            part[i] += (l.a_kcontig ? l.a[p + i * l.lda] : l.a[i + p * l.lda]) * y;
+        }
+        for (int64_t i = 0; i < l.m; ++i) acc[i] = s == 0 ? part[i] : acc[i] + part[i];
+      }
+      for (int64_t p = 0; p < k1 && sk.splits == 1; ++p) {
         const float y = l.b_ncontig ? l.b[j + p * l.ldb] : l.b[p + j * l.ldb];
         for (int64_t i = 0; i < l.m; ++i) {
           const float x = l.a_kcontig ? l.a[p + i * l.lda] : l.a[i + p * l.lda];
@@ -312,6 +333,10 @@ public:
     if (l.stop_event) recorded_[l.stop_event] = std::chrono::steady_clock::now();
     std::lock_guard<std::mutex> lock(g_sim.mutex);
     ++g_sim.kernel_launches;
+    if (sk.splits > 1) {
+      ++g_sim.split_launches;
+      g_sim.last_splits = sk.splits;
+    }
     return 0;
   }
 
@@ -416,6 +441,8 @@ extern "C" __attribute__((visibility("default"))) void xvram_hostsim_reset() {
   for (auto& s : g_sim.sites) s = Injection{};
   g_sim.free_bytes = g_sim.total_bytes = 16ull << 30;
   g_sim.kernel_launches = 0;
+  g_sim.split_launches = 0;
+  g_sim.last_splits = 0;
   g_sim.device_count = 1;
   g_sim.current_device = 0;
   g_sim.last_init_ordinal = -1;
@@ -444,6 +471,16 @@ extern "C" __attribute__((visibility("default"))) void xvram_hostsim_set_memory(
   std::lock_guard<std::mutex> lock(g_sim.mutex);
   g_sim.free_bytes = free_b;
   g_sim.total_bytes = total_b;
+}
+
+// Launches that split K since the last reset; *last_splits = the K ranges of
+// the last one.
+extern "C" __attribute__((visibility("default"))) uint64_t xvram_hostsim_split_launches(
+    int* last_splits) {
+  using namespace xvram;
+  std::lock_guard<std::mutex> lock(g_sim.mutex);
+  if (last_splits != nullptr) *last_splits = g_sim.last_splits;
+  return g_sim.split_launches;
 }
 
 extern "C" __attribute__((visibility("default"))) uint64_t xvram_hostsim_kernel_launches() {

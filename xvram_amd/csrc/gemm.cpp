@@ -316,7 +316,7 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   if (bias && p.bias_length() * 4 > frame_bytes)
     return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "gemm", "make_plan",
                       "working_set_too_large: the bias vector exceeds one cache frame");
-  const uint64_t frame_count = total_frames - (bias && total_frames > 0 ? 1 : 0);
+  uint64_t frame_count = total_frames - (bias && total_frames > 0 ? 1 : 0);
   if (frame_count < 3)
     return make_error(XVRAM_STATUS_BUDGET_PRESSURE, "gemm", "make_plan",
                       "working_set_too_large: fewer than three cache frames");
@@ -413,6 +413,14 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   out.tiles_m = ceil_div(p.m, tm);
   out.tiles_n = ceil_div(p.n, tn);
   out.panels_k = ceil_div(p.k, bk);
+  // A launch of fewer 256 x 256 tiles than CUs splits its K, its partials in
+  // one frame of the pool (kernels::split_k_shape for the plan's tile and
+  // panel): that frame is taken from the schedule's.
+  out.scratch = frame_count >= 4 &&
+                kernels::split_k_shape(static_cast<int64_t>(tm), static_cast<int64_t>(tn),
+                                       static_cast<int64_t>(bk), !p.a.transposed && p.b.transposed,
+                                       F).splits > 1;
+  if (out.scratch) --frame_count;
 
   // Lookahead: launches whose panels are acquired (and pinned) before they are
   // enqueued, so copies run ahead of compute. At most 3 frames per one-panel
@@ -485,7 +493,8 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   out.d2h_bytes_planned = c_bytes;
   // The block's C tiles, one pass's A and B panels and the launches acquired
   // ahead (and the bias frame).
-  out.frames_in_use = std::min<uint64_t>(total_frames, best.need + (bias ? 1 : 0));
+  out.frames_in_use =
+      std::min<uint64_t>(total_frames, best.need + (bias ? 1 : 0) + (out.scratch ? 1 : 0));
 
   // Launch order: blocks in a serpentine; K passes (groups of `panels` K
   // panels, fixed boundaries) alternate direction from block to block so the
@@ -499,7 +508,9 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
       total > 100000000ull)
     return make_error(XVRAM_STATUS_INVALID_ARGUMENT, "gemm", "make_plan", "too_many_tiles");
   out.launches.reserve(total);
-  out.lanes = panels * one_panel_flops <= kDualLaneMaxFlops ? 2 : 1;
+  // A split launch fills the chip by itself, and its partials' frame serves
+  // one launch at a time: one lane.
+  out.lanes = !out.scratch && panels * one_panel_flops <= kDualLaneMaxFlops ? 2 : 1;
   uint64_t block_seq = 0;
   for (uint64_t bi = 0; bi < blocks_m; ++bi) {
     for (uint64_t s = 0; s < blocks_n; ++s, ++block_seq) {
@@ -654,6 +665,21 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
       return e;
     }
   }
+
+  // Split launches keep their partials in one frame taken for the operation.
+  Frame* scratch = nullptr;
+  if (plan.scratch) {
+    if (Error e = rt.take_scratch(scratch)) {
+      if (bias) (void)rt.release_after(*bias, rt.compute_stream(), false);
+      (void)rt.finish_operation(operation_id);
+      return e;
+    }
+  }
+  const auto release_scratch = [&]() -> Error {
+    Frame* f = scratch;
+    scratch = nullptr;
+    return f ? rt.release_scratch(*f) : Error{};
+  };
 
   // Unpins what an acquisition already holds (its launch never runs).
   const auto drop = [&](Acquired& acq) {
@@ -813,6 +839,10 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
       k.k = static_cast<int>(kp.depth);
       k.alpha = p.alpha;
       k.beta = (n == 0 && l.first_panel) ? p.beta : 1.f;
+      if (scratch) {
+        k.workspace = reinterpret_cast<float*>(scratch->address);
+        k.workspace_bytes = rt.frame_bytes();
+      }
       k.a_kcontig = p.a.transposed;
       k.b_ncontig = p.b.transposed;
       k.padded = true;
@@ -877,6 +907,7 @@ Error execute_gemm(Runtime& rt, const GemmPlanData& plan, uint64_t operation_id,
     }
   }
   if (bias && !result) result = rt.release_after_lanes(*bias);
+  if (Error e = release_scratch(); e && !result) result = e;
   if (!result && hooks.tail) result = hooks.tail();
   if (result) {
     // Unpin what was acquired ahead, drop partial C panels, drain the device.

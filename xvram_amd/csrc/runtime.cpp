@@ -962,6 +962,25 @@ Error Runtime::release_after_lanes(Frame& f) {
   return unpin(f, false);
 }
 
+Error Runtime::take_scratch(Frame*& out) {
+  if (poisoned_) return make_error(XVRAM_STATUS_POISONED, "cache", "scratch", "session is poisoned");
+  Frame* f = nullptr;
+  if (Error e = select_frame(f)) return e;
+  if (Error e = map_frame_at(*f, f->slot)) return abandon_mapping(*f, e);
+  move(*f, EntryState::resident_clean);
+  f->pins = 1;
+  f->last_use = ++tick_;
+  out = f;
+  return {};
+}
+
+Error Runtime::release_scratch(Frame& f) {
+  if (Error e = release_after_lanes(f)) return e;
+  move(f, EntryState::evicting);
+  if (!f.retire_pending) move(f, EntryState::host_clean);
+  return {};
+}
+
 Error Runtime::unpin(Frame& f, bool dirty) {
   --f.pins;
   if (dirty && f.state != EntryState::resident_dirty) {

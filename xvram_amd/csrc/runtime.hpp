@@ -293,6 +293,12 @@ public:
   // Unpins after work enqueued on both compute lanes (a frame every launch of
   // an operation reads, such as a bias vector).
   Error release_after_lanes(Frame& frame);
+  // A frame of the pool as a kernel workspace for the current operation
+  // (split-K partials): not a cache entry (never filled, never written back),
+  // mapped at its arena slot and pinned until release_scratch, which retires
+  // it after the last kernel of either compute lane.
+  Error take_scratch(Frame*& out);
+  Error release_scratch(Frame& frame);
   // Writes a dirty entry back to its host bytes (D2H stream, ordered after the
   // frame's last consumer). With `evict` the entry then leaves the cache (and
   // clean entries overlapping the written bytes are dropped); otherwise it

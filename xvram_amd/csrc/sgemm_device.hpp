@@ -28,6 +28,12 @@ struct Params {
   const float* a2;
   const float* b2;
   int k_split;
+  // Split K (ring kernels only): splits > 1 cuts K into ranges of
+  // split_depth; blockIdx.x covers tiles x splits and each workgroup stores
+  // its range's raw sums to partial + split * m * n (column-major, ld = m).
+  int splits;
+  int split_depth;
+  float* partial;
 };
 
 __device__ __forceinline__ float4 zero4() { return make_float4(0.f, 0.f, 0.f, 0.f); }
@@ -66,6 +72,57 @@ __device__ __forceinline__ void tile_coords(const Params& p, int& tm, int& tn) {
   const int in_group = id - group * span;
   tm = first_m + in_group % rows;
   tn = in_group / rows;
+}
+
+// Split-K launches: workgroup -> (tile_m, tile_n), returning its K range
+// index. Ids are remapped per XCD as in tile_coords; the ids of one range are
+// consecutive, so each XCD works on whole ranges and keeps their A and B
+// K-slices in its own L2.
+template <int kGroupM>
+__device__ __forceinline__ int split_coords(const Params& p, int& tm, int& tn) {
+  const int tiles = p.tiles_m * p.tiles_n;
+  const int total = tiles * p.splits;
+  int id = blockIdx.x;
+  constexpr int kXcds = 8;
+  if ((total % kXcds) == 0) {
+    const int per = total / kXcds;
+    id = (id % kXcds) * per + id / kXcds;
+  }
+  const int split = id / tiles;
+  id -= split * tiles;
+  const int span = kGroupM * p.tiles_n;
+  const int group = id / span;
+  const int first_m = group * kGroupM;
+  const int rows = min(p.tiles_m - first_m, kGroupM);
+  const int in_group = id - group * span;
+  tm = first_m + in_group % rows;
+  tn = in_group / rows;
+  return split;
+}
+
+// The launch parameters of K range `split` of a split launch: operand bases
+// moved to the range's first k (k-contiguous operands by k elements, the
+// others by k lines), K = the range's depth.
+__device__ __forceinline__ void narrow_to_split(Params& p, int split, bool a_kcontig,
+                                                bool b_kcontig) {
+  const int k0 = split * p.split_depth;
+  p.a += a_kcontig ? (int64_t)k0 : (int64_t)k0 * p.lda;
+  p.b += b_kcontig ? (int64_t)k0 : (int64_t)k0 * p.ldb;
+  p.k = min(p.split_depth, p.k - k0);
+}
+
+// Where a workgroup of a split launch stores its raw sums: its range's
+// partial (ld = m) with alpha 1, beta 0 and no epilogue (1 * x is exact).
+__device__ __forceinline__ Params partial_target(const Params& p, int split) {
+  Params o = p;
+  o.c = p.partial + (int64_t)split * p.m * p.n;
+  o.ldc = p.m;
+  o.alpha = 1.f;
+  o.beta = 0.f;
+  o.bias_row = nullptr;
+  o.bias_col = nullptr;
+  o.relu = 0;
+  return o;
 }
 
 // Writes one wave's accumulators: acc[i][j] holds MFMA block (row block i,

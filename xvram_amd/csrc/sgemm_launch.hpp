@@ -21,6 +21,16 @@
 // spanning less than 2^31 bytes from its base (two_panel_valid below);
 // anything else returns hipErrorInvalidValue.
 //
+// Split K (optional, workspace set): a launch whose C has fewer 256 x 256
+// tiles than the chip has CUs (m and n multiples of 256, K a multiple of 4
+// for N/T and of 8 for the other forms, one K panel) may cut its K into
+// ranges (split_k_plan below), one workgroup per tile and range; each stores
+// the raw partial sums of its range to the workspace (`splits` dense m x n
+// column-major matrices), and a second kernel adds them in range order and
+// applies alpha, beta and the epilogue. The order of the additions is fixed,
+// so C is the same from run to run. Without a workspace large enough for two
+// partials the launch runs unsplit.
+//
 // start_event / stop_event (hipEvent_t, optional) are recorded by the dispatch
 // itself (hipExtLaunchKernelGGL): no separate marker packets run between
 // kernels, and stop_event completes when the kernel does, so it can serve as
@@ -51,7 +61,57 @@ struct SgemmLaunch {
   int k_split = 0;
   void* start_event = nullptr;
   void* stop_event = nullptr;
+  float* workspace = nullptr; // split-K partials (16-byte aligned), nullptr = none
+  uint64_t workspace_bytes = 0;
 };
+
+// MI355X: 256 compute units; a launch with fewer tiles than this leaves CUs
+// idle unless its K is split.
+constexpr int64_t kComputeUnits = 256;
+// K per workgroup of a split launch, at least (a range this deep keeps the
+// ring kernels' prologue and the partial's store small next to its MFMA work).
+constexpr int64_t kSplitMinDepth = 256;
+
+struct SplitK {
+  int splits = 1; // 1 = not split
+  int depth = 0;  // K per range (multiple of 32); the last range holds the rest
+};
+
+// The split of an m x n x k launch of form `nt` (A op N, B op T) or not,
+// given a workspace of `workspace_bytes` (see "Split K" above): as many ranges
+// as fill one workgroup per CU, each at least kSplitMinDepth deep, at most as
+// many partials as the workspace holds.
+inline SplitK split_k_shape(int64_t m, int64_t n, int64_t k, bool nt, uint64_t workspace_bytes) {
+  if (m <= 0 || n <= 0 || k <= 0 || m % 256 != 0 || n % 256 != 0 || k % (nt ? 4 : 8) != 0)
+    return {};
+  const int64_t tiles = (m / 256) * (n / 256);
+  if (tiles >= kComputeUnits) return {};
+  const int64_t partial = m * n * 4;
+  int64_t s = kComputeUnits / tiles;
+  if (k / kSplitMinDepth < s) s = k / kSplitMinDepth;
+  if (static_cast<int64_t>(workspace_bytes / partial) < s)
+    s = static_cast<int64_t>(workspace_bytes / partial);
+  if (s < 2) return {};
+  const int64_t depth = (k + s - 1) / s;
+  const int64_t depth32 = (depth + 31) / 32 * 32;
+  const int64_t splits = (k + depth32 - 1) / depth32;
+  if (splits < 2) return {};
+  return SplitK{static_cast<int>(splits), static_cast<int>(depth32)};
+}
+
+// The split of one launch: split_k_shape, for a one-panel launch with a
+// 16-byte aligned workspace whose operand panels each span less than 2^31
+// bytes (the ring kernels' 32-bit buffer offsets).
+inline SplitK split_k_plan(const SgemmLaunch& l) {
+  constexpr int64_t kLimit = int64_t(1) << 31;
+  if (l.workspace == nullptr || l.a2 != nullptr || l.b2 != nullptr ||
+      reinterpret_cast<uintptr_t>(l.workspace) % 16 != 0)
+    return {};
+  const int64_t a_bytes = (l.a_kcontig ? int64_t{l.m} : int64_t{l.k}) * l.lda * 4;
+  const int64_t b_bytes = (l.b_ncontig ? int64_t{l.k} : int64_t{l.n}) * l.ldb * 4;
+  if (a_bytes >= kLimit || b_bytes >= kLimit) return {};
+  return split_k_shape(l.m, l.n, l.k, !l.a_kcontig && l.b_ncontig, l.workspace_bytes);
+}
 
 // Enqueues the launch on `stream` (a hipStream_t); returns a hipError_t.
 int launch_sgemm(const SgemmLaunch& launch, void* stream);

@@ -323,6 +323,9 @@ int launch_sgemm(const SgemmLaunch& launch, void* stream) {
   p.a2 = launch.a2;
   p.b2 = launch.b2;
   p.k_split = launch.k_split;
+  p.splits = 1;
+  p.split_depth = 0;
+  p.partial = nullptr;
   auto* s = static_cast<hipStream_t>(stream);
   auto* e0 = static_cast<hipEvent_t>(launch.start_event);
   auto* e1 = static_cast<hipEvent_t>(launch.stop_event);
@@ -334,6 +337,16 @@ int launch_sgemm(const SgemmLaunch& launch, void* stream) {
     return static_cast<int>(launch_wide(p, launch.a_kcontig, launch.b_ncontig, s, e0, e1));
   }
   p.k_split = 0;
+  // Fewer tiles than CUs: split K when a workspace is given (fixed-order
+  // reduction; sgemm_launch.hpp).
+  if (const SplitK sk = split_k_plan(launch); sk.splits > 1) {
+    p.tiles_m = launch.m / wide_tile();
+    p.tiles_n = launch.n / wide_tile();
+    p.splits = sk.splits;
+    p.split_depth = sk.depth;
+    p.partial = launch.workspace;
+    return static_cast<int>(launch_wide(p, launch.a_kcontig, launch.b_ncontig, s, e0, e1));
+  }
   if (wide_fits(launch)) {
     p.tiles_m = (launch.m + wide_tile() - 1) / wide_tile();
     p.tiles_n = (launch.n + wide_tile() - 1) / wide_tile();

@@ -405,8 +405,13 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float lds[4 * kRing * kSlot];
   asm volatile("; accumulators in AGPRs" ::: "a0");
 
-  int tile_m, tile_n;
-  tile_coords<kGroupM>(p, tile_m, tile_n);
+  int tile_m, tile_n, split = 0;
+  if (!kTwo && p.splits > 1) {
+    split = split_coords<kGroupM>(p, tile_m, tile_n);
+    narrow_to_split(p, split, false, false); // A op N, B op T: K runs along lines
+  } else {
+    tile_coords<kGroupM>(p, tile_m, tile_n);
+  }
   const int m0 = tile_m * kTile;
   const int n0 = tile_n * kTile;
   const int tid = threadIdx.x;
@@ -567,8 +572,10 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
     }(std::make_integer_sequence<int, kRing>{});
   }
 
-  // Every tile is interior: two columns of C per batch of loads.
-  store_c_interior<4, 2, true>(p, acc, m0 + wm, n0 + wn, lrow, lhalf);
+  // Every tile is interior: two columns of C per batch of loads. A split
+  // launch stores its range's raw sums instead.
+  const Params out = (!kTwo && p.splits > 1) ? partial_target(p, split) : p;
+  store_c_interior<4, 2, true>(out, acc, m0 + wm, n0 + wn, lrow, lhalf);
 }
 
 // ---- barrier-free kernel for layouts with a k-contiguous operand ------------
@@ -629,8 +636,13 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring8_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float lds[4 * kRing8 * 2 * kHalf8];
   asm volatile("; accumulators in AGPRs" ::: "a0");
 
-  int tile_m, tile_n;
-  tile_coords<kGroupM>(p, tile_m, tile_n);
+  int tile_m, tile_n, split = 0;
+  if (!kTwo && p.splits > 1) {
+    split = split_coords<kGroupM>(p, tile_m, tile_n);
+    narrow_to_split(p, split, kAKC, kBKC);
+  } else {
+    tile_coords<kGroupM>(p, tile_m, tile_n);
+  }
   const int m0 = tile_m * kTile;
   const int n0 = tile_n * kTile;
   const int tid = threadIdx.x;
@@ -795,7 +807,53 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring8_kernel(Params p) {
   // value computed before the loop were hoisted above it and spilled.
   int lane_e;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_e));
-  store_c_interior<4, 2, true>(p, acc, m0 + wm, n0 + wn, lane_e & 31, lane_e >> 5);
+  const Params out = (!kTwo && p.splits > 1) ? partial_target(p, split) : p;
+  store_c_interior<4, 2, true>(out, acc, m0 + wm, n0 + wn, lane_e & 31, lane_e >> 5);
+}
+
+// ---- split-K reduction --------------------------------------------------------
+//
+// C = alpha * (P_0 + P_1 + ... + P_{S-1}) + beta * C, + bias, ReLU: the
+// partials of a split launch added in range order (fixed, so C is the same
+// from run to run), then the same epilogue arithmetic as store_c_interior.
+// One thread per four consecutive rows of one column (m is a multiple of
+// 256): the partials and C are read and written as 16-byte vectors, the
+// threads of a wave covering 256 consecutive floats of a column.
+__global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(Params p) {
+  const int64_t quads = (int64_t)(p.m / 4) * p.n;
+  const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (idx >= quads) return;
+  const int col = (int)(idx / (p.m / 4));
+  const int row = (int)(idx - (int64_t)col * (p.m / 4)) * 4;
+  const int64_t stride = (int64_t)p.m * p.n;
+  const float* part = p.partial + (int64_t)col * p.m + row;
+  float4 sum = *reinterpret_cast<const float4*>(part);
+  for (int s = 1; s < p.splits; ++s) {
+    const float4 v = *reinterpret_cast<const float4*>(part + s * stride);
+    sum.x += v.x;
+    sum.y += v.y;
+    sum.z += v.z;
+    sum.w += v.w;
+  }
+  float* cp = p.c + (int64_t)col * p.ldc + row;
+  float r[4] = {p.alpha * sum.x, p.alpha * sum.y, p.alpha * sum.z, p.alpha * sum.w};
+  if (p.beta != 0.f) {
+    const float4 old = *reinterpret_cast<const float4*>(cp);
+    r[0] = p.alpha * sum.x + p.beta * old.x;
+    r[1] = p.alpha * sum.y + p.beta * old.y;
+    r[2] = p.alpha * sum.z + p.beta * old.z;
+    r[3] = p.alpha * sum.w + p.beta * old.w;
+  }
+  if (p.bias_row != nullptr || p.bias_col != nullptr || p.relu != 0) {
+    const float bias_c = p.bias_col != nullptr ? p.bias_col[col] : 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (p.bias_row != nullptr) r[t] += p.bias_row[row + t];
+      r[t] += bias_c;
+      if (p.relu != 0 && r[t] < 0.f) r[t] = 0.f;
+    }
+  }
+  *reinterpret_cast<float4*>(cp) = make_float4(r[0], r[1], r[2], r[3]);
 }
 
 } // namespace
@@ -810,8 +868,27 @@ int wide_tile() { return kTile; }
 // the dispatch itself.
 hipError_t launch_wide(const Params& p, bool a_kcontig, bool b_ncontig, hipStream_t stream,
                        hipEvent_t start, hipEvent_t stop) {
-  const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
   const dim3 block(kThreads);
+  if (p.splits > 1) {
+    // Split K (the caller has checked split_k_plan's conditions): the ring
+    // kernel over tiles x ranges into the partials, then the reduction; the
+    // start event rides on the first dispatch, the stop event on the second.
+    const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n * p.splits));
+    if (!a_kcontig && b_ncontig)
+      hipExtLaunchKernelGGL(sgemm_ring_kernel<false>, grid, block, 0, stream, start, nullptr, 0, p);
+    else if (!a_kcontig && !b_ncontig)
+      hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, false>), grid, block, 0, stream, start, nullptr, 0, p);
+    else if (a_kcontig && !b_ncontig)
+      hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, false>), grid, block, 0, stream, start, nullptr, 0, p);
+    else
+      hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, false>), grid, block, 0, stream, start, nullptr, 0, p);
+    if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    const int64_t quads = (int64_t)(p.m / 4) * p.n;
+    const dim3 rgrid(static_cast<unsigned>((quads + kThreads - 1) / kThreads));
+    hipExtLaunchKernelGGL(splitk_reduce_kernel, rgrid, block, 0, stream, nullptr, stop, 0, p);
+    return hipGetLastError();
+  }
+  const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
   const bool interior = p.m % kTile == 0 && p.n % kTile == 0;
   if (interior && !a_kcontig && b_ncontig && p.k % 4 == 0) {
     if (p.a2 != nullptr)
