@@ -27,6 +27,20 @@
  * Y (batch x out) is op(A) = X, op(B) = W^T (operation_b = T), C = Y, with a
  * per-column bias.
  *
+ * Version 2 adds the tile GEMM on device memory the caller owns:
+ *
+ *     sgemm_device(&desc, hip_stream)
+ *
+ * enqueues C = act(alpha * op(A) * op(B) + beta * C + bias) on the stream with
+ * the kernels gemm_execute runs on each tile (full-precision FP32 MFMA), for
+ * operands already in HBM, e.g. the resolved ranges a transaction callback
+ * receives (enqueue on its native_stream). It returns once the work is
+ * enqueued. A launch with fewer 256 x 256 tiles than the GPU has CUs splits
+ * its K (partial sums in a workspace, added in a fixed order: the same result
+ * on every call); the workspace is desc.workspace when it holds every partial,
+ * else one the library allocates stream-ordered on the stream
+ * (hipMallocAsync, freed behind the kernels).
+ *
  * Conventions are those of xvram.h: struct_size first, reserved members and
  * unknown flags must be zero.
  */
@@ -42,8 +56,9 @@ extern "C" {
 /* The version passed to xvram_get_api for the extension table ('X','A' in the
    top bytes keeps it clear of the reference's small ABI numbers). */
 #define XVRAM_AMD_EXT_ABI_VERSION_1 UINT32_C(0x58410001)
-/* Value of xvram_amd_ext_v1.ext_version. */
+/* Values of xvram_amd_ext_v1.ext_version: 2 = the table has sgemm_device. */
 #define XVRAM_AMD_EXT_VERSION_1 UINT32_C(1)
+#define XVRAM_AMD_EXT_VERSION_2 UINT32_C(2)
 
 typedef uint32_t xvram_amd_bias_axis;
 enum {
@@ -85,6 +100,30 @@ typedef struct xvram_amd_device_info_v1 {
   uint64_t reserved[4];
 } xvram_amd_device_info_v1;
 
+/* One GEMM on device memory, column-major (see sgemm_device above). Every
+   pointer is device memory of the stream's GPU, 16-byte aligned; leading
+   dimensions are in floats, multiples of 4, at least the stored rows; each
+   operand buffer holds ld x (stored columns) floats. m, n, k in 1..2^31-1. */
+typedef struct xvram_amd_sgemm_v1 {
+  uint32_t struct_size;
+  uint32_t flags;
+  const float* a;       /* op N: A(i,p) = a[i + p*lda] (m x k); op T: a[p + i*lda] */
+  const float* b;       /* op N: B(p,j) = b[p + j*ldb] (k x n); op T: b[j + p*ldb] */
+  float* c;             /* C(i,j) = c[i + j*ldc] (m x n) */
+  const float* bias;    /* m (PER_ROW) or n (PER_COLUMN) floats; NULL with BIAS_NONE */
+  void* workspace;      /* optional split-K workspace; NULL = the library's */
+  uint64_t workspace_bytes;
+  uint64_t m, n, k;
+  uint64_t lda, ldb, ldc;
+  double alpha;         /* converted to float */
+  double beta;          /* converted to float; 0 = C is not read */
+  xvram_matrix_operation operation_a;
+  xvram_matrix_operation operation_b;
+  xvram_amd_bias_axis bias_axis;
+  xvram_amd_activation activation;
+  uint64_t reserved[4];
+} xvram_amd_sgemm_v1;
+
 typedef struct xvram_amd_ext_v1 {
   uint32_t struct_size;
   uint32_t ext_version;
@@ -97,7 +136,14 @@ typedef struct xvram_amd_ext_v1 {
                                                       xvram_gemm_plan* out_plan);
   /* Fills `out` (struct_size >= v1, preserved) for device `ordinal`. */
   xvram_status(XVRAM_CALL* device_get_info)(int32_t ordinal, xvram_amd_device_info_v1* out);
-  uint64_t reserved[3];
+  /* ext_version >= 2: one GEMM on device memory, enqueued on `hip_stream` (a
+     hipStream_t; NULL = the default stream of the calling thread's device).
+     No counterpart in the reference (its tile GEMM is internal). Returns
+     INVALID_ARGUMENT for a malformed descriptor, DEVICE_OUT_OF_MEMORY when a
+     needed workspace cannot be allocated, CUDA_ERROR (a hipError_t) when the
+     enqueue fails, UNSUPPORTED in a build without a GPU. */
+  xvram_status(XVRAM_CALL* sgemm_device)(const xvram_amd_sgemm_v1* desc, void* hip_stream);
+  uint64_t reserved[2];
 } xvram_amd_ext_v1;
 
 #ifdef __cplusplus

@@ -95,6 +95,66 @@ def test_ctypes_mirror_matches_header(header_layout):
         assert getattr(CTYPES[s], f).offset == off, (s, f)
 
 
+def test_extension_ctypes_mirror_matches_header(tmp_path):
+    """The extension header's structures (no reference counterpart) as gcc lays
+    them out, against the ctypes mirror the tests call through."""
+    structs = {"xvram_amd_epilogue_v1": abi.EpilogueV1, "xvram_amd_device_info_v1": abi.DeviceInfoV1,
+               "xvram_amd_sgemm_v1": abi.SgemmDeviceV1, "xvram_amd_ext_v1": abi.ExtV1}
+    lines = ["#include <xvram/xvram_amd_ext.h>", "#include <stdio.h>", "#include <stddef.h>",
+             "int main(void){"]
+    for name, cls in structs.items():
+        lines.append(f'printf("S {name} %zu\\n", sizeof({name}));')
+        for field, _ in cls._fields_:
+            lines.append(f'printf("O {name} {field} %zu\\n", offsetof({name}, {field}));')
+    lines.append("return 0;}")
+    src = tmp_path / "ext.c"
+    src.write_text("\n".join(lines))
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", f"-I{ROOT}/include", str(src), "-o",
+                    str(tmp_path / "ext")], check=True)
+    out = subprocess.run([str(tmp_path / "ext")], check=True, capture_output=True, text=True).stdout
+    for line in out.splitlines():
+        parts = line.split()
+        cls = structs[parts[1]]
+        if parts[0] == "S":
+            assert ctypes.sizeof(cls) == int(parts[2]), parts[1]
+        else:
+            assert getattr(cls, parts[2]).offset == int(parts[3]), (parts[1], parts[2])
+
+
+def test_device_gemm_rules_without_a_gpu():
+    """sgemm_device's descriptor checks (INVALID_ARGUMENT / INCOMPATIBLE_ABI)
+    run before any device work; a valid descriptor is UNSUPPORTED in the host
+    simulation, which has no device memory."""
+    lib = xv.Library(xv.HOSTSIM_LIB)
+    call = lib.ext.sgemm_device
+
+    def valid():
+        d = abi.sgemm_device_init()
+        d.a, d.b, d.c = 4096, 8192, 12288  # 16-byte aligned stand-ins, never dereferenced
+        d.m, d.n, d.k = 256, 256, 256
+        d.lda = d.ldb = d.ldc = 256
+        return d
+
+    assert call(ctypes.byref(valid()), None) == abi.UNSUPPORTED
+    assert call(None, None) == abi.INCOMPATIBLE_ABI
+    d = valid()
+    d.struct_size = 8
+    assert call(ctypes.byref(d), None) == abi.INCOMPATIBLE_ABI
+    bad = [("flags", 1), ("operation_a", 2), ("bias_axis", 3), ("activation", 2), ("a", None),
+           ("m", 0), ("k", 1 << 31), ("lda", 128), ("ldc", 258), ("b", 8200),
+           ("bias_axis", abi.BIAS_PER_ROW), ("workspace_bytes", 64)]
+    for field, value in bad:
+        d = valid()
+        setattr(d, field, value)
+        assert call(ctypes.byref(d), None) == abi.INVALID_ARGUMENT, field
+    d = valid()
+    d.operation_a = abi.OP_T  # A stored k x m: lda must cover k, B (op N) k x n: ldb too
+    d.k, d.lda, d.ldb = 512, 256, 512
+    assert call(ctypes.byref(d), None) == abi.INVALID_ARGUMENT
+    d.lda = 512
+    assert call(ctypes.byref(d), None) == abi.UNSUPPORTED
+
+
 def _elf_exports(path):
     """Defined dynamic symbols as the reference's export contract reads them
     (tests/contract/sdk_export_contract.py:66-99): `nm -D --defined-only
@@ -163,10 +223,11 @@ def test_extension_table_through_get_api(path):
     ext = abi.ExtV1()
     size = ctypes.sizeof(ext)
     assert lib.get_api(abi.EXT_ABI_VERSION_1, size, ctypes.byref(ext)) == abi.SUCCESS
-    assert ext.struct_size == size and ext.ext_version == abi.EXT_VERSION_1
+    assert ext.struct_size == size and ext.ext_version == abi.EXT_VERSION_2
     assert ctypes.cast(ext.gemm_plan_create_epilogue, ctypes.c_void_p).value
     assert ctypes.cast(ext.device_get_info, ctypes.c_void_p).value
-    assert list(ext.reserved) == [0, 0, 0]
+    assert ctypes.cast(ext.sgemm_device, ctypes.c_void_p).value
+    assert list(ext.reserved) == [0, 0]
     assert lib.get_api(abi.EXT_ABI_VERSION_1, size - 1, ctypes.byref(ext)) == abi.INVALID_ARGUMENT
     assert lib.get_api(abi.EXT_ABI_VERSION_1, size, None) == abi.INVALID_ARGUMENT
     for version in (abi.EXT_ABI_VERSION_1 + 1, abi.EXT_ABI_VERSION_1 - 1, 0x58410000, 1 << 31):

@@ -265,6 +265,7 @@ def plan_info_init() -> GemmPlanInfo:
 # and the table's own ext_version (XVRAM_AMD_EXT_VERSION_1).
 EXT_ABI_VERSION_1 = 0x58410001
 EXT_VERSION_1 = 1
+EXT_VERSION_2 = 2  # the table has sgemm_device
 BIAS_NONE, BIAS_PER_ROW, BIAS_PER_COLUMN = 0, 1, 2
 ACTIVATION_NONE, ACTIVATION_RELU = 0, 1
 
@@ -286,12 +287,30 @@ class DeviceInfoV1(Structure):
                 ("runtime_version", c_int32), ("reserved", c_uint64 * 4)]
 
 
+class SgemmDeviceV1(Structure):
+    """xvram_amd_sgemm_v1: one GEMM on device memory (pointers as integers)."""
+    _fields_ = [("struct_size", c_uint32), ("flags", c_uint32), ("a", c_void_p),
+                ("b", c_void_p), ("c", c_void_p), ("bias", c_void_p), ("workspace", c_void_p),
+                ("workspace_bytes", c_uint64), ("m", c_uint64), ("n", c_uint64), ("k", c_uint64),
+                ("lda", c_uint64), ("ldb", c_uint64), ("ldc", c_uint64), ("alpha", c_double),
+                ("beta", c_double), ("operation_a", c_uint32), ("operation_b", c_uint32),
+                ("bias_axis", c_uint32), ("activation", c_uint32), ("reserved", c_uint64 * 4)]
+
+
 class ExtV1(Structure):
     _fields_ = [("struct_size", c_uint32), ("ext_version", c_uint32),
                 ("gemm_plan_create_epilogue",
                  _F(c_uint32, _H, POINTER(GemmDesc), POINTER(EpilogueV1), POINTER(_H))),
                 ("device_get_info", _F(c_uint32, c_int32, POINTER(DeviceInfoV1))),
-                ("reserved", c_uint64 * 3)]
+                ("sgemm_device", _F(c_uint32, POINTER(SgemmDeviceV1), c_void_p)),
+                ("reserved", c_uint64 * 2)]
+
+
+def sgemm_device_init() -> SgemmDeviceV1:
+    d = SgemmDeviceV1()
+    d.struct_size = ctypes.sizeof(SgemmDeviceV1)
+    d.alpha = 1.0
+    return d
 
 
 def epilogue_init() -> EpilogueV1:

@@ -31,7 +31,7 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
 HOST_SOURCES = ["api.cpp", "errors.cpp", "session.cpp", "runtime.cpp", "gemm.cpp", "policy.cpp"]
-HIP_SOURCES = ["sgemm_mfma.hip", "sgemm_wide.hip"]
+HIP_SOURCES = ["sgemm_mfma.hip", "sgemm_wide.hip", "sgemm_direct.hip"]
 COMMON_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-fvisibility=hidden", "-DXVRAM_BUILDING_LIBRARY",
                 f"-I{INCLUDE}", f"-I{CSRC}", "-Wall", "-Wextra", "-Wno-unused-parameter"]
 # Packed-FP32 instructions are disabled for every HIP compile.

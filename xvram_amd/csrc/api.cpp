@@ -274,6 +274,79 @@ Error read_epilogue(Session* session, const xvram_amd_epilogue_v1& in, EpilogueS
   return {};
 }
 
+// The extension's device-memory GEMM descriptor (no reference counterpart).
+using DeviceGemm = xvram_amd_sgemm_v1;
+constexpr uint64_t kInt32Max = static_cast<uint64_t>(INT32_MAX);
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+const Rule<DeviceGemm> kDeviceGemmRules[] = {
+    {[](const DeviceGemm& d) { return d.flags == 0 && zeroed(d.reserved); },
+     "flags and reserved[] must be zero"},
+    {[](const DeviceGemm& d) {
+       return d.operation_a <= XVRAM_MATRIX_OP_T && d.operation_b <= XVRAM_MATRIX_OP_T &&
+              d.bias_axis <= XVRAM_AMD_BIAS_PER_COLUMN && d.activation <= XVRAM_AMD_ACTIVATION_RELU;
+     },
+     "an operation, bias axis or activation is not a known value"},
+    {[](const DeviceGemm& d) { return d.a != nullptr && d.b != nullptr && d.c != nullptr; },
+     "a, b and c must be device pointers"},
+    {[](const DeviceGemm& d) {
+       return d.m > 0 && d.n > 0 && d.k > 0 && d.m <= kInt32Max && d.n <= kInt32Max &&
+              d.k <= kInt32Max;
+     },
+     "m, n and k must lie in 1..2^31-1"},
+    {[](const DeviceGemm& d) {
+       const uint64_t a_rows = d.operation_a == XVRAM_MATRIX_OP_N ? d.m : d.k;
+       const uint64_t b_rows = d.operation_b == XVRAM_MATRIX_OP_N ? d.k : d.n;
+       return d.lda >= a_rows && d.ldb >= b_rows && d.ldc >= d.m && d.lda % 4 == 0 &&
+              d.ldb % 4 == 0 && d.ldc % 4 == 0;
+     },
+     "leading dimensions must cover the stored rows and be multiples of 4 floats"},
+    {[](const DeviceGemm& d) {
+       return aligned16(d.a) && aligned16(d.b) && aligned16(d.c) && aligned16(d.workspace);
+     },
+     "a, b, c and the workspace must be 16-byte aligned"},
+    {[](const DeviceGemm& d) { return (d.bias_axis != XVRAM_AMD_BIAS_NONE) == (d.bias != nullptr); },
+     "a bias vector needs a bias axis and a bias axis needs a bias vector"},
+    {[](const DeviceGemm& d) { return d.workspace != nullptr || d.workspace_bytes == 0; },
+     "workspace_bytes is given without a workspace"},
+};
+
+Error read_device_gemm(const DeviceGemm* d, const char* entry, kernels::SgemmLaunch& out) {
+  if (!versioned(d)) return too_old(entry, "the device GEMM descriptor is missing or older than v1");
+  if (Error e = first_broken(kDeviceGemmRules, *d, entry)) return e;
+  out.a = d->a;
+  out.b = d->b;
+  out.c = d->c;
+  out.lda = static_cast<int64_t>(d->lda);
+  out.ldb = static_cast<int64_t>(d->ldb);
+  out.ldc = static_cast<int64_t>(d->ldc);
+  out.m = static_cast<int>(d->m);
+  out.n = static_cast<int>(d->n);
+  out.k = static_cast<int>(d->k);
+  out.alpha = static_cast<float>(d->alpha);
+  out.beta = static_cast<float>(d->beta);
+  out.a_kcontig = d->operation_a == XVRAM_MATRIX_OP_T;
+  out.b_ncontig = d->operation_b == XVRAM_MATRIX_OP_T;
+  out.padded = true;
+  if (d->bias_axis == XVRAM_AMD_BIAS_PER_ROW) out.bias_row = d->bias;
+  if (d->bias_axis == XVRAM_AMD_BIAS_PER_COLUMN) out.bias_col = d->bias;
+  out.relu = d->activation == XVRAM_AMD_ACTIVATION_RELU;
+  out.workspace = static_cast<float*>(d->workspace);
+  out.workspace_bytes = d->workspace_bytes;
+  return {};
+}
+
+Error device_gemm_failure(int rc, const char* entry) {
+  if (rc == kNoDevice)
+    return make_error(XVRAM_STATUS_UNSUPPORTED, kStage, entry,
+                      "this build has no GPU (host simulation)");
+  Error e = make_error(rc == 2 /* hipErrorOutOfMemory */ ? XVRAM_STATUS_DEVICE_OUT_OF_MEMORY
+                                                          : XVRAM_STATUS_CUDA_ERROR,
+                       kStage, entry, "the HIP runtime refused the launch or its workspace");
+  e.native_domain = XVRAM_NATIVE_ERROR_CUDA;
+  e.native_code = rc;
+  return e;
+}
+
 // ---- handles -----------------------------------------------------------------
 
 bool live(const xvram_session_t* h) { return h != nullptr && h->session; }
@@ -705,6 +778,16 @@ xvram_status XVRAM_CALL operation_get_error(xvram_operation op, xvram_error_info
 
 void XVRAM_CALL operation_release(xvram_operation op) noexcept { delete op; }
 
+xvram_status XVRAM_CALL sgemm_device(const xvram_amd_sgemm_v1* desc, void* stream) noexcept {
+  constexpr const char* entry = "sgemm_device";
+  return guarded(nullptr, entry, [&]() -> Error {
+    kernels::SgemmLaunch launch;
+    if (Error e = read_device_gemm(desc, entry, launch)) return e;
+    if (const int rc = direct_sgemm(launch, stream)) return device_gemm_failure(rc, entry);
+    return {};
+  });
+}
+
 xvram_status XVRAM_CALL device_get_info(int32_t ordinal, xvram_amd_device_info_v1* out) noexcept {
   if (!versioned(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
   try {
@@ -786,9 +869,10 @@ const xvram_api_v2 kApiV2 = {
 // the one export so the library's symbol set stays the reference's.
 const xvram_amd_ext_v1 kExtV1 = {
     .struct_size = sizeof(xvram_amd_ext_v1),
-    .ext_version = XVRAM_AMD_EXT_VERSION_1,
+    .ext_version = XVRAM_AMD_EXT_VERSION_2,
     .gemm_plan_create_epilogue = entry::gemm_plan_create_epilogue,
     .device_get_info = entry::device_get_info,
+    .sgemm_device = entry::sgemm_device,
     .reserved = {},
 };
 

@@ -92,6 +92,15 @@ public:
 
 // Defined by exactly one of device_hip.cpp / device_hostsim.cpp.
 std::unique_ptr<Device> make_device();
+
+// What direct_sgemm returns where there is no device (the host simulation).
+constexpr int kNoDevice = -2;
+// Enqueues one tile-kernel launch on caller device memory on `stream` (a
+// hipStream_t, NULL = the calling thread's default stream). A launch that
+// splits K uses launch.workspace when it holds every partial the split wants,
+// else a stream-ordered allocation freed behind the kernels. Returns 0, the
+// native error code, or kNoDevice (sgemm_direct.hip / device_hostsim.cpp).
+int direct_sgemm(const kernels::SgemmLaunch& launch, void* stream);
 // Describes device `ordinal` without disturbing the calling thread's current
 // device; returns 0 or the native error code.
 int describe_device(int ordinal, DeviceInfo& out);

@@ -410,6 +410,9 @@ int describe_device(int ordinal, DeviceInfo& out) {
   return 0;
 }
 
+// Caller device memory does not exist in the simulation.
+int direct_sgemm(const kernels::SgemmLaunch&, void*) { return kNoDevice; }
+
 } // namespace xvram
 
 // Test-only controls exported by libxvram_hostsim.so.

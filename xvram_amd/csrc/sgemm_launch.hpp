@@ -99,18 +99,30 @@ inline SplitK split_k_shape(int64_t m, int64_t n, int64_t k, bool nt, uint64_t w
   return SplitK{static_cast<int>(splits), static_cast<int>(depth32)};
 }
 
-// The split of one launch: split_k_shape, for a one-panel launch with a
-// 16-byte aligned workspace whose operand panels each span less than 2^31
-// bytes (the ring kernels' 32-bit buffer offsets).
-inline SplitK split_k_plan(const SgemmLaunch& l) {
+// The split a launch takes given room for `workspace_bytes` of partials: none
+// for a two-panel launch or one whose operand panels do not each span less
+// than 2^31 bytes (the ring kernels' 32-bit buffer offsets), else
+// split_k_shape.
+inline SplitK split_k_for(const SgemmLaunch& l, uint64_t workspace_bytes) {
   constexpr int64_t kLimit = int64_t(1) << 31;
-  if (l.workspace == nullptr || l.a2 != nullptr || l.b2 != nullptr ||
-      reinterpret_cast<uintptr_t>(l.workspace) % 16 != 0)
-    return {};
+  if (l.a2 != nullptr || l.b2 != nullptr) return {};
   const int64_t a_bytes = (l.a_kcontig ? int64_t{l.m} : int64_t{l.k}) * l.lda * 4;
   const int64_t b_bytes = (l.b_ncontig ? int64_t{l.k} : int64_t{l.n}) * l.ldb * 4;
   if (a_bytes >= kLimit || b_bytes >= kLimit) return {};
-  return split_k_shape(l.m, l.n, l.k, !l.a_kcontig && l.b_ncontig, l.workspace_bytes);
+  return split_k_shape(l.m, l.n, l.k, !l.a_kcontig && l.b_ncontig, workspace_bytes);
+}
+
+// The split of one launch with its own 16-byte aligned workspace.
+inline SplitK split_k_plan(const SgemmLaunch& l) {
+  if (l.workspace == nullptr || reinterpret_cast<uintptr_t>(l.workspace) % 16 != 0) return {};
+  return split_k_for(l, l.workspace_bytes);
+}
+
+// Bytes of partials a launch's split wants when the workspace is not the
+// limit (0: it does not split).
+inline uint64_t split_k_bytes_wanted(const SgemmLaunch& l) {
+  const SplitK sk = split_k_for(l, ~uint64_t{0});
+  return sk.splits > 1 ? static_cast<uint64_t>(sk.splits) * uint64_t(l.m) * uint64_t(l.n) * 4 : 0;
 }
 
 // Enqueues the launch on `stream` (a hipStream_t); returns a hipError_t.
