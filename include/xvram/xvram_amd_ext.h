@@ -143,7 +143,17 @@ typedef struct xvram_amd_ext_v1 {
      needed workspace cannot be allocated, CUDA_ERROR (a hipError_t) when the
      enqueue fails, UNSUPPORTED in a build without a GPU. */
   xvram_status(XVRAM_CALL* sgemm_device)(const xvram_amd_sgemm_v1* desc, void* hip_stream);
-  uint64_t reserved[2];
+  /* ext_version >= 2: sgemm_device that allocates nothing, for callers that
+     cannot allocate (code under stream capture, tight serving loops). No
+     counterpart in the reference. A split that desc->workspace cannot hold
+     uses the library's static per-GPU scratch of 64 MiB (the most any split
+     wants: one 256 KiB partial per CU), held until the process ends and
+     shared by every call on that GPU: calls that overlap on one GPU race.
+     A split wanting more returns INVALID_ARGUMENT. Same results as
+     sgemm_device. */
+  xvram_status(XVRAM_CALL* sgemm_device_no_alloc)(const xvram_amd_sgemm_v1* desc,
+                                                  void* hip_stream);
+  uint64_t reserved[1];
 } xvram_amd_ext_v1;
 
 #ifdef __cplusplus

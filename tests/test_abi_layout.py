@@ -122,12 +122,16 @@ def test_extension_ctypes_mirror_matches_header(tmp_path):
 
 
 def test_device_gemm_rules_without_a_gpu():
-    """sgemm_device's descriptor checks (INVALID_ARGUMENT / INCOMPATIBLE_ABI)
-    run before any device work; a valid descriptor is UNSUPPORTED in the host
-    simulation, which has no device memory."""
+    """sgemm_device's (and sgemm_device_no_alloc's) descriptor checks
+    (INVALID_ARGUMENT / INCOMPATIBLE_ABI) run before any device work; a valid
+    descriptor is UNSUPPORTED in the host simulation, which has no device
+    memory."""
     lib = xv.Library(xv.HOSTSIM_LIB)
-    call = lib.ext.sgemm_device
+    for call in (lib.ext.sgemm_device, lib.ext.sgemm_device_no_alloc):
+        check_device_gemm_rules(call)
 
+
+def check_device_gemm_rules(call):
     def valid():
         d = abi.sgemm_device_init()
         d.a, d.b, d.c = 4096, 8192, 12288  # 16-byte aligned stand-ins, never dereferenced
@@ -227,7 +231,8 @@ def test_extension_table_through_get_api(path):
     assert ctypes.cast(ext.gemm_plan_create_epilogue, ctypes.c_void_p).value
     assert ctypes.cast(ext.device_get_info, ctypes.c_void_p).value
     assert ctypes.cast(ext.sgemm_device, ctypes.c_void_p).value
-    assert list(ext.reserved) == [0, 0]
+    assert ctypes.cast(ext.sgemm_device_no_alloc, ctypes.c_void_p).value
+    assert list(ext.reserved) == [0]
     assert lib.get_api(abi.EXT_ABI_VERSION_1, size - 1, ctypes.byref(ext)) == abi.INVALID_ARGUMENT
     assert lib.get_api(abi.EXT_ABI_VERSION_1, size, None) == abi.INVALID_ARGUMENT
     for version in (abi.EXT_ABI_VERSION_1 + 1, abi.EXT_ABI_VERSION_1 - 1, 0x58410000, 1 << 31):

@@ -303,7 +303,8 @@ class ExtV1(Structure):
                  _F(c_uint32, _H, POINTER(GemmDesc), POINTER(EpilogueV1), POINTER(_H))),
                 ("device_get_info", _F(c_uint32, c_int32, POINTER(DeviceInfoV1))),
                 ("sgemm_device", _F(c_uint32, POINTER(SgemmDeviceV1), c_void_p)),
-                ("reserved", c_uint64 * 2)]
+                ("sgemm_device_no_alloc", _F(c_uint32, POINTER(SgemmDeviceV1), c_void_p)),
+                ("reserved", c_uint64 * 1)]
 
 
 def sgemm_device_init() -> SgemmDeviceV1:

@@ -339,6 +339,9 @@ Error device_gemm_failure(int rc, const char* entry) {
   if (rc == kNoDevice)
     return make_error(XVRAM_STATUS_UNSUPPORTED, kStage, entry,
                       "this build has no GPU (host simulation)");
+  if (rc == kScratchTooSmall)
+    return make_error(XVRAM_STATUS_INVALID_ARGUMENT, kStage, entry,
+                      "the split's partials exceed the 64 MiB static scratch; pass a workspace");
   Error e = make_error(rc == 2 /* hipErrorOutOfMemory */ ? XVRAM_STATUS_DEVICE_OUT_OF_MEMORY
                                                           : XVRAM_STATUS_CUDA_ERROR,
                        kStage, entry, "the HIP runtime refused the launch or its workspace");
@@ -788,6 +791,18 @@ xvram_status XVRAM_CALL sgemm_device(const xvram_amd_sgemm_v1* desc, void* strea
   });
 }
 
+// sgemm_device without any allocation (the static per-GPU scratch serves a
+// split the caller's workspace cannot hold).
+xvram_status XVRAM_CALL sgemm_device_no_alloc(const xvram_amd_sgemm_v1* desc, void* stream) noexcept {
+  constexpr const char* entry = "sgemm_device_no_alloc";
+  return guarded(nullptr, entry, [&]() -> Error {
+    kernels::SgemmLaunch launch;
+    if (Error e = read_device_gemm(desc, entry, launch)) return e;
+    if (const int rc = direct_sgemm_no_alloc(launch, stream)) return device_gemm_failure(rc, entry);
+    return {};
+  });
+}
+
 xvram_status XVRAM_CALL device_get_info(int32_t ordinal, xvram_amd_device_info_v1* out) noexcept {
   if (!versioned(out)) return XVRAM_STATUS_INVALID_ARGUMENT;
   try {
@@ -873,6 +888,7 @@ const xvram_amd_ext_v1 kExtV1 = {
     .gemm_plan_create_epilogue = entry::gemm_plan_create_epilogue,
     .device_get_info = entry::device_get_info,
     .sgemm_device = entry::sgemm_device,
+    .sgemm_device_no_alloc = entry::sgemm_device_no_alloc,
     .reserved = {},
 };
 

@@ -101,6 +101,12 @@ constexpr int kNoDevice = -2;
 // else a stream-ordered allocation freed behind the kernels. Returns 0, the
 // native error code, or kNoDevice (sgemm_direct.hip / device_hostsim.cpp).
 int direct_sgemm(const kernels::SgemmLaunch& launch, void* stream);
+// What direct_sgemm_no_alloc returns for a split wanting more than its scratch.
+constexpr int kScratchTooSmall = -3;
+// direct_sgemm that allocates nothing: a split that the launch's own
+// workspace cannot hold uses the library's static per-GPU scratch (64 MiB,
+// shared by every call on that GPU).
+int direct_sgemm_no_alloc(const kernels::SgemmLaunch& launch, void* stream);
 // Describes device `ordinal` without disturbing the calling thread's current
 // device; returns 0 or the native error code.
 int describe_device(int ordinal, DeviceInfo& out);

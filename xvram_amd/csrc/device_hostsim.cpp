@@ -412,6 +412,7 @@ int describe_device(int ordinal, DeviceInfo& out) {
 
 // Caller device memory does not exist in the simulation.
 int direct_sgemm(const kernels::SgemmLaunch&, void*) { return kNoDevice; }
+int direct_sgemm_no_alloc(const kernels::SgemmLaunch&, void*) { return kNoDevice; }
 
 } // namespace xvram
 
