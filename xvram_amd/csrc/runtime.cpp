@@ -96,8 +96,10 @@ Error Runtime::poison(std::string_view stage, std::string_view operation,
   return make_error(XVRAM_STATUS_POISONED, stage, operation, message);
 }
 
-// Polls rather than blocks (hipEventSynchronize has no time limit): yields for
-// the first millisecond, then sleeps between queries.
+// Polls rather than blocks (hipEventSynchronize has no time limit). The host
+// spins (yielding) through the first 50 ms, the length of the longest waits
+// of a running schedule (a frame's last kernel), so completion is seen at
+// once; longer waits sleep 100 us between queries.
 Error Runtime::await_event(Event event, std::string_view stage, std::string_view operation) {
   if (quarantined_)
     return make_error(XVRAM_STATUS_POISONED, stage, operation,
@@ -120,20 +122,29 @@ Error Runtime::await_event(Event event, std::string_view stage, std::string_view
       e.status = XVRAM_STATUS_TIMEOUT;
       return e;
     }
-    if (now - begun < std::chrono::milliseconds(1)) std::this_thread::yield();
-    else std::this_thread::sleep_for(std::chrono::microseconds(20));
+    if (now - begun < std::chrono::milliseconds(50)) std::this_thread::yield();
+    else std::this_thread::sleep_for(std::chrono::microseconds(100));
   }
 }
 
-Error Runtime::await_stream(Stream stream, std::string_view stage, std::string_view operation) {
+Error Runtime::await_streams(std::initializer_list<Stream> streams, std::string_view stage,
+                             std::string_view operation) {
   if (quarantined_)
     return make_error(XVRAM_STATUS_POISONED, stage, operation,
                       "device work of this session is quarantined after a stalled or failed wait");
-  if (int rc = device_->event_record(sync_marker_, stream)) {
-    quarantined_ = true;
-    return device_failure(rc, stage, operation);
+  if (streams.size() > static_cast<size_t>(kSyncMarkers))
+    return make_error(XVRAM_STATUS_INTERNAL, stage, operation, "too many streams for one wait");
+  int used = 0;
+  for (Stream s : streams) {
+    if (int rc = device_->event_record(sync_markers_[used], s)) {
+      quarantined_ = true;
+      return device_failure(rc, stage, operation);
+    }
+    ++used;
   }
-  return await_event(sync_marker_, stage, operation);
+  for (int i = 0; i < used; ++i)
+    if (Error e = await_event(sync_markers_[i], stage, operation)) return e;
+  return {};
 }
 
 // Session setup (reference src/residency/runtime.cpp:212-596): bind the
@@ -199,7 +210,8 @@ Error Runtime::setup() {
   if (int rc = device_->event_create(&op_start_)) return device_failure(rc, "setup", "event");
   if (int rc = device_->event_create(&op_start2_)) return device_failure(rc, "setup", "event");
   if (int rc = device_->event_create(&carry_fence_)) return device_failure(rc, "setup", "event");
-  if (int rc = device_->event_create(&sync_marker_)) return device_failure(rc, "setup", "event");
+  for (Event& marker : sync_markers_)
+    if (int rc = device_->event_create(&marker)) return device_failure(rc, "setup", "event");
   t_.flags = XVRAM_TELEMETRY_NO_PHYSICAL_ALIASES | XVRAM_TELEMETRY_STABLE_VIRTUAL_ADDRESSES;
   setup_done_ = true;
   return {};
@@ -212,8 +224,7 @@ Error Runtime::drain() {
   if (!setup_done_ || closed_) return {};
   if (!poisoned_)
     if (Error e = flush_all()) return e;
-  for (Stream s : {h2d_, compute_, compute2_, d2h_})
-    if (Error e = await_stream(s, "drain", "stream_wait")) return e;
+  if (Error e = await_streams({h2d_, compute_, compute2_, d2h_}, "drain", "stream_wait")) return e;
   writebacks_settled();
   return {};
 }
@@ -265,10 +276,10 @@ Error Runtime::close() {
   for (Frame& f : frames_) f.pins = 0;
   if (!poisoned_)
     if (Error e = flush_all(); e && !first) first = e;
-  for (Stream s : {h2d_, compute_, compute2_, d2h_}) {
-    if (quarantined_) break;
-    if (Error e = await_stream(s, "close", "stream_wait"); e && !first) first = e;
-  }
+  if (!quarantined_)
+    if (Error e = await_streams({h2d_, compute_, compute2_, d2h_}, "close", "stream_wait");
+        e && !first)
+      first = e;
   if (quarantined_) return abandon_device_resources();
   for (Frame& f : frames_) {
     if (f.keyed) {
@@ -307,9 +318,13 @@ Error Runtime::close() {
   carried_events_.clear();
   carried_trace_.clear();
   pending_writebacks_.clear();
-  for (Event* e : {&op_start_, &op_start2_, &carry_fence_, &sync_marker_}) {
+  for (Event* e : {&op_start_, &op_start2_, &carry_fence_}) {
     if (*e) device_->event_destroy(*e);
     *e = nullptr;
+  }
+  for (Event& marker : sync_markers_) {
+    if (marker) device_->event_destroy(marker);
+    marker = nullptr;
   }
   for (Stream s : {h2d_, compute_, compute2_, d2h_})
     if (s) device_->stream_destroy(s);
@@ -346,7 +361,8 @@ Error Runtime::abandon_device_resources() {
   carried_trace_.clear();
   pending_writebacks_.clear();
   compute_ = compute2_ = h2d_ = d2h_ = nullptr;
-  op_start_ = op_start2_ = carry_fence_ = sync_marker_ = nullptr;
+  op_start_ = op_start2_ = carry_fence_ = nullptr;
+  for (Event& marker : sync_markers_) marker = nullptr;
   workspace_va_ = 0;
   arena_ = 0;
   t_.resident_bytes = 0;
@@ -1669,9 +1685,8 @@ Error Runtime::finish_operation(uint64_t operation_id) {
   };
   const double enqueued_ms = host_ms(); // everything is enqueued: the host waits from here
   Error first;
-  for (Stream s : {compute_, compute2_, d2h_}) {
-    if (Error e = await_stream(s, "operation", "stream_wait"); e && !first) first = e;
-  }
+  if (Error e = await_streams({compute_, compute2_, d2h_}, "operation", "stream_wait"); e)
+    first = e;
   // This operation's own fills end at the carry fence; carried fills run on.
   if (Error e = carry_active_ ? await_event(carry_fence_, "operation", "fill_wait")
                               : await_stream(h2d_, "operation", "stream_wait");

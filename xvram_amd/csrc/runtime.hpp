@@ -375,7 +375,13 @@ public:
   // error, the runtime is quarantined and the call fails (TIMEOUT / the
   // device error).
   Error await_event(Event event, std::string_view stage, std::string_view operation);
-  Error await_stream(Stream stream, std::string_view stage, std::string_view operation);
+  Error await_stream(Stream stream, std::string_view stage, std::string_view operation) {
+    return await_streams({stream}, stage, operation);
+  }
+  // Every queue in `streams` (at most kSyncMarkers): a marker is recorded on
+  // each first, so the waits overlap.
+  Error await_streams(std::initializer_list<Stream> streams, std::string_view stage,
+                      std::string_view operation);
   Error abandon_device_resources();
   Error poison(std::string_view stage, std::string_view operation, std::string_view message);
 
@@ -449,7 +455,10 @@ private:
   std::vector<PanelKey> lost_;
   Error check_not_lost(const PanelKey& range, const char* stage, const char* operation) const;
   void forget_lost_within(const PanelKey& rewritten);
-  Event sync_marker_ = nullptr; // recorded on a stream to wait for its queue
+  // Recorded on streams to wait for their queues (one per stream a single
+  // wait covers: all are recorded before any is polled).
+  static constexpr int kSyncMarkers = 4;
+  Event sync_markers_[kSyncMarkers] = {};
   bool launches_blocked_ = false;
 
   uint64_t granularity_ = 0;
