@@ -8,6 +8,10 @@ ABI, against the FP64 oracle.
   full K (oracle/sample.py); plus the analytic pattern at the same shapes,
   every element bit-exact. A repeated execution moves no bytes: C stays
   cached (dirty) between executions of the write-back cache.
+* The same sweep's 8192^3 and 16384^3 under the reference's default session
+  (64 MiB frames, automatic budget): tiled, the operands cached; the sample
+  (one full column and row per 2048-wide band, two per 4096-wide tile) and the
+  pattern.
 * Config 4: 32768^3 N/T under a 2 GiB budget of 64 MiB frames, seeded U[-1,1):
   one full column per tile column, one full row per tile row of the plan's C
   grid, and 1024 random elements -- every C block of the out-of-core schedule
@@ -160,6 +164,62 @@ def test_c3_resident_pattern_every_element(lib, synth, oracle_mod, size, frame, 
         expect = oracle_mod.pattern_expected_matrix(m, n, k).astype(np.float32)
         bad = int(np.count_nonzero(got != expect))
         log(f"C3 pattern {size}^3 N{'NT'[op_b]}: {m * n} elements, {bad} differ")
+        assert bad == 0
+        plan.release()
+    finally:
+        closed(s)
+
+
+# The same sweep under the reference's default session (xvram.h:135-150:
+# 64 MiB frames, cache_target_bytes 0 = free memory - headroom), as a drop-in
+# caller that never tunes frames gets it: 8192^3 and 16384^3 are tiled into
+# 4096 x 4096 C tiles with 4096-deep K panels (two per launch after the first
+# pass), the operands stay cached, and a repeated execution moves no bytes.
+C3_DEFAULT = [(size, op_b) for size in (8192, 16384) for op_b in (abi.OP_N, abi.OP_T)]
+C3_DEFAULT_IDS = [f"{size}_n{'nt'[op_b]}" for size, op_b in C3_DEFAULT]
+
+
+@pytest.mark.parametrize("size,op_b", C3_DEFAULT, ids=C3_DEFAULT_IDS)
+def test_c3_default_session_random(lib, synth, size, op_b):
+    m = n = k = size
+    s = xv.Session(lib)  # XVRAM_SESSION_CONFIG_V1_INIT
+    try:
+        assert s.config.chunk_size_bytes == 64 * MiB and s.config.cache_target_bytes == 0
+        a, b, c, plan, (b_rows, b_cols) = operands(s, m, n, k, op_b)
+        info = plan.info()
+        assert (info.tile_m, info.tile_n, info.tile_k) == (4096, 4096, 4096)
+        assert info.tile_count == (size // 4096) ** 3
+        fill_uniform(synth, a, m * k, 311)
+        fill_uniform(synth, b, k * n, 312)
+        run_op(plan)
+        again = run_op(plan)
+        assert again.bytes_h2d == 0 and again.bytes_d2h == 0  # resident: all hits
+        t = time.perf_counter()
+        res = spread_check(SeededOperand(311, m, k, False),
+                           SeededOperand(312, b_rows, b_cols, op_b == abi.OP_T),
+                           column_reader(c, m), 2048, 2048, seed=size + 7 + op_b, randoms=1024)
+        log(f"C3 default session {size}^3 N{'NT'[op_b]}: {res['elements']} elements, "
+            f"violations {res['violations']}, err/bound {res['max_err_over_bound']:.3e} "
+            f"({time.perf_counter() - t:.1f} s)")
+        assert res["elements"] >= 50000 and res["violations"] == 0
+        plan.release()
+    finally:
+        closed(s)
+
+
+@pytest.mark.parametrize("size,op_b", C3_DEFAULT, ids=C3_DEFAULT_IDS)
+def test_c3_default_session_pattern_every_element(lib, synth, oracle_mod, size, op_b):
+    m = n = k = size
+    s = xv.Session(lib)
+    try:
+        a, b, c, plan, (b_rows, b_cols) = operands(s, m, n, k, op_b)
+        fill_pattern(a, synth.synth_fill_pattern_a, m, k, 0)
+        fill_pattern(b, synth.synth_fill_pattern_b, b_rows, b_cols, 1 if op_b == abi.OP_T else 0)
+        run_op(plan)
+        got = c.read(dtype=np.float32).reshape(n, m).T
+        expect = oracle_mod.pattern_expected_matrix(m, n, k).astype(np.float32)
+        bad = int(np.count_nonzero(got != expect))
+        log(f"C3 default session pattern {size}^3 N{'NT'[op_b]}: {m * n} elements, {bad} differ")
         assert bad == 0
         plan.release()
     finally:

@@ -9,7 +9,16 @@ size in pinned host memory (the product-side pattern fillers, themselves
 checked against the oracle on the CPU), the GEMM runs once through the C ABI
 with the benchmark's budget, frames and N/T operands, and all of C is read back
 and compared -- every element of the north-star 65536^3 product out of core, and
-of config 4's 32768^3 product under a 2 GiB budget."""
+of config 4's 32768^3 product under a 2 GiB budget.
+
+The pattern repeats with period 3 in rows and 5 in columns, so with 8192-wide
+tiles a C block routed between tile rows t and t+3 (or tile columns t and
+t+5) would still match it. The north-star product is therefore also run on
+seeded U[-1,1) operands and checked against the FP64 oracle on one full
+column in every tile column, one full row in every tile row and 1024 random
+elements, each with its full K (oracle/sample.py), within
+|C - C_ref| <= 4*K*2^-24*(|A||B|)_ij (src/gemm_bench/executor.cpp:779-843
+checks the reference's runs the same way, on a sample)."""
 import ctypes
 import os
 import time
@@ -37,6 +46,7 @@ def synth():
     for name in ("synth_fill_pattern_a", "synth_fill_pattern_b"):
         getattr(lib, name).argtypes = [fp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64,
                                        ctypes.c_int]
+    lib.synth_fill_uniform.argtypes = [fp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64]
     return lib
 
 
@@ -112,4 +122,53 @@ def test_every_element_of_the_pattern_product(synth, oracle_mod, size, budget, f
         t = s.telemetry()
         assert t.mappings == t.unmaps and t.physical_handles_created == t.physical_handles_released
         assert t.unsafe_transitions == 0 and t.unsafe_remaps == 0
+        s.release()
+
+
+def test_north_star_random_every_tile_row_and_column_sampled(synth):
+    from oracle.sample import SeededOperand, spread_check
+
+    m = n = k = 65536
+    budget, frame = 16 * GiB, 1024 * MiB
+    lib = xv.load()
+    s = xv.Session(lib, chunk_size_bytes=frame, cache_target_bytes=budget)
+    fp = ctypes.POINTER(ctypes.c_float)
+    try:
+        t = time.perf_counter()
+        a = s.allocation(m * k * 4)          # A, op N: stored m x k
+        b = s.allocation(n * k * 4)          # B, op T: stored n x k
+        c = s.allocation(m * n * 4)
+        buf = np.empty(GiB // 4, dtype=np.float32)
+        for alloc, seed in ((a, 11), (b, 12)):
+            for e0 in range(0, m * k, buf.size):
+                synth.synth_fill_uniform(buf.ctypes.data_as(fp), buf.size, seed, e0)
+                alloc.write(buf, offset=e0 * 4)
+        log(f"{m}^3 random: operands built ({time.perf_counter() - t:.1f} s)")
+        plan = xv.GemmPlan(s, xv.matrix(a, m, k, m), xv.matrix(b, n, k, n), xv.matrix(c, m, n, m),
+                           abi.OP_N, abi.OP_T)
+        info = plan.info()
+        assert (info.tile_m, info.tile_n) == (8192, 8192)
+        t = time.perf_counter()
+        plan.execute()
+        log(f"{m}^3 random: executed in {time.perf_counter() - t:.2f} s")
+        plan.release()
+
+        def read_columns(j0, j1):
+            out = np.empty((j1 - j0) * m, dtype=np.float32)
+            c.read_into(out, offset=j0 * m * 4)
+            return out.reshape(j1 - j0, m).T
+
+        t = time.perf_counter()
+        res = spread_check(SeededOperand(11, m, k, False), SeededOperand(12, n, k, True),
+                           read_columns, info.tile_m, info.tile_n, seed=65536, randoms=1024)
+        log(f"{m}^3 random: {res['elements']} elements checked ({time.perf_counter() - t:.1f} s): "
+            f"columns {res['full_columns']}, rows {res['full_rows']}, violations "
+            f"{res['violations']}, err/bound {res['max_err_over_bound']:.3e}")
+        assert len(res["full_columns"]) == m // info.tile_n
+        assert len(res["full_rows"]) == m // info.tile_m
+        assert res["violations"] == 0
+    finally:
+        s.close()
+        t = s.telemetry()
+        assert t.mappings == t.unmaps and t.physical_handles_created == t.physical_handles_released
         s.release()
