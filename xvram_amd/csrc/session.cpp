@@ -57,18 +57,37 @@ xvram_operation_info_v1 Operation::snapshot() const {
   return info;
 }
 
-bool Operation::settled_within(uint64_t timeout_ms) const {
-  if (timeout_ms == XVRAM_TIMEOUT_INFINITE) {
-    settled_.wait();
-    return true;
+// Callers mostly wait for an operation right after submitting it, and many
+// operations (a resident GEMM, a transaction) end within a few milliseconds.
+// Watching the phase word for that long sees the end without a blocked
+// thread's sleep and wake-up (tens of microseconds per operation on a busy
+// host); a longer wait then blocks on the promise.
+constexpr auto kWatchBeforeBlocking = std::chrono::milliseconds(2);
+
+bool Operation::ends_within(Clock::duration limit) const {
+  const Clock::time_point until = Clock::now() + limit;
+  for (unsigned i = 1;; ++i) {
+    if (terminal(phase_.load(std::memory_order_acquire))) return true;
+    if (i % 64 == 0 && Clock::now() >= until) return false;
+    __builtin_ia32_pause();
   }
+}
+
+bool Operation::settled_within(uint64_t timeout_ms) const {
   // Waits longer than the clock can express are waits without bound.
   constexpr uint64_t kLongest = uint64_t{1} << 40; // ~35 years
-  if (timeout_ms >= kLongest) {
+  const bool bounded = timeout_ms != XVRAM_TIMEOUT_INFINITE && timeout_ms < kLongest;
+  const auto watch = bounded ? std::min<Clock::duration>(kWatchBeforeBlocking,
+                                                         std::chrono::milliseconds(timeout_ms))
+                             : Clock::duration(kWatchBeforeBlocking);
+  // A terminal phase is stored after the record and before the promise is set.
+  if (ends_within(watch)) return true;
+  if (!bounded) {
     settled_.wait();
     return true;
   }
-  return settled_.wait_for(std::chrono::milliseconds(timeout_ms)) == std::future_status::ready;
+  return settled_.wait_for(std::chrono::milliseconds(timeout_ms) - watch) ==
+         std::future_status::ready;
 }
 
 Error Operation::cancel() {
@@ -246,18 +265,36 @@ void Session::worker() {
     exit_promise_.set_value();
     return;
   }
+  uint64_t taken = 0;
   for (bool running = true; running;) {
     Job job;
+    await_job(taken);
     {
-      std::unique_lock<std::mutex> lock(jobs_mutex_);
-      jobs_ready_.wait(lock, [this]() { return !jobs_.empty(); });
+      std::lock_guard<std::mutex> lock(jobs_mutex_);
       job = std::move(jobs_.front());
       jobs_.pop_front();
     }
+    ++taken;
     running = !job.shutdown;
     execute(job);
   }
   exit_promise_.set_value();
+}
+
+// A caller that waited for one operation usually submits the next within
+// microseconds: the worker watches the queue counter for a short while before
+// it sleeps, so such a job starts without a wake-up.
+void Session::await_job(uint64_t taken) {
+  constexpr auto kWatch = std::chrono::microseconds(500);
+  const Clock::time_point until = Clock::now() + kWatch;
+  for (unsigned i = 1; jobs_pushed_.load(std::memory_order_acquire) == taken; ++i) {
+    if (i % 64 == 0 && Clock::now() >= until) {
+      std::unique_lock<std::mutex> lock(jobs_mutex_);
+      jobs_ready_.wait(lock, [this]() { return !jobs_.empty(); });
+      return;
+    }
+    __builtin_ia32_pause();
+  }
 }
 
 void Session::execute(Job& job) {
@@ -289,6 +326,7 @@ Error Session::enqueue(std::function<Error(Operation&)> body, uint64_t units, ui
       return make_error(XVRAM_STATUS_CLOSED, "session", "submit",
                         "the session is closed or closing; nothing more can be queued");
     jobs_.push_back(Job{op, std::move(body), std::move(gemm), false});
+    jobs_pushed_.fetch_add(1, std::memory_order_release);
   }
   jobs_ready_.notify_one();
   out = std::move(op);
@@ -579,6 +617,7 @@ Error Session::close(uint64_t timeout_ms) {
     setup_error = setup_error_;
     if (!setup_failed && !sealed_ && worker_started_) {
       jobs_.push_back(Job{shutdown_, {}, nullptr, true});
+      jobs_pushed_.fetch_add(1, std::memory_order_release);
       jobs_ready_.notify_one();
     }
     sealed_ = true;

@@ -70,6 +70,8 @@ public:
 private:
   void publish(xvram_operation_state terminal, const Error& result, double elapsed_ms,
                const OperationTraffic& traffic);
+  // True if the phase turns terminal within `limit` of watching it.
+  bool ends_within(Clock::duration limit) const;
 
   const uint64_t id_;
   const uint64_t units_total_;
@@ -174,6 +176,9 @@ private:
   // The plan of the job queued first, if it is a GEMM whose operands are live.
   std::shared_ptr<GemmPlanRecord> gemm_queued_next() const;
   void worker();
+  // Returns once a job is queued: watches jobs_pushed_ for a short while after
+  // the last job, then sleeps on jobs_ready_.
+  void await_job(uint64_t taken);
   void execute(Job& job);
   void publish_telemetry();
   bool join_worker(uint64_t timeout_ms);
@@ -192,6 +197,7 @@ private:
   mutable std::mutex jobs_mutex_;
   std::condition_variable jobs_ready_;
   std::deque<Job> jobs_;
+  std::atomic<uint64_t> jobs_pushed_{0}; // jobs ever queued (the idle worker watches it)
   bool sealed_ = false;          // no more jobs; the shutdown job is queued
   bool setup_failed_ = false;
   Error setup_error_;
