@@ -398,6 +398,8 @@ static_assert(4 * (kAhead - 2) == 20, "steady-state wait below");
 struct RingSource {
   __amdgpu_buffer_rsrc_t a, b;
   int base;
+  int count = 0;  // sgemm_ring8_kernel: K slots of this panel
+  int rotate = 0; // sgemm_ring8_kernel: slot loaded first (< count)
 };
 
 template <bool kTwo>
@@ -608,9 +610,11 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
 // Used only for launches whose tiles are all interior (m and n multiples of
 // 256) and whose K is a multiple of 8: every load then stays inside the
 // tile's lines and the K extent, so no predication is needed.
-constexpr int kRing8 = 4;     // slots per wave
-constexpr int kSlotK = 8;     // k values per slot
-constexpr int kHalf8 = 1024;  // floats of one operand half per slot (128 x 8)
+constexpr int kRing8 = 4;       // slots per wave
+constexpr int kSlotK = 8;       // k values per slot
+constexpr int kHalf8 = 1024;    // floats of one operand half per slot (128 x 8)
+constexpr int kTurnClasses = 8; // rotated K order (op-T A): tile rows per cycle of turns
+constexpr int kTurnSlots = 8;   // slots between the turns of consecutive tile rows (256 B)
 static_assert(4 * kRing8 * 2 * kHalf8 * 4 <= 160 * 1024, "rings fit the LDS");
 static_assert(8 * kRing8 <= 63, "outstanding loads fit the vmcnt counter");
 static_assert(8 * kRing8 == 32, "two-panel launches split K at multiples of 32");
@@ -672,11 +676,25 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring8_kernel(Params p) {
     return kc ? panel_rsrc(x + (int64_t)e0 * ld, (uint32_t)((255 * ld + kk) * 4))
               : panel_rsrc(x + e0, (uint32_t)(((int64_t)kk * ld - e0) * 4));
   };
-  const RingSource lo{rsrc(p.a, p.lda, m0, k1, kAKC), rsrc(p.b, p.ldb, n0, k1, kBKC), 0};
+  // Rotated K order (op-T A): the tile row's slots are visited from slot
+  // `turn` on, wrapping within each panel, so tile rows on one XCD read their
+  // k-contiguous lines at different k. With a power-of-two lda every line of
+  // every tile row otherwise sits at the same offset modulo the L2's channel
+  // interleave at the same moment, which at 8192^3 T/N costs 3 % and at the
+  // split 16384 x 256 x 16384 launch 9 % against a padded lda; the tile rows
+  // sharing a tile column still read its lines within kTurnClasses *
+  // kTurnSlots slots of one another. Each tile sums its slots in one fixed
+  // order.
+  const int turn = kAKC ? (tile_m % kTurnClasses) * kTurnSlots : 0;
+  RingSource lo{rsrc(p.a, p.lda, m0, k1, kAKC), rsrc(p.b, p.ldb, n0, k1, kBKC), 0};
+  lo.count = kTwo ? q_split : slots;
+  lo.rotate = turn % lo.count;
   RingSource hi = lo;
   if constexpr (kTwo) {
     const int k2 = p.k - k1;
     hi = RingSource{rsrc(p.a2, p.lda, m0, k2, kAKC), rsrc(p.b2, p.ldb, n0, k2, kBKC), q_split};
+    hi.count = slots - q_split;
+    hi.rotate = turn % hi.count;
   }
   // Lane offsets of load I of a half in its panel's first slot: k-row 2I + h,
   // elements w + 4*lrow .. +3 (extent-contiguous), or line w + 4*lrow + I, k
@@ -699,7 +717,11 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring8_kernel(Params p) {
   // Load L (0..3: A, 4..7: B; load index L & 3) of slot q into ring slot S.
   auto issue = [&]<int S, int L>(int q, Int<S>, Int<L>, const RingSource& src) {
     constexpr int off = (S * 2 * kHalf8 + (L >> 2) * kHalf8 + (L & 3) * 256) * 4;
-    const uint32_t qq = (uint32_t)(q - src.base);
+    uint32_t qq = (uint32_t)(q - src.base);
+    if constexpr (kAKC) {
+      qq += (uint32_t)src.rotate;
+      if (qq >= (uint32_t)src.count) qq -= (uint32_t)src.count;
+    }
     if constexpr (L < 4) {
       const uint32_t so = __builtin_amdgcn_readfirstlane(adv_a * qq);
       load_lds16<off>(ring_lds, vo_a[L & 3], src.a, so);
