@@ -636,6 +636,7 @@ def main() -> int:
     m, n, k, op_a, op_b, budget, frame, desc = WORKLOADS[args.workload]
     if args.frame_mib:
         frame = args.frame_mib * MiB
+        desc += f"; frames of {args.frame_mib} MiB instead of the workload's"
     log(f"workload {args.workload}: {desc}")
     cfg = dict(chunk_size_bytes=frame)
     if budget:
