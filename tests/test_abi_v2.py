@@ -51,12 +51,22 @@ int main(void) {
     assert ctypes.sizeof(abi.ApiV2) == 464
 
 
-@pytest.fixture(params=[xv.PRODUCT_LIB, xv.HOSTSIM_LIB], ids=["product", "hostsim"])
-def v2(request):
-    lib = xv.Library(request.param)
+def v2_table(path):
+    lib = xv.Library(path)
     api = abi.ApiV2()
     assert lib.get_api(2, ctypes.sizeof(api), ctypes.byref(api)) == abi.SUCCESS
     return lib, api
+
+
+@pytest.fixture(params=[xv.PRODUCT_LIB, xv.HOSTSIM_LIB], ids=["product", "hostsim"])
+def v2(request):
+    return v2_table(request.param)
+
+
+@pytest.fixture()
+def v2_sim():
+    """Sessions need a device: the hostsim library provides one on the CPU."""
+    return v2_table(xv.HOSTSIM_LIB)
 
 
 def test_v2_table(v2):
@@ -79,10 +89,8 @@ def create_v2(api, cfg):
     return status, handle
 
 
-def test_v2_config_validation_and_modes(v2):
-    lib, api = v2
-    if lib.path != xv.HOSTSIM_LIB:
-        pytest.skip("session creation needs a device; the hostsim library provides one")
+def test_v2_config_validation_and_modes(v2_sim):
+    lib, api = v2_sim
     lib.dll.xvram_hostsim_reset()
     cfg = abi.session_config_v2_init()
     assert create_v2(api, cfg)[0] == abi.UNSUPPORTED          # the INIT default is ADAPTIVE
@@ -110,10 +118,8 @@ def test_v2_config_validation_and_modes(v2):
     assert create_v2(api, c)[0] == abi.INVALID_ARGUMENT
 
 
-def test_v2_disabled_session_and_telemetry(v2):
-    lib, api = v2
-    if lib.path != xv.HOSTSIM_LIB:
-        pytest.skip("session creation needs a device; the hostsim library provides one")
+def test_v2_disabled_session_and_telemetry(v2_sim):
+    lib, api = v2_sim
     lib.dll.xvram_hostsim_reset()
     cfg = abi.session_config_v2_init()
     cfg.compression_mode = abi.COMPRESSION_DISABLED
