@@ -7,7 +7,10 @@ memory the caller owns, enqueued on the caller's HIP stream, through the C ABI
   the same bits both ways, within the FP64 bound.
 * The config-5 launch shape in every form (4096 x 256 x 4096, 16 ranges) with
   alpha, beta and a per-row bias + ReLU: within the bound.
-* Shapes that do not split (256 tiles; ragged edges on the 256 x 128 kernel).
+* Shapes that do not split (256 tiles; K too shallow for two ranges).
+* Config 2's ragged shape (3001 x 2047 x 4099, alpha 1.5, beta 0.5): 12 x 16
+  tiles of 256 x 128 split into 2 ranges, with the library's workspace and
+  with the caller's: the same bits both ways, within the bound.
 * Inside a transaction callback, on the resolved addresses of a session's
   allocations and the callback's native_stream (the use the entry point is
   for): C read back through allocation_read.
@@ -185,12 +188,27 @@ def test_config5_launch_shape_with_epilogue(lib, hip, oracle_mod, form):
 
 
 @pytest.mark.parametrize("m,n,k,form", [(4096, 4096, 256, "NT"), (1000, 700, 300, "TN"),
-                                        (257, 1031, 517, "TT")])
+                                        (257, 1031, 500, "TT")])
 def test_unsplit_shapes(lib, hip, oracle_mod, m, n, k, form):
     outs, ref, absab = run_device_gemm(lib, hip, oracle_mod, m, n, k, FORMS[form], 521, beta=0.5)
     bad, _, ratio = oracle_mod.check_bound(np.asfortranarray(outs[0]), k, ref, absab)
     log(f"{m}x{n}x{k} {form}: violations {bad}, err/bound {ratio:.3e}")
     assert bad == 0
+
+
+@pytest.mark.parametrize("form", sorted(FORMS))
+def test_config2_ragged_split(lib, hip, oracle_mod, form):
+    m, n, k = 3001, 2047, 4099
+    outs, ref, absab = run_device_gemm(lib, hip, oracle_mod, m, n, k, FORMS[form], 541,
+                                       alpha=1.5, beta=0.5)
+    bad, _, ratio = oracle_mod.check_bound(np.asfortranarray(outs[0]), k, ref, absab)
+    log(f"config 2 {m}x{n}x{k} {form}, library workspace: violations {bad}, "
+        f"err/bound {ratio:.3e}")
+    assert bad == 0
+    # Two partials of 3004 x 2047 floats in a workspace of the caller's.
+    mine, _, _ = run_device_gemm(lib, hip, oracle_mod, m, n, k, FORMS[form], 541, alpha=1.5,
+                                 beta=0.5, workspace_bytes=2 * 3004 * 2047 * 4)
+    assert np.array_equal(mine[0].view(np.uint32), outs[0].view(np.uint32))
 
 
 def test_inside_a_transaction_callback(lib, oracle_mod):

@@ -17,6 +17,12 @@ the epilogue.
   T/N under 1 GiB frames: 64 tiles, 4 ranges of 4096): pattern bit-exact.
 * Config 1's shape (1024^3 N/N, 16 tiles, 4 ranges): every element within the
   FP64 bound.
+* Launches that are not whole 256 x 256 tiles split on the 256 x 128 kernel:
+  501 x 200 x 2048 (2 x 2 tiles, 8 ranges; partials of leading dimension 504)
+  bit-exact on the pattern in all four forms; 501 x 200 x 1000 (three ranges,
+  a K tail) with alpha, beta and a per-row or per-column bias + ReLU within the
+  bound, two executions bit-identical; config 2's shape (3001 x 2047 x 4099,
+  2 ranges) in all four forms with alpha 1.5, beta 0.5 within the bound.
 
 Tolerance: |C - C_ref| <= 4*K*2^-24*(|alpha||A||B| + |beta C0| + |bias|)_ij."""
 import ctypes
@@ -68,7 +74,8 @@ def closed(s):
 class Gemm:
     """op(A) m x k, op(B) k x n, C m x n column-major, stored per `ops`."""
 
-    def __init__(self, s, m, n, k, ops, alpha=1.0, beta=0.0, bias=None, relu=False):
+    def __init__(self, s, m, n, k, ops, alpha=1.0, beta=0.0, bias=None, relu=False,
+                 axis=abi.BIAS_PER_COLUMN):
         self.m, self.n, self.k, self.ops = m, n, k, ops
         self.a_shape = (m, k) if ops[0] == abi.OP_N else (k, m)
         self.b_shape = (k, n) if ops[1] == abi.OP_N else (n, k)
@@ -81,8 +88,7 @@ class Gemm:
             if bias is not None:
                 v = s.allocation(bias.nbytes)
                 v.write(bias)
-            ep = xv.epilogue(v, abi.BIAS_PER_COLUMN if v is not None else abi.BIAS_NONE,
-                             relu=relu)
+            ep = xv.epilogue(v, axis if v is not None else abi.BIAS_NONE, relu=relu)
         self.plan = xv.GemmPlan(s, xv.matrix(self.a, *self.a_shape, self.a_shape[0]),
                                 xv.matrix(self.b, *self.b_shape, self.b_shape[0]),
                                 xv.matrix(self.c, m, n, m), ops[0], ops[1], alpha, beta,
@@ -194,6 +200,87 @@ def test_split_config1_shape(lib, synth, oracle_mod):
         ref, absab = oracle_mod.sgemm_f64(np.asfortranarray(a_st), np.asfortranarray(b_st))
         bad, _, ratio = oracle_mod.check_bound(g.result(), k, ref, absab)
         log(f"1024^3 NN: violations {bad}, err/bound {ratio:.3e}")
+        assert bad == 0
+        g.plan.release()
+    finally:
+        closed(s)
+
+
+@pytest.mark.parametrize("form", sorted(FORMS))
+def test_ragged_split_pattern(lib, synth, oracle_mod, form):
+    m, n, k = 501, 200, 2048
+    s = xv.Session(lib, chunk_size_bytes=64 * MiB, cache_target_bytes=2 * GiB)
+    try:
+        g = Gemm(s, m, n, k, FORMS[form])
+        g.fill_pattern(synth)
+        g.execute()
+        got = g.result()
+        expect = oracle_mod.pattern_expected_matrix(m, n, k).astype(np.float32)
+        bad = int(np.count_nonzero(got != expect))
+        log(f"ragged pattern {m}x{n}x{k} {form}: {bad} of {m * n} differ")
+        assert bad == 0
+        g.plan.release()
+    finally:
+        closed(s)
+
+
+@pytest.mark.parametrize("axis", [abi.BIAS_PER_ROW, abi.BIAS_PER_COLUMN], ids=["row", "col"])
+@pytest.mark.parametrize("form", sorted(FORMS))
+def test_ragged_split_k_tail_beta_epilogue(lib, synth, oracle_mod, form, axis):
+    m, n, k = 501, 200, 1000
+    alpha, beta = 1.25, -0.5
+    length = m if axis == abi.BIAS_PER_ROW else n
+    bias = (oracle_mod.fill_uniform(length, 97) * 0.5).astype(np.float32)
+    s = xv.Session(lib, chunk_size_bytes=64 * MiB, cache_target_bytes=2 * GiB)
+    try:
+        g = Gemm(s, m, n, k, FORMS[form], alpha, beta, bias=bias, relu=True, axis=axis)
+        a_st, b_st = list(g.fill_uniform(synth, 98, 99))
+        c0 = np.empty(m * n, dtype=np.float32)
+        synth.synth_fill_uniform(c0.ctypes.data_as(FP), c0.size, 100, 0)
+        outs = []
+        for _ in range(2):
+            g.c.write(c0)
+            g.execute()
+            outs.append(g.result().copy())
+        assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+        a_op = a_st if FORMS[form][0] == abi.OP_N else a_st.T
+        b_op = b_st if FORMS[form][1] == abi.OP_N else b_st.T
+        ref, absab = oracle_mod.sgemm_f64(np.asfortranarray(a_op), np.asfortranarray(b_op),
+                                          alpha, beta, np.asfortranarray(c0.reshape(n, m).T))
+        badd = bias[:, None] if axis == abi.BIAS_PER_ROW else bias[None, :]
+        ref = np.maximum(ref + badd.astype(np.float64), 0.0)
+        absab = absab + np.abs(badd)
+        bad, _, ratio = oracle_mod.check_bound(outs[0], k, ref, absab)
+        log(f"ragged tail {m}x{n}x{k} {form} bias {'row' if length == m else 'col'}: "
+            f"violations {bad}, err/bound {ratio:.3e}")
+        assert bad == 0
+        g.plan.release()
+    finally:
+        closed(s)
+
+
+@pytest.mark.parametrize("form", sorted(FORMS))
+def test_config2_shape_split(lib, synth, oracle_mod, form):
+    """Config 2 (3001 x 2047 x 4099, alpha 1.5, beta 0.5) resident: one launch of
+    12 x 16 tiles of 256 x 128 that splits K into 2 ranges."""
+    m, n, k = 3001, 2047, 4099
+    alpha, beta = 1.5, 0.5
+    s = xv.Session(lib, chunk_size_bytes=64 * MiB, cache_target_bytes=2 * GiB)
+    try:
+        g = Gemm(s, m, n, k, FORMS[form], alpha, beta)
+        assert g.plan.info().tile_count == 1
+        a_st, b_st = list(g.fill_uniform(synth, 101, 102))
+        c0 = np.empty(m * n, dtype=np.float32)
+        synth.synth_fill_uniform(c0.ctypes.data_as(FP), c0.size, 103, 0)
+        g.c.write(c0)
+        g.execute()
+        got = g.result()
+        a_op = a_st if FORMS[form][0] == abi.OP_N else a_st.T
+        b_op = b_st if FORMS[form][1] == abi.OP_N else b_st.T
+        ref, absab = oracle_mod.sgemm_f64(np.asfortranarray(a_op), np.asfortranarray(b_op),
+                                          alpha, beta, np.asfortranarray(c0.reshape(n, m).T))
+        bad, _, ratio = oracle_mod.check_bound(np.asfortranarray(got), k, ref, absab)
+        log(f"config 2 {m}x{n}x{k} {form}: violations {bad}, err/bound {ratio:.3e}")
         assert bad == 0
         g.plan.release()
     finally:

@@ -1,16 +1,19 @@
 """CPU tests of split-K launches over libxvram_hostsim.so.
 
-A launch whose C has fewer 256 x 256 tiles than the chip has CUs cuts its K
-into ranges (kernels::split_k_plan: as many as fill one workgroup per CU, each
-at least 256 deep, in multiples of 32), accumulates each range into a partial
-held in one frame of the pool, and adds the partials in range order before
-alpha, beta and the epilogue. The simulated device performs exactly that data
-flow (partials written to and read back from the frame, which must be mapped)
-and counts the launches that split, so these tests check the planner's
-reservation of the frame, the executor's use of it, the split arithmetic
-(bit-exact analytic pattern, FP64 bound with K tails, beta and the epilogue)
-and that repeated runs give identical bits. The same launches on the GPU are
-in tests/test_gpu_split_k.py."""
+A launch that would leave workgroup slots idle cuts its K into ranges
+(kernels::split_k_shape: as many as fill the chip, each at least 256 deep, in
+multiples of 32), accumulates each range into a partial held in one frame of
+the pool (leading dimension m rounded up to 4), and adds the partials in range
+order before alpha, beta and the epilogue. Launches of interior 256 x 256 tiles
+split on the ring kernels (one workgroup per CU); the others on the 256 x 128
+kernel (two per CU). The simulated device performs exactly that data flow
+(partials written to and read back from the frame, which must be mapped) and
+counts the launches that split, so these tests check the rule itself (through
+the library's own split_k_shape), the planner's reservation of the frame, the
+executor's use of it, the split arithmetic (bit-exact analytic pattern, FP64
+bound with K tails, beta and the epilogue, ragged m and n) and that repeated
+runs give identical bits. The same launches on the GPU are in
+tests/test_gpu_split_k.py."""
 import ctypes
 
 import numpy as np
@@ -36,13 +39,19 @@ def sim():
     lib.dll.xvram_hostsim_reset()
 
 
+def narrow_splits(lib):
+    lib.dll.xvram_hostsim_narrow_split_launches.restype = ctypes.c_uint64
+    return lib.dll.xvram_hostsim_narrow_split_launches()
+
+
 def split_stats(lib):
     last = ctypes.c_int(0)
     count = lib.dll.xvram_hostsim_split_launches(ctypes.byref(last))
     return count, last.value
 
 
-def run(s, a_op, b_op, ops, c0=None, alpha=1.0, beta=0.0, bias=None, relu=False, repeat=1):
+def run(s, a_op, b_op, ops, c0=None, alpha=1.0, beta=0.0, bias=None, relu=False, repeat=1,
+        axis=abi.BIAS_PER_COLUMN):
     m, k = a_op.shape
     n = b_op.shape[1]
     a_st = a_op if ops[0] == abi.OP_N else a_op.T
@@ -59,7 +68,7 @@ def run(s, a_op, b_op, ops, c0=None, alpha=1.0, beta=0.0, bias=None, relu=False,
         if bias is not None:
             V = s.allocation(bias.nbytes)
             V.write(bias)
-        ep = xv.epilogue(V, abi.BIAS_PER_COLUMN if V is not None else abi.BIAS_NONE, relu=relu)
+        ep = xv.epilogue(V, axis if V is not None else abi.BIAS_NONE, relu=relu)
     plan = xv.GemmPlan(s, xv.matrix(A, *a_st.shape, lda), xv.matrix(B, *b_st.shape, ldb),
                        xv.matrix(C, m, n, ldc), ops[0], ops[1], alpha, beta, epilogue=ep)
     outs = []
@@ -124,15 +133,92 @@ def test_split_across_k_panels(sim, oracle_mod):
     assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))
 
 
-def test_no_split_when_k_is_shallow_or_tiles_fill_the_chip(sim, oracle_mod):
-    """K = 384 leaves fewer than two ranges of 256; ragged C (m = 500) is not
-    a whole number of 256 x 256 tiles: both run unsplit."""
-    for m, n, k in ((512, 256, 384), (500, 256, 2048)):
-        a_op, b_op = pattern_operands(m, n, k)
-        with session(sim) as s:
-            (out,), _ = run(s, a_op, b_op, FORMS["NN"])
-        assert split_stats(sim)[0] == 0
-        assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))
+def test_no_split_when_k_is_shallow(sim, oracle_mod):
+    """K = 384 leaves fewer than two ranges of 256: unsplit."""
+    m, n, k = 512, 256, 384
+    a_op, b_op = pattern_operands(m, n, k)
+    with session(sim) as s:
+        (out,), _ = run(s, a_op, b_op, FORMS["NN"])
+    assert split_stats(sim)[0] == 0
+    assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))
+
+
+MiB_ = 1 << 20
+
+
+@pytest.mark.parametrize("m,n,k,nt,ring,ws,expect", [
+    # the C5 chain's launch: 16 tiles of 256 x 256 -> 16 ranges of 256 (ring kernels)
+    (4096, 256, 4096, False, True, 64 * MiB_, (16, 256, 0)),
+    # the resident C5 layer: 64 tiles -> 4 ranges of 4096
+    (16384, 256, 16384, False, True, 1 << 30, (4, 4096, 0)),
+    # config 1: 16 tiles; K / 256 limits it to 4 ranges
+    (1024, 1024, 1024, False, True, 64 * MiB_, (4, 256, 0)),
+    # config 2: ragged, 12 x 16 tiles of 256 x 128 -> 2 ranges on the 256 x 128 kernel
+    (3001, 2047, 4099, False, True, 64 * MiB_, (2, 2080, 1)),
+    # 256 tiles of 256 x 256 fill the chip
+    (4096, 4096, 4096, True, True, 64 * MiB_, (1, 0, 0)),
+    # ragged, but 17 x 16 tiles of 256 x 256: the general 256 x 256 kernel, unsplit
+    (4100, 4096, 4096, True, True, 64 * MiB_, (1, 0, 0)),
+    # interior but K not a multiple of 8 (N/N): the 256 x 128 kernel; N/T splits on the ring
+    (1024, 1024, 1004, False, True, 64 * MiB_, (3, 352, 1)),
+    (1024, 1024, 1004, True, True, 64 * MiB_, (3, 352, 0)),
+    # operand panels the ring kernels cannot address: the 256 x 128 kernel
+    (1024, 1024, 1024, False, False, 64 * MiB_, (4, 256, 1)),
+    # the workspace holds 3 partials: 3 ranges; 1 partial: unsplit
+    (4096, 256, 4096, False, True, 12 * MiB_, (3, 1376, 0)),
+    (4096, 256, 4096, False, True, 4 * MiB_, (1, 0, 0)),
+    # partials of m rounded up to 4: 501 x 200 -> ld 504
+    (501, 200, 2048, False, True, 8 * 504 * 200 * 4, (8, 256, 1)),
+    (501, 200, 2048, False, True, 8 * 504 * 200 * 4 - 1, (7, 320, 1)),
+])
+def test_split_rule(sim, m, n, k, nt, ring, ws, expect):
+    fn = sim.dll.xvram_hostsim_split_shape
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                   ctypes.c_uint64, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]
+    depth, narrow = ctypes.c_int(0), ctypes.c_int(0)
+    splits = fn(m, n, k, int(nt), int(ring), ws, ctypes.byref(depth), ctypes.byref(narrow))
+    assert (splits, depth.value, narrow.value) == expect
+
+
+@pytest.mark.parametrize("form", sorted(FORMS))
+def test_ragged_split_pattern_is_exact(sim, oracle_mod, form):
+    """501 x 200 x 2048: not whole 256 x 256 tiles, so the 256 x 128 kernel's
+    2 x 2 tiles split K into 8 ranges of 256; the partials' leading dimension
+    is 504 (m rounded up to 4) and the reduction's last quad of each column
+    holds one row."""
+    m, n, k = 501, 200, 2048
+    a_op, b_op = pattern_operands(m, n, k)
+    with session(sim) as s:
+        (out,), info = run(s, a_op, b_op, FORMS[form])
+    assert info.tile_count == 1
+    assert split_stats(sim) == (1, 8) and narrow_splits(sim) == 1
+    assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))
+
+
+@pytest.mark.parametrize("axis", [abi.BIAS_PER_ROW, abi.BIAS_PER_COLUMN], ids=["row", "col"])
+@pytest.mark.parametrize("form", sorted(FORMS))
+def test_ragged_split_with_k_tail_beta_and_epilogue(sim, oracle_mod, form, axis):
+    """501 x 200 x 1000 on the 256 x 128 kernel: three ranges (352, 352, 296),
+    alpha, beta and a per-row or per-column bias with ReLU after the
+    reduction. Within the FP64 bound, and the same bits on every run."""
+    m, n, k = 501, 200, 1000
+    a_op = uniform(oracle_mod, m, k, 81)
+    b_op = uniform(oracle_mod, k, n, 82)
+    c0 = uniform(oracle_mod, m, n, 83)
+    length = m if axis == abi.BIAS_PER_ROW else n
+    bias = (oracle_mod.fill_uniform(length, 84) * 0.5).astype(np.float32)
+    with session(sim) as s:
+        outs, _ = run(s, a_op, b_op, FORMS[form], c0, alpha=1.25, beta=-0.5, bias=bias,
+                      relu=True, repeat=2, axis=axis)
+    assert split_stats(sim) == (2, 3) and narrow_splits(sim) == 2
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    a64, b64 = a_op.astype(np.float64), b_op.astype(np.float64)
+    badd = bias[:, None] if axis == abi.BIAS_PER_ROW else bias[None, :]
+    ref = np.maximum(1.25 * (a64 @ b64) - 0.5 * c0 + badd, 0.0)
+    absab = 1.25 * (np.abs(a64) @ np.abs(b64)) + 0.5 * np.abs(c0) + np.abs(badd)
+    bound = 4 * k * 2.0 ** -24 * absab + 1e-30
+    assert np.all(np.abs(outs[0] - ref) <= bound)
 
 
 def test_split_frame_is_returned_to_the_pool(sim, oracle_mod):

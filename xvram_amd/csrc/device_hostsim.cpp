@@ -60,8 +60,9 @@ struct SimState {
   uint64_t free_bytes = 16ull << 30;
   uint64_t total_bytes = 16ull << 30;
   uint64_t kernel_launches = 0;
-  uint64_t split_launches = 0; // launches that split K (kernels::split_k_plan)
-  int last_splits = 0;         // K ranges of the last split launch
+  uint64_t split_launches = 0;  // launches that split K (kernels::split_k_plan)
+  uint64_t narrow_splits = 0;   // of those, split on the 256 x 128 kernel
+  int last_splits = 0;          // K ranges of the last split launch
   int device_count = 1;       // simulated devices 0 .. device_count-1
   int current_device = 0;     // what the calling thread sees as current (-1: none)
   int last_init_ordinal = -1; // the device the last session set up on
@@ -283,9 +284,10 @@ public:
       return kSimBadAccess;
     // A split launch writes its partials to the workspace (sgemm_launch.hpp).
     const kernels::SplitK sk = two ? kernels::SplitK{} : kernels::split_k_plan(l);
-    const int64_t mn = int64_t{l.m} * l.n;
+    const int64_t ldp = kernels::split_partial_ld(l.m);
+    const int64_t partial = ldp * l.n;
     if (sk.splits > 1 && !accessible(reinterpret_cast<uint64_t>(l.workspace),
-                                     static_cast<uint64_t>(sk.splits * mn * 4)))
+                                     static_cast<uint64_t>(sk.splits * partial * 4)))
       return kSimBadAccess;
     // Events attached to the dispatch are stamped around the kernel itself.
     if (l.start_event) recorded_[l.start_event] = std::chrono::steady_clock::now();
@@ -297,7 +299,7 @@ public:
     for (int64_t j = 0; j < l.n; ++j) {
       std::fill(acc.begin(), acc.end(), 0.f);
       for (int s = 0; s < sk.splits && sk.splits > 1; ++s) {
-        float* part = l.workspace + s * mn + j * l.m;
+        float* part = l.workspace + s * partial + j * ldp;
         std::fill(part, part + l.m, 0.f);
         const int64_t p_end = std::min<int64_t>(l.k, int64_t{s + 1} * sk.depth);
         for (int64_t p = int64_t{s} * sk.depth; p < p_end; ++p) {
@@ -335,6 +337,7 @@ public:
     ++g_sim.kernel_launches;
     if (sk.splits > 1) {
       ++g_sim.split_launches;
+      if (sk.narrow) ++g_sim.narrow_splits;
       g_sim.last_splits = sk.splits;
     }
     return 0;
@@ -446,6 +449,7 @@ extern "C" __attribute__((visibility("default"))) void xvram_hostsim_reset() {
   g_sim.free_bytes = g_sim.total_bytes = 16ull << 30;
   g_sim.kernel_launches = 0;
   g_sim.split_launches = 0;
+  g_sim.narrow_splits = 0;
   g_sim.last_splits = 0;
   g_sim.device_count = 1;
   g_sim.current_device = 0;
@@ -485,6 +489,27 @@ extern "C" __attribute__((visibility("default"))) uint64_t xvram_hostsim_split_l
   std::lock_guard<std::mutex> lock(g_sim.mutex);
   if (last_splits != nullptr) *last_splits = g_sim.last_splits;
   return g_sim.split_launches;
+}
+
+// The split rule itself (kernels::split_k_shape) for a launch shape: returns
+// the number of K ranges (1 = unsplit), their depth and whether they run on
+// the 256 x 128 kernel.
+extern "C" __attribute__((visibility("default"))) int xvram_hostsim_split_shape(
+    int64_t m, int64_t n, int64_t k, int nt, int ring, uint64_t workspace_bytes, int* depth,
+    int* narrow) {
+  const xvram::kernels::SplitK sk =
+      xvram::kernels::split_k_shape(m, n, k, nt != 0, ring != 0, workspace_bytes);
+  if (depth != nullptr) *depth = sk.depth;
+  if (narrow != nullptr) *narrow = sk.narrow ? 1 : 0;
+  return sk.splits;
+}
+
+// Of those, the launches whose ranges ran on the 256 x 128 kernel (tiles that
+// are not all interior 256 x 256 ones).
+extern "C" __attribute__((visibility("default"))) uint64_t xvram_hostsim_narrow_split_launches() {
+  using namespace xvram;
+  std::lock_guard<std::mutex> lock(g_sim.mutex);
+  return g_sim.narrow_splits;
 }
 
 extern "C" __attribute__((visibility("default"))) uint64_t xvram_hostsim_kernel_launches() {

@@ -413,13 +413,14 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   out.tiles_m = ceil_div(p.m, tm);
   out.tiles_n = ceil_div(p.n, tn);
   out.panels_k = ceil_div(p.k, bk);
-  // A launch of fewer 256 x 256 tiles than CUs splits its K, its partials in
+  // A launch that leaves workgroup slots idle splits its K, its partials in
   // one frame of the pool (kernels::split_k_shape for the plan's tile and
-  // panel): that frame is taken from the schedule's.
+  // panel; its panels are below 2^31 bytes): that frame is taken from the
+  // schedule's.
   out.scratch = frame_count >= 4 &&
                 kernels::split_k_shape(static_cast<int64_t>(tm), static_cast<int64_t>(tn),
                                        static_cast<int64_t>(bk), !p.a.transposed && p.b.transposed,
-                                       F).splits > 1;
+                                       true, F).splits > 1;
   if (out.scratch) --frame_count;
 
   // Lookahead: launches whose panels are acquired (and pinned) before they are

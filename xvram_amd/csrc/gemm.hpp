@@ -138,7 +138,7 @@ struct GemmPlanData {
   uint64_t frames_in_use = 0;              // frames the schedule keeps busy at once
   int lanes = 1;                           // compute lanes the launches alternate over
   uint32_t panels_per_launch = 1;          // K panels one launch covers (1 or 2)
-  // Launches of fewer 256 x 256 tiles than CUs split K (kernels::split_k_plan)
+  // Launches that leave workgroup slots idle split K (kernels::split_k_plan)
   // into partials held in one frame of the pool, taken for the operation.
   bool scratch = false;
   std::vector<TileLaunch> launches;

@@ -28,9 +28,9 @@ struct Params {
   const float* a2;
   const float* b2;
   int k_split;
-  // Split K (ring kernels only): splits > 1 cuts K into ranges of
-  // split_depth; blockIdx.x covers tiles x splits and each workgroup stores
-  // its range's raw sums to partial + split * m * n (column-major, ld = m).
+  // Split K: splits > 1 cuts K into ranges of split_depth; blockIdx.x covers
+  // tiles x splits and each workgroup stores its range's raw sums to partial
+  // `split` (column-major, ld = m rounded up to 4; partial_target).
   int splits;
   int split_depth;
   float* partial;
@@ -111,12 +111,17 @@ __device__ __forceinline__ void narrow_to_split(Params& p, int split, bool a_kco
   p.k = min(p.split_depth, p.k - k0);
 }
 
+// Leading dimension of the partials of a split launch (sgemm_launch.hpp's
+// split_partial_ld): m rounded up to 4, so every column is 16-byte aligned.
+__host__ __device__ __forceinline__ int64_t partial_ld(int m) { return ((int64_t)m + 3) / 4 * 4; }
+
 // Where a workgroup of a split launch stores its raw sums: its range's
-// partial (ld = m) with alpha 1, beta 0 and no epilogue (1 * x is exact).
+// partial (ld = partial_ld(m)) with alpha 1, beta 0 and no epilogue (1 * x
+// is exact).
 __device__ __forceinline__ Params partial_target(const Params& p, int split) {
   Params o = p;
-  o.c = p.partial + (int64_t)split * p.m * p.n;
-  o.ldc = p.m;
+  o.ldc = partial_ld(p.m);
+  o.c = p.partial + (int64_t)split * o.ldc * p.n;
   o.alpha = 1.f;
   o.beta = 0.f;
   o.bias_row = nullptr;

@@ -21,15 +21,19 @@
 // spanning less than 2^31 bytes from its base (two_panel_valid below);
 // anything else returns hipErrorInvalidValue.
 //
-// Split K (optional, workspace set): a launch whose C has fewer 256 x 256
-// tiles than the chip has CUs (m and n multiples of 256, K a multiple of 4
-// for N/T and of 8 for the other forms, one K panel) may cut its K into
-// ranges (split_k_plan below), one workgroup per tile and range; each stores
-// the raw partial sums of its range to the workspace (`splits` dense m x n
-// column-major matrices), and a second kernel adds them in range order and
-// applies alpha, beta and the epilogue. The order of the additions is fixed,
-// so C is the same from run to run. Without a workspace large enough for two
-// partials the launch runs unsplit.
+// Split K (optional, workspace set): a launch that would leave CUs idle may
+// cut its K into ranges (split_k_plan below), one workgroup per tile and
+// range; each stores the raw partial sums of its range to the workspace
+// (`splits` column-major m x n matrices, leading dimension m rounded up to 4,
+// split_partial_ld), and a second kernel adds them in range order and applies
+// alpha, beta and the epilogue. Launches whose tiles are all interior 256 x
+// 256 tiles (m and n multiples of 256, K a multiple of 4 for N/T and of 8 for
+// the other forms) split on the ring kernels when they have fewer tiles than
+// the chip has CUs; other launches with fewer than 256 tiles of 256 x 256
+// split on the 256 x 128 kernel (two workgroups per CU) when they have fewer
+// of its tiles than it has slots. The order of the additions is fixed, so C
+// is the same from run to run. Without a workspace large enough for two
+// partials the launch runs unsplit. One K panel only.
 //
 // start_event / stop_event (hipEvent_t, optional) are recorded by the dispatch
 // itself (hipExtLaunchKernelGGL): no separate marker packets run between
@@ -73,21 +77,37 @@ constexpr int64_t kComputeUnits = 256;
 constexpr int64_t kSplitMinDepth = 256;
 
 struct SplitK {
-  int splits = 1; // 1 = not split
-  int depth = 0;  // K per range (multiple of 32); the last range holds the rest
+  int splits = 1;      // 1 = not split
+  int depth = 0;       // K per range (multiple of 32); the last range holds the rest
+  bool narrow = false; // the ranges run on the 256 x 128 kernel (else the ring kernels)
 };
+
+// Leading dimension of a split launch's partials: m rounded up to 4 floats,
+// so every column starts 16-byte aligned.
+inline int64_t split_partial_ld(int64_t m) { return (m + 3) / 4 * 4; }
 
 // The split of an m x n x k launch of form `nt` (A op N, B op T) or not,
 // given a workspace of `workspace_bytes` (see "Split K" above): as many ranges
-// as fill one workgroup per CU, each at least kSplitMinDepth deep, at most as
-// many partials as the workspace holds.
-inline SplitK split_k_shape(int64_t m, int64_t n, int64_t k, bool nt, uint64_t workspace_bytes) {
-  if (m <= 0 || n <= 0 || k <= 0 || m % 256 != 0 || n % 256 != 0 || k % (nt ? 4 : 8) != 0)
-    return {};
-  const int64_t tiles = (m / 256) * (n / 256);
-  if (tiles >= kComputeUnits) return {};
-  const int64_t partial = m * n * 4;
-  int64_t s = kComputeUnits / tiles;
+// as fill the chip's workgroup slots, each at least kSplitMinDepth deep, at
+// most as many partials as the workspace holds. `ring` = the ring kernels can
+// address the operand panels (each spans less than 2^31 bytes).
+inline SplitK split_k_shape(int64_t m, int64_t n, int64_t k, bool nt, bool ring,
+                            uint64_t workspace_bytes) {
+  if (m <= 0 || n <= 0 || k <= 0) return {};
+  const bool interior = ring && m % 256 == 0 && n % 256 == 0 && k % (nt ? 4 : 8) == 0;
+  int64_t tiles = 0, slots = 0;
+  if (interior) {
+    tiles = (m / 256) * (n / 256);
+    slots = kComputeUnits;
+  } else {
+    // At least one 256 x 256 tile per CU runs a 256 x 256 kernel unsplit.
+    if (((m + 255) / 256) * ((n + 255) / 256) >= kComputeUnits) return {};
+    tiles = ((m + 255) / 256) * ((n + 127) / 128);
+    slots = 2 * kComputeUnits;
+  }
+  if (tiles >= slots) return {};
+  const int64_t partial = split_partial_ld(m) * n * 4;
+  int64_t s = slots / tiles;
   if (k / kSplitMinDepth < s) s = k / kSplitMinDepth;
   if (static_cast<int64_t>(workspace_bytes / partial) < s)
     s = static_cast<int64_t>(workspace_bytes / partial);
@@ -96,20 +116,19 @@ inline SplitK split_k_shape(int64_t m, int64_t n, int64_t k, bool nt, uint64_t w
   const int64_t depth32 = (depth + 31) / 32 * 32;
   const int64_t splits = (k + depth32 - 1) / depth32;
   if (splits < 2) return {};
-  return SplitK{static_cast<int>(splits), static_cast<int>(depth32)};
+  return SplitK{static_cast<int>(splits), static_cast<int>(depth32), !interior};
 }
 
 // The split a launch takes given room for `workspace_bytes` of partials: none
-// for a two-panel launch or one whose operand panels do not each span less
-// than 2^31 bytes (the ring kernels' 32-bit buffer offsets), else
-// split_k_shape.
+// for a two-panel launch, else split_k_shape (on the ring kernels only when
+// each operand panel spans less than 2^31 bytes, their 32-bit buffer offsets).
 inline SplitK split_k_for(const SgemmLaunch& l, uint64_t workspace_bytes) {
   constexpr int64_t kLimit = int64_t(1) << 31;
   if (l.a2 != nullptr || l.b2 != nullptr) return {};
   const int64_t a_bytes = (l.a_kcontig ? int64_t{l.m} : int64_t{l.k}) * l.lda * 4;
   const int64_t b_bytes = (l.b_ncontig ? int64_t{l.k} : int64_t{l.n}) * l.ldb * 4;
-  if (a_bytes >= kLimit || b_bytes >= kLimit) return {};
-  return split_k_shape(l.m, l.n, l.k, !l.a_kcontig && l.b_ncontig, workspace_bytes);
+  return split_k_shape(l.m, l.n, l.k, !l.a_kcontig && l.b_ncontig,
+                       a_bytes < kLimit && b_bytes < kLimit, workspace_bytes);
 }
 
 // The split of one launch with its own 16-byte aligned workspace.
@@ -122,7 +141,9 @@ inline SplitK split_k_plan(const SgemmLaunch& l) {
 // limit (0: it does not split).
 inline uint64_t split_k_bytes_wanted(const SgemmLaunch& l) {
   const SplitK sk = split_k_for(l, ~uint64_t{0});
-  return sk.splits > 1 ? static_cast<uint64_t>(sk.splits) * uint64_t(l.m) * uint64_t(l.n) * 4 : 0;
+  return sk.splits > 1
+             ? static_cast<uint64_t>(sk.splits) * uint64_t(split_partial_ld(l.m)) * uint64_t(l.n) * 4
+             : 0;
 }
 
 // Enqueues the launch on `stream` (a hipStream_t); returns a hipError_t.

@@ -57,6 +57,7 @@ namespace xvram::kernels {
 int wide_tile();
 hipError_t launch_wide(const device::Params& p, bool a_kcontig, bool b_ncontig,
                        hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+hipError_t launch_splitk_reduce(const device::Params& p, hipStream_t stream, hipEvent_t stop);
 
 namespace {
 
@@ -169,8 +170,15 @@ __global__ __launch_bounds__(kThreads, 2) void sgemm_mfma_kernel(Params p) {
   __shared__ __attribute__((aligned(16))) float lds_a[2][kStageK * kPitchA];
   __shared__ __attribute__((aligned(16))) float lds_b[2][kStageK * kPitchN];
 
-  int tile_m, tile_n;
-  tile_coords<kGroupM>(p, tile_m, tile_n);
+  // A split launch (p.splits > 1): each workgroup multiplies one K range of
+  // its tile into that range's partial (sgemm_device.hpp).
+  int tile_m, tile_n, split = 0;
+  if (p.splits > 1) {
+    split = split_coords<kGroupM>(p, tile_m, tile_n);
+    narrow_to_split(p, split, AK, !BN);
+  } else {
+    tile_coords<kGroupM>(p, tile_m, tile_n);
+  }
   const int m0 = tile_m * kTileM;
   const int n0 = tile_n * kTileN;
   const int tid = threadIdx.x;
@@ -263,12 +271,13 @@ __global__ __launch_bounds__(kThreads, 2) void sgemm_mfma_kernel(Params p) {
     mfmas((kSteps - 1) & 1);
   }
 
-  store_c_tile<2, false>(p, acc, m0 + wm, n0 + wn, lrow, lhalf);
+  if (p.splits > 1) store_c_tile<2, false>(partial_target(p, split), acc, m0 + wm, n0 + wn, lrow, lhalf);
+  else store_c_tile<2, false>(p, acc, m0 + wm, n0 + wn, lrow, lhalf);
 }
 
 template <bool AK, bool BN>
 hipError_t launch_variant(const Params& p, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
-  const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
+  const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n * p.splits));
   hipExtLaunchKernelGGL((sgemm_mfma_kernel<AK, BN>), grid, dim3(kThreads), 0, stream, start, stop,
                         0, p);
   return hipGetLastError();
@@ -337,15 +346,27 @@ int launch_sgemm(const SgemmLaunch& launch, void* stream) {
     return static_cast<int>(launch_wide(p, launch.a_kcontig, launch.b_ncontig, s, e0, e1));
   }
   p.k_split = 0;
-  // Fewer tiles than CUs: split K when a workspace is given (fixed-order
-  // reduction; sgemm_launch.hpp).
+  // Fewer tiles than workgroup slots: split K when a workspace is given
+  // (fixed-order reduction; sgemm_launch.hpp), on the ring kernels for
+  // interior 256 x 256 tiles, else on the 256 x 128 kernel.
   if (const SplitK sk = split_k_plan(launch); sk.splits > 1) {
-    p.tiles_m = launch.m / wide_tile();
-    p.tiles_n = launch.n / wide_tile();
     p.splits = sk.splits;
     p.split_depth = sk.depth;
     p.partial = launch.workspace;
-    return static_cast<int>(launch_wide(p, launch.a_kcontig, launch.b_ncontig, s, e0, e1));
+    if (!sk.narrow) {
+      p.tiles_m = launch.m / wide_tile();
+      p.tiles_n = launch.n / wide_tile();
+      return static_cast<int>(launch_wide(p, launch.a_kcontig, launch.b_ncontig, s, e0, e1));
+    }
+    p.tiles_m = (launch.m + kTileM - 1) / kTileM;
+    p.tiles_n = (launch.n + kTileN - 1) / kTileN;
+    hipError_t err;
+    if (!launch.a_kcontig && !launch.b_ncontig) err = launch_variant<false, false>(p, s, e0, nullptr);
+    else if (!launch.a_kcontig && launch.b_ncontig) err = launch_variant<false, true>(p, s, e0, nullptr);
+    else if (launch.a_kcontig && !launch.b_ncontig) err = launch_variant<true, false>(p, s, e0, nullptr);
+    else err = launch_variant<true, true>(p, s, e0, nullptr);
+    if (err != hipSuccess) return static_cast<int>(err);
+    return static_cast<int>(launch_splitk_reduce(p, s, e1));
   }
   if (wide_fits(launch)) {
     p.tiles_m = (launch.m + wide_tile() - 1) / wide_tile();

@@ -837,18 +837,21 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring8_kernel(Params p) {
 //
 // C = alpha * (P_0 + P_1 + ... + P_{S-1}) + beta * C, + bias, ReLU: the
 // partials of a split launch added in range order (fixed, so C is the same
-// from run to run), then the same epilogue arithmetic as store_c_interior.
-// One thread per four consecutive rows of one column (m is a multiple of
-// 256): the partials and C are read and written as 16-byte vectors, the
-// threads of a wave covering 256 consecutive floats of a column.
+// from run to run), then the same epilogue arithmetic as store_c_tile. One
+// thread per four consecutive rows of one column (ceil(m / 4) per column, the
+// threads of a wave covering 256 consecutive floats of a column): the partials
+// (ld = partial_ld(m)) are read as 16-byte vectors, C too where the four rows
+// lie inside it, element by element in a column's last, partial quad (m not a
+// multiple of 4).
 __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(Params p) {
-  const int64_t quads = (int64_t)(p.m / 4) * p.n;
+  const int64_t per_col = ((int64_t)p.m + 3) / 4;
   const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (idx >= quads) return;
-  const int col = (int)(idx / (p.m / 4));
-  const int row = (int)(idx - (int64_t)col * (p.m / 4)) * 4;
-  const int64_t stride = (int64_t)p.m * p.n;
-  const float* part = p.partial + (int64_t)col * p.m + row;
+  if (idx >= per_col * p.n) return;
+  const int col = (int)(idx / per_col);
+  const int row = (int)(idx - (int64_t)col * per_col) * 4;
+  const int64_t ldp = partial_ld(p.m);
+  const int64_t stride = ldp * p.n;
+  const float* part = p.partial + (int64_t)col * ldp + row;
   float4 sum = *reinterpret_cast<const float4*>(part);
   for (int s = 1; s < p.splits; ++s) {
     const float4 v = *reinterpret_cast<const float4*>(part + s * stride);
@@ -858,29 +861,50 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(Params p) {
     sum.w += v.w;
   }
   float* cp = p.c + (int64_t)col * p.ldc + row;
-  float r[4] = {p.alpha * sum.x, p.alpha * sum.y, p.alpha * sum.z, p.alpha * sum.w};
-  if (p.beta != 0.f) {
-    const float4 old = *reinterpret_cast<const float4*>(cp);
-    r[0] = p.alpha * sum.x + p.beta * old.x;
-    r[1] = p.alpha * sum.y + p.beta * old.y;
-    r[2] = p.alpha * sum.z + p.beta * old.z;
-    r[3] = p.alpha * sum.w + p.beta * old.w;
-  }
-  if (p.bias_row != nullptr || p.bias_col != nullptr || p.relu != 0) {
-    const float bias_c = p.bias_col != nullptr ? p.bias_col[col] : 0.f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      if (p.bias_row != nullptr) r[t] += p.bias_row[row + t];
-      r[t] += bias_c;
-      if (p.relu != 0 && r[t] < 0.f) r[t] = 0.f;
+  const bool extra = p.bias_row != nullptr || p.bias_col != nullptr || p.relu != 0;
+  const float bias_c = p.bias_col != nullptr ? p.bias_col[col] : 0.f;
+  const auto finish = [&](float v, int r) {
+    if (p.bias_row != nullptr) v += p.bias_row[r];
+    v += bias_c;
+    return (p.relu != 0 && v < 0.f) ? 0.f : v;
+  };
+  if (row + 4 <= p.m) {
+    float r[4] = {p.alpha * sum.x, p.alpha * sum.y, p.alpha * sum.z, p.alpha * sum.w};
+    if (p.beta != 0.f) {
+      const float4 old = *reinterpret_cast<const float4*>(cp);
+      r[0] = p.alpha * sum.x + p.beta * old.x;
+      r[1] = p.alpha * sum.y + p.beta * old.y;
+      r[2] = p.alpha * sum.z + p.beta * old.z;
+      r[3] = p.alpha * sum.w + p.beta * old.w;
     }
+    if (extra) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) r[t] = finish(r[t], row + t);
+    }
+    *reinterpret_cast<float4*>(cp) = make_float4(r[0], r[1], r[2], r[3]);
+    return;
   }
-  *reinterpret_cast<float4*>(cp) = make_float4(r[0], r[1], r[2], r[3]);
+  const float v[4] = {sum.x, sum.y, sum.z, sum.w};
+  for (int t = 0; t < 4 && row + t < p.m; ++t) {
+    const float val = p.alpha * v[t];
+    const float out = p.beta != 0.f ? val + p.beta * cp[t] : val;
+    cp[t] = extra ? finish(out, row + t) : out;
+  }
 }
 
 } // namespace
 
 int wide_tile() { return kTile; }
+
+// The reduction of a split launch whose workgroups have been enqueued on
+// `stream` (p.splits, p.split_depth and p.partial set); `stop` (optional) is
+// recorded by its dispatch.
+hipError_t launch_splitk_reduce(const Params& p, hipStream_t stream, hipEvent_t stop) {
+  const int64_t quads = (((int64_t)p.m + 3) / 4) * p.n;
+  const dim3 grid(static_cast<unsigned>((quads + kThreads - 1) / kThreads));
+  hipExtLaunchKernelGGL(splitk_reduce_kernel, grid, dim3(kThreads), 0, stream, nullptr, stop, 0, p);
+  return hipGetLastError();
+}
 
 // Launches a 256 x 256 kernel for `p` (tiles_m / tiles_n already in 256s):
 // for launches of interior tiles only, sgemm_ring_kernel (N/T, K a multiple
@@ -905,10 +929,7 @@ hipError_t launch_wide(const Params& p, bool a_kcontig, bool b_ncontig, hipStrea
     else
       hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, false>), grid, block, 0, stream, start, nullptr, 0, p);
     if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
-    const int64_t quads = (int64_t)(p.m / 4) * p.n;
-    const dim3 rgrid(static_cast<unsigned>((quads + kThreads - 1) / kThreads));
-    hipExtLaunchKernelGGL(splitk_reduce_kernel, rgrid, block, 0, stream, nullptr, stop, 0, p);
-    return hipGetLastError();
+    return launch_splitk_reduce(p, stream, stop);
   }
   const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
   const bool interior = p.m % kTile == 0 && p.n % kTile == 0;
