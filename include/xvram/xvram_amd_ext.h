@@ -35,7 +35,7 @@
  * the kernels gemm_execute runs on each tile (full-precision FP32 MFMA), for
  * operands already in HBM, e.g. the resolved ranges a transaction callback
  * receives (enqueue on its native_stream). It returns once the work is
- * enqueued. A launch with fewer 256 x 256 tiles than the GPU has CUs splits
+ * enqueued. A launch that would leave the GPU's workgroup slots idle splits
  * its K (partial sums in a workspace, added in a fixed order: the same result
  * on every call); the workspace is desc.workspace when it holds every partial,
  * else one the library allocates stream-ordered on the stream
@@ -147,7 +147,8 @@ typedef struct xvram_amd_ext_v1 {
      cannot allocate (code under stream capture, tight serving loops). No
      counterpart in the reference. A split that desc->workspace cannot hold
      uses the library's static per-GPU scratch of 64 MiB (the most any split
-     wants: one 256 KiB partial per CU), held until the process ends and
+     wants: one 256 x 256 partial tile per CU, or one 256 x 128 tile per
+     workgroup slot of the 256 x 128 kernel), held until the process ends and
      shared by every call on that GPU: calls that overlap on one GPU race.
      A split wanting more returns INVALID_ARGUMENT. Same results as
      sgemm_device. */
