@@ -11,6 +11,10 @@ memory the caller owns, enqueued on the caller's HIP stream, through the C ABI
 * Config 2's ragged shape (3001 x 2047 x 4099, alpha 1.5, beta 0.5): 12 x 16
   tiles of 256 x 128 split into 2 ranges, with the library's workspace and
   with the caller's: the same bits both ways, within the bound.
+* Interior 256 x 256 tiles whose operand panel the ring kernels cannot
+  address: op-T A with a leading dimension of 2^20 floats (a 2 GiB panel,
+  beyond their 32-bit buffer offsets), 512 x 512 x 2048 in 8 ranges on the
+  256 x 128 kernel, within the bound.
 * Inside a transaction callback, on the resolved addresses of a session's
   allocations and the callback's native_stream (the use the entry point is
   for): C read back through allocation_read.
@@ -209,6 +213,41 @@ def test_config2_ragged_split(lib, hip, oracle_mod, form):
     mine, _, _ = run_device_gemm(lib, hip, oracle_mod, m, n, k, FORMS[form], 541, alpha=1.5,
                                  beta=0.5, workspace_bytes=2 * 3004 * 2047 * 4)
     assert np.array_equal(mine[0].view(np.uint32), outs[0].view(np.uint32))
+
+
+def test_split_on_the_256x128_kernel(lib, hip, oracle_mod):
+    """op-T A stored k x m with lda = 2^20: the panel of A spans m * lda * 4 =
+    2 GiB, which the ring kernels' 32-bit buffer offsets cannot reach, so the
+    launch of 2 x 2 interior 256 x 256 tiles splits on the 256 x 128 kernel
+    instead: 2 x 4 of its tiles, K in 8 ranges."""
+    m, n, k = 512, 512, 2048
+    lda = 1 << 20
+    a_op = np.asfortranarray(oracle_mod.fill_uniform(m * k, 551).reshape(k, m).T)
+    b_op = np.asfortranarray(oracle_mod.fill_uniform(k * n, 552).reshape(n, k).T)
+    a_lines = np.ascontiguousarray(a_op)  # row i of op(A) = line i of the stored A
+    b_flat, ldb = stored(b_op, abi.OP_N)
+    c_flat, ldc = padded(np.zeros((m, n), np.float32))
+    pa = hip.alloc(m * lda * 4)
+    pb, pc = hip.alloc(b_flat.nbytes), hip.alloc(c_flat.nbytes)
+    s = hip.stream()
+    try:
+        hip.ok(hip.rt.hipMemset(ctypes.c_void_p(pa), 0, ctypes.c_size_t(m * lda * 4)), "hipMemset")
+        hip.ok(hip.rt.hipMemcpy2D(ctypes.c_void_p(pa), ctypes.c_size_t(lda * 4),
+                                  a_lines.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(k * 4),
+                                  ctypes.c_size_t(k * 4), ctypes.c_size_t(m), 1), "hipMemcpy2D")
+        hip.put(pb, b_flat)
+        hip.put(pc, c_flat)
+        d = desc_for((pa, pb, pc), m, n, k, (abi.OP_T, abi.OP_N), (lda, ldb, ldc))
+        assert lib.ext.sgemm_device(ctypes.byref(d), ctypes.c_void_p(s)) == abi.SUCCESS
+        hip.sync(s)
+        got = hip.get(pc, c_flat.size).reshape(n, ldc)[:, :m].T
+    finally:
+        for p in (pa, pb, pc):
+            hip.free(p)
+    ref, absab = oracle_mod.sgemm_f64(a_op, b_op)
+    bad, _, ratio = oracle_mod.check_bound(np.asfortranarray(got), k, ref, absab)
+    log(f"{m}x{n}x{k} TN, lda 2^20 (256 x 128 kernel): violations {bad}, err/bound {ratio:.3e}")
+    assert bad == 0
 
 
 def test_inside_a_transaction_callback(lib, oracle_mod):

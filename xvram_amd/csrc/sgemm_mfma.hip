@@ -271,8 +271,8 @@ __global__ __launch_bounds__(kThreads, 2) void sgemm_mfma_kernel(Params p) {
     mfmas((kSteps - 1) & 1);
   }
 
-  if (p.splits > 1) store_c_tile<2, false>(partial_target(p, split), acc, m0 + wm, n0 + wn, lrow, lhalf);
-  else store_c_tile<2, false>(p, acc, m0 + wm, n0 + wn, lrow, lhalf);
+  const Params out = p.splits > 1 ? partial_target(p, split) : p;
+  store_c_tile<2, false>(out, acc, m0 + wm, n0 + wn, lrow, lhalf);
 }
 
 template <bool AK, bool BN>
