@@ -1,10 +1,10 @@
 """Split-K launches on the MI355X, through the C ABI, against the oracle.
 
-Launches whose C has fewer 256 x 256 tiles than the chip's 256 CUs split K
-(kernels::split_k_plan): each K range of each tile is one workgroup of the
-ring kernels, writing raw partial sums into one frame of the pool, and a
-second kernel adds the partials in range order and applies alpha, beta and
-the epilogue.
+Launches that would leave workgroup slots idle split K (kernels::split_k_plan):
+each K range of each tile is one workgroup (of the ring kernels for interior
+256 x 256 tiles, else of the 256 x 128 kernel), writing raw partial sums into
+one frame of the pool, and a second kernel adds the partials in range order
+and applies alpha, beta and the epilogue.
 
 * The config-5 launch shape (4096 x 256 x 4096 under 64 MiB frames: 16 tiles,
   16 ranges of 256, the partials filling the frame exactly), all four forms:
