@@ -386,6 +386,11 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_wide_kernel(Params p) {
 // takes two K panels per pass through HBM (one read and one write of C, one
 // prologue) instead of one. Only the loads' source changes, so C is bit-identical
 // to a one-panel launch over the same K.
+//
+// Split instance (kSplit): workgroup ids cover tiles x K ranges
+// (split_coords); each workgroup narrows its operands to its range and stores
+// raw sums to its range's partial (partial_target), which
+// splitk_reduce_kernel adds up. The one-panel instance carries none of this.
 constexpr int kRing = 8;   // slots (k-pairs) per wave
 constexpr int kAhead = 7;  // prefetch distance in k-pairs
 constexpr int kSlot = 1024; // floats per slot: A 4 x 128, then B 4 x 128
@@ -402,13 +407,14 @@ struct RingSource {
   int rotate = 0; // sgemm_ring8_kernel: slot loaded first (< count)
 };
 
-template <bool kTwo>
+template <bool kTwo, bool kSplit>
 __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
+  static_assert(!(kTwo && kSplit), "a two-panel launch never splits");
   __shared__ __attribute__((aligned(16))) float lds[4 * kRing * kSlot];
   asm volatile("; accumulators in AGPRs" ::: "a0");
 
   int tile_m, tile_n, split = 0;
-  if (!kTwo && p.splits > 1) {
+  if constexpr (kSplit) {
     split = split_coords<kGroupM>(p, tile_m, tile_n);
     narrow_to_split(p, split, false, false); // A op N, B op T: K runs along lines
   } else {
@@ -576,7 +582,7 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
 
   // Every tile is interior: two columns of C per batch of loads. A split
   // launch stores its range's raw sums instead.
-  const Params out = (!kTwo && p.splits > 1) ? partial_target(p, split) : p;
+  const Params out = kSplit ? partial_target(p, split) : p;
   store_c_interior<4, 2, true>(out, acc, m0 + wm, n0 + wn, lrow, lhalf);
 }
 
@@ -635,13 +641,14 @@ __device__ __forceinline__ void wait_slots(int after) {
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template <bool kAKC, bool kBKC, bool kTwo>
+template <bool kAKC, bool kBKC, bool kTwo, bool kSplit>
 __global__ __launch_bounds__(kThreads, 1) void sgemm_ring8_kernel(Params p) {
+  static_assert(!(kTwo && kSplit), "a two-panel launch never splits");
   __shared__ __attribute__((aligned(16))) float lds[4 * kRing8 * 2 * kHalf8];
   asm volatile("; accumulators in AGPRs" ::: "a0");
 
   int tile_m, tile_n, split = 0;
-  if (!kTwo && p.splits > 1) {
+  if constexpr (kSplit) {
     split = split_coords<kGroupM>(p, tile_m, tile_n);
     narrow_to_split(p, split, kAKC, kBKC);
   } else {
@@ -829,7 +836,7 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring8_kernel(Params p) {
   // value computed before the loop were hoisted above it and spilled.
   int lane_e;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_e));
-  const Params out = (!kTwo && p.splits > 1) ? partial_target(p, split) : p;
+  const Params out = kSplit ? partial_target(p, split) : p;
   store_c_interior<4, 2, true>(out, acc, m0 + wm, n0 + wn, lane_e & 31, lane_e >> 5);
 }
 
@@ -921,13 +928,13 @@ hipError_t launch_wide(const Params& p, bool a_kcontig, bool b_ncontig, hipStrea
     // start event rides on the first dispatch, the stop event on the second.
     const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n * p.splits));
     if (!a_kcontig && b_ncontig)
-      hipExtLaunchKernelGGL(sgemm_ring_kernel<false>, grid, block, 0, stream, start, nullptr, 0, p);
+      hipExtLaunchKernelGGL((sgemm_ring_kernel<false, true>), grid, block, 0, stream, start, nullptr, 0, p);
     else if (!a_kcontig && !b_ncontig)
-      hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, false>), grid, block, 0, stream, start, nullptr, 0, p);
+      hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, false, true>), grid, block, 0, stream, start, nullptr, 0, p);
     else if (a_kcontig && !b_ncontig)
-      hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, false>), grid, block, 0, stream, start, nullptr, 0, p);
+      hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, false, true>), grid, block, 0, stream, start, nullptr, 0, p);
     else
-      hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, false>), grid, block, 0, stream, start, nullptr, 0, p);
+      hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, false, true>), grid, block, 0, stream, start, nullptr, 0, p);
     if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     return launch_splitk_reduce(p, stream, stop);
   }
@@ -935,20 +942,20 @@ hipError_t launch_wide(const Params& p, bool a_kcontig, bool b_ncontig, hipStrea
   const bool interior = p.m % kTile == 0 && p.n % kTile == 0;
   if (interior && !a_kcontig && b_ncontig && p.k % 4 == 0) {
     if (p.a2 != nullptr)
-      hipExtLaunchKernelGGL(sgemm_ring_kernel<true>, grid, block, 0, stream, start, stop, 0, p);
+      hipExtLaunchKernelGGL((sgemm_ring_kernel<true, false>), grid, block, 0, stream, start, stop, 0, p);
     else
-      hipExtLaunchKernelGGL(sgemm_ring_kernel<false>, grid, block, 0, stream, start, stop, 0, p);
+      hipExtLaunchKernelGGL((sgemm_ring_kernel<false, false>), grid, block, 0, stream, start, stop, 0, p);
   } else if (interior && p.k % kSlotK == 0) {
     const bool two = p.a2 != nullptr;
     if (!a_kcontig && !b_ncontig)
-      two ? hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, true>), grid, block, 0, stream, start, stop, 0, p)
-          : hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, false>), grid, block, 0, stream, start, stop, 0, p);
+      two ? hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, true, false>), grid, block, 0, stream, start, stop, 0, p)
+          : hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, false, false>), grid, block, 0, stream, start, stop, 0, p);
     else if (a_kcontig && !b_ncontig)
-      two ? hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, true>), grid, block, 0, stream, start, stop, 0, p)
-          : hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, false>), grid, block, 0, stream, start, stop, 0, p);
+      two ? hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, true, false>), grid, block, 0, stream, start, stop, 0, p)
+          : hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, false, false>), grid, block, 0, stream, start, stop, 0, p);
     else
-      two ? hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, true>), grid, block, 0, stream, start, stop, 0, p)
-          : hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, false>), grid, block, 0, stream, start, stop, 0, p);
+      two ? hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, true, false>), grid, block, 0, stream, start, stop, 0, p)
+          : hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, false, false>), grid, block, 0, stream, start, stop, 0, p);
   } else if (!a_kcontig && !b_ncontig)
     hipExtLaunchKernelGGL((sgemm_wide_kernel<false, false>), grid, block, 0, stream, start, stop, 0, p);
   else if (!a_kcontig && b_ncontig)
