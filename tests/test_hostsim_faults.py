@@ -13,9 +13,9 @@ read-back. Whatever the site and moment:
   that saw no fault tears down balanced.
 
 Across the matrix the faults fire during session setup, allocation, the GEMM,
-the transaction, allocation release and session close; event_sync is never
-reached here (the simulation's events complete at once, so event_query never
-reports one pending)."""
+the transaction, allocation release and session close. (The device layer has
+no blocking wait: every wait polls event_query, whose failures are covered
+here and whose never-ending case is tests/test_hostsim_stall.py.)"""
 import ctypes
 
 import numpy as np
@@ -29,7 +29,7 @@ from gemm_cases import pattern_operands
 KiB = 1 << 10
 SITES = ["init", "mem_info", "va_reserve", "va_free", "mem_create", "mem_release", "mem_map",
          "mem_unmap", "set_access", "host_alloc", "stream_create", "event_create",
-         "event_record", "event_query", "event_sync", "copy_h2d", "copy_d2h", "launch"]
+         "event_record", "event_query", "copy_h2d", "copy_d2h", "launch"]
 INJECTED = 9001  # the simulation's injected error code
 
 

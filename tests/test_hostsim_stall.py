@@ -28,7 +28,7 @@ from gemm_cases import uniform
 
 KiB = 1 << 10
 F = 16 * KiB
-SITE_EVENT_HANG = 18
+SITE_EVENT_HANG = 17
 STALL_MS = 150
 # Generous bound for one failed call: the first expired wait quarantines the
 # session, after which no further wait is attempted.

@@ -23,7 +23,7 @@ from gemm_cases import uniform
 KiB = 1 << 10
 F = 4 * KiB  # hostsim granularity = frame size used here
 R, RW, WO = abi.ACCESS_READ, abi.ACCESS_READ_WRITE, abi.ACCESS_WRITE_ONLY
-SITE_COPY_H2D = 15
+SITE_COPY_H2D = 14
 
 
 @pytest.fixture()

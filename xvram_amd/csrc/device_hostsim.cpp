@@ -34,8 +34,8 @@ namespace {
 
 enum Site {
   kInit, kMemInfo, kVaReserve, kVaFree, kMemCreate, kMemRelease, kMemMap, kMemUnmap, kSetAccess,
-  kHostAlloc, kStreamCreate, kEventCreate, kEventRecord, kEventQuery, kEventSync, kCopyH2D,
-  kCopyD2H, kLaunch,
+  kHostAlloc, kStreamCreate, kEventCreate, kEventRecord, kEventQuery, kCopyH2D, kCopyD2H,
+  kLaunch,
   // Not a failure: once this site "fails", the event being recorded never
   // completes (event_query keeps answering kNotReady), as if the work queued
   // before it on its stream hung. Persistent: every later record hangs too.
