@@ -10,6 +10,8 @@ libxvram_hostsim.so (plans only: the operands are allocated, never multiplied).
   would fill one frame, plans two 32768-deep launches instead of one.
 - Frames of 512 MiB and below keep their shapes: 8192 x 8192 x 16384 launches
   at 512 MiB, 4096^3 at 64 MiB.
+- The reference planner's large-K regression fixture (row-major 2049 x 2049 x
+  32769 under 64 MiB chunks) plans under both of its targets.
 
 Each case allocates its operands in host memory (zero-filled): at most 5 GiB."""
 import pytest
@@ -54,3 +56,29 @@ def test_panels_stay_below_two_gib(sim):
                          ids=["512MiB", "64MiB"])
 def test_smaller_frames_keep_their_shapes(sim, frame, k, expected):
     assert plan_shape(sim, 8192, 8192, k, frame, 31) == expected
+
+
+@pytest.mark.parametrize("target_mib", [256, 384])
+def test_reference_large_k_fixture(sim, target_mib):
+    """The reference planner's large-K regression fixture
+    (tests/unit/gemm_planner_tests.cpp:265-300): 2049 x 2049 x 32769 with every
+    matrix row-major, 64 MiB chunks, a 4 MiB workspace cap. The reference's
+    chunk planner needs five resident chunks (a 384 MiB target; 256 MiB is
+    working_set_too_large) and plans 165 tiles of 512 x 2049 x 1024. The panel
+    planner needs three frames, so both targets plan: 2049 x 2049 C tiles and
+    4096-deep K panels, 9 per tile (the last one 1 deep), three frames at most
+    in use (A, B and C panels of 32.8 MiB, 32.8 MiB and 16 MiB)."""
+    m = n = 2049
+    k = 32769
+    with xv.Session(sim, chunk_size_bytes=64 * MiB, cache_target_bytes=target_mib * MiB,
+                    workspace_cap_bytes=4 * MiB, device_headroom_bytes=0) as s:
+        A, B, C = s.allocation(m * k * 4), s.allocation(k * n * 4), s.allocation(m * n * 4)
+        plan = xv.GemmPlan(s, xv.matrix(A, m, k, k, abi.ROW_MAJOR),
+                           xv.matrix(B, k, n, n, abi.ROW_MAJOR),
+                           xv.matrix(C, m, n, n, abi.ROW_MAJOR))
+        info = plan.info()
+        assert (info.tile_m, info.tile_n, info.tile_k, info.tile_count) == (2049, 2049, 4096, 9)
+        assert info.maximum_working_set_bytes == 3 * 64 * MiB
+        plan.release()
+        for h in (A, B, C):
+            h.release()
