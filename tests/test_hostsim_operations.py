@@ -91,6 +91,36 @@ def test_cancel_of_a_queued_operation_settles_at_once(sim):
             op.release()
 
 
+def test_bounded_waits_last_their_timeout(sim):
+    """A waiter watches the phase word for up to 2 ms before it blocks: a
+    bounded wait on a running operation still lasts its whole timeout, below
+    and above that window, and reports TIMEOUT; an operation that ends while
+    waiters watch or block wakes them with SUCCESS."""
+    with session(sim) as s:
+        a = s.allocation(F)
+        gate = Gate()
+        held = s.transaction([xv.access(a, 0, F)], gate)
+        assert gate.entered.wait(30)
+        for timeout_ms in (1, 2, 3, 25):
+            t = time.perf_counter()
+            st, info = held.wait(timeout_ms)
+            elapsed_ms = (time.perf_counter() - t) * 1e3
+            assert st == abi.TIMEOUT and info.state == abi.OPERATION_RUNNING
+            assert elapsed_ms >= timeout_ms * 0.99, (timeout_ms, elapsed_ms)
+        results = []
+        waiters = [threading.Thread(target=lambda: results.append(held.wait(10000)[0]))
+                   for _ in range(4)]
+        for w in waiters:
+            w.start()
+        time.sleep(0.001)  # some waiters still watching, some perhaps blocked
+        gate.open.set()
+        for w in waiters:
+            w.join(30)
+        assert results == [abi.SUCCESS] * 4
+        assert held.poll().state == abi.OPERATION_COMPLETED
+        held.release()
+
+
 def test_queue_deadline_fails_with_timeout(sim):
     with session(sim) as s:
         a = s.allocation(F)
