@@ -94,6 +94,7 @@ def test_split_pattern_is_exact(sim, oracle_mod, form):
     with session(sim) as s:
         (out,), info = run(s, a_op, b_op, FORMS[form])
     assert (info.tile_m, info.tile_n, info.tile_k, info.tile_count) == (m, n, k, 1)
+    assert info.maximum_working_set_bytes == 4 * 16 * MiB  # C, A, B and the partials' frame
     assert split_stats(sim) == (1, 8)
     assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))
 
@@ -138,8 +139,8 @@ def test_no_split_when_k_is_shallow(sim, oracle_mod):
     m, n, k = 512, 256, 384
     a_op, b_op = pattern_operands(m, n, k)
     with session(sim) as s:
-        (out,), _ = run(s, a_op, b_op, FORMS["NN"])
-    assert split_stats(sim)[0] == 0
+        (out,), info = run(s, a_op, b_op, FORMS["NN"])
+    assert split_stats(sim)[0] == 0 and info.maximum_working_set_bytes == 3 * 16 * MiB
     assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))
 
 

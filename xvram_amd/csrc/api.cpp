@@ -712,10 +712,13 @@ xvram_status XVRAM_CALL gemm_plan_get_info(xvram_gemm_plan p,
     info.tile_m = plan.problem.swapped ? plan.tn : plan.tm;
     info.tile_n = plan.problem.swapped ? plan.tm : plan.tn;
     info.tile_k = plan.bk;
-    // One launch's working set: its C tile and an A and a B panel frame per
-    // K panel it covers.
+    // One launch's working set: its C tile, an A and a B panel frame per K
+    // panel it covers, and the frame of split-K partials when the plan's
+    // launches split K (all from the cache's frames; the workspace cap stays
+    // unused by GEMMs).
     info.maximum_working_set_bytes =
-        (1 + 2 * uint64_t{plan.panels_per_launch}) * p->session->chunk_size_bytes();
+        (1 + 2 * uint64_t{plan.panels_per_launch} + (plan.scratch ? 1 : 0)) *
+        p->session->chunk_size_bytes();
     info.workspace_bytes = 0;
     // Tiles of the plan's geometry (reference planner.cpp:163 tile_count):
     // C tiles x K panels, however many K panels one launch covers.
