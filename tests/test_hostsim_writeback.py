@@ -16,6 +16,7 @@ import xvram_amd as xv
 from xvram_amd import abi
 
 KiB = 1 << 10
+SITE_LAUNCH = 16  # the host simulation's kernel-launch site (device_hostsim.cpp)
 F = 16 * KiB
 R, RW, WO = abi.ACCESS_READ, abi.ACCESS_READ_WRITE, abi.ACCESS_WRITE_ONLY
 
@@ -269,10 +270,12 @@ def test_failed_operation_keeps_earlier_outputs(sim):
                          xv.matrix(other, big, big, big))
         run(p0)
         p0.release()
-        # 256^3 tiles: each launch of the host simulation's loop takes tens of ms.
+        # 256^3 tiles; the second launch is held 1.5 s, so the 500 ms deadline
+        # expires between launches, after the first one.
         p2 = xv.GemmPlan(s, xv.matrix(A2, big, big, big), xv.matrix(B2, big, big, big),
-                         xv.matrix(C2, big, big, big), deadline_ms=5)
+                         xv.matrix(C2, big, big, big), deadline_ms=500)
         assert p2.info().tile_count == 8
+        slow_second_launch(sim)
         op = p2.submit()
         st, info = op.wait()
         assert st == abi.SUCCESS and info.result == abi.TIMEOUT
@@ -295,11 +298,22 @@ def test_failed_operation_keeps_earlier_outputs(sim):
         p3.release()
 
 
+def slow_second_launch(sim):
+    """The host simulation's next-but-one kernel launch sleeps 1.5 s first."""
+    fn = sim.dll.xvram_hostsim_delay
+    fn.argtypes = [ctypes.c_int, ctypes.c_long, ctypes.c_int]
+    fn.restype = ctypes.c_int
+    assert fn(SITE_LAUNCH, 1, 1500) == 0
+
+
 def failing_repeat(s, A, B, C, big):
-    """Runs the same product again under a 5 ms deadline; returns the failed
-    operation's info, or skips when the deadline expired before any launch."""
+    """Runs the same product again under a 500 ms deadline with its second
+    launch held 1.5 s; returns the failed operation's info (or skips when the
+    deadline expired before any launch: a host too loaded to reach the first
+    launch in 500 ms)."""
     p = xv.GemmPlan(s, xv.matrix(A, big, big, big), xv.matrix(B, big, big, big),
-                    xv.matrix(C, big, big, big), deadline_ms=5)
+                    xv.matrix(C, big, big, big), deadline_ms=500)
+    slow_second_launch(s.lib)
     op = p.submit()
     st, info = op.wait()
     assert st == abi.SUCCESS and info.result == abi.TIMEOUT
