@@ -25,7 +25,9 @@ per-launch durations, is the kernels' time (``kernel_overlap_ms`` reports the
 difference); ``kernel_ms_per_tile`` is that time per tile of the plan (one C
 tile x one K panel; a launch covers one or two K panels, and the launches of
 an operation's first K pass may run as several K-slice kernels). Other workloads:
-``--workload`` (config 3's resident sweep, config 4, the config-5 chain).
+``--workload`` (config 3's resident sweep, config 4, the config-5 chain, and
+configs 1 and 2 as single GEMMs on device memory through the extension's
+sgemm_device, timed with HIP events on the caller's stream).
 ``cpu_baseline`` times the FP64 reference loop (the oracle's restatement of
 the reference's CPU GEMM) on a bounded sample of the same product, on all host
 cores and, faithful to the reference example, on one thread. ``sample_check``
@@ -81,6 +83,15 @@ for _s, _frame in ((4096, 64 * MiB), (8192, 256 * MiB), (16384, 1024 * MiB)):
 WORKLOADS["resident_c5_layer_tn"] = (
     16384, 256, 16384, OP_T, OP_N, 0, 1024 * MiB,
     "FP32 SGEMM T/N 16384 x 256 x 16384 (one config-5 layer, weights resident; split K)")
+# Configs 1 and 2 as single GEMMs on device memory through the extension's
+# sgemm_device (the library's tile-kernel dispatch on the caller's buffers and
+# stream): config 1 = 1024^3 N/N, alpha 1, beta 0; config 2 = 3001 x 2047 x
+# 4099 in each form, alpha 1.5, beta 0.5. Both have fewer tiles than the chip
+# has CUs, so their launches split K (the partials in a stream-ordered
+# workspace of the library's).
+DEVICE = {"device_c1_nn": (1024, 1024, 1024, OP_N, OP_N, 1.0, 0.0)}
+for _oa, _ob in ((OP_N, OP_N), (OP_N, OP_T), (OP_T, OP_N), (OP_T, OP_T)):
+    DEVICE[f"device_c2_{'nt'[_oa]}{'nt'[_ob]}"] = (3001, 2047, 4099, _oa, _ob, 1.5, 0.5)
 DEFAULT = "ns65536_nt_16g"
 # Config 5: 8 x [Y = ReLU(X W^T + b)], X 256 x 16384 ~ N(0,1), W 16384 x 16384 and
 # b ~ N(0, 1/16384), 2 GiB budget of 64 MiB frames; one step = one 8-layer forward.
@@ -584,6 +595,125 @@ def run_chain(args, xv, lib, synth, link) -> int:
     return 0 if violations == 0 else 1
 
 
+def run_device(args, xv, lib, synth) -> int:
+    """One GEMM per step on device memory through sgemm_device; the K steps
+    are enqueued back to back on one stream and timed with HIP events on it.
+    The result of one more launch from the initial C is checked on every
+    element against the FP64 oracle after the timed region."""
+    import ctypes
+
+    from xvram_amd import abi
+
+    m, n, k, op_a, op_b, alpha, beta = DEVICE[args.workload]
+    rt = ctypes.CDLL("libamdhip64.so")
+
+    def ok(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: hipError {rc}")
+
+    def stored(rows, cols, seed):
+        ld = (rows + 3) // 4 * 4
+        host = np.empty(ld * cols, dtype=np.float32)
+        synth.synth_fill_uniform(host.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                 host.size, seed, 0)
+        ptr = ctypes.c_void_p()
+        ok(rt.hipMalloc(ctypes.byref(ptr), ctypes.c_size_t(host.nbytes)), "hipMalloc")
+        ok(rt.hipMemcpy(ptr, host.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(host.nbytes),
+                        1), "hipMemcpy")
+        return ptr, ld, host
+
+    a_rows, a_cols = (m, k) if op_a == OP_N else (k, m)
+    b_rows, b_cols = (k, n) if op_b == OP_N else (n, k)
+    pa, lda, a_host = stored(a_rows, a_cols, 1)
+    pb, ldb, b_host = stored(b_rows, b_cols, 2)
+    pc, ldc, c_host = stored(m, n, 3)
+    stream = ctypes.c_void_p()
+    ok(rt.hipStreamCreateWithFlags(ctypes.byref(stream), 1), "hipStreamCreateWithFlags")
+    events = [ctypes.c_void_p(), ctypes.c_void_p()]
+    for e in events:
+        ok(rt.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+    d = abi.sgemm_device_init()
+    d.a, d.b, d.c = pa.value, pb.value, pc.value
+    d.m, d.n, d.k, d.lda, d.ldb, d.ldc = m, n, k, lda, ldb, ldc
+    d.operation_a, d.operation_b = op_a, op_b
+    d.alpha, d.beta = alpha, beta
+
+    def launch():
+        status = lib.ext.sgemm_device(ctypes.byref(d), stream)
+        if status != abi.SUCCESS:
+            raise RuntimeError(f"sgemm_device returned {status}")
+
+    for _ in range(args.warmup):
+        launch()
+    ok(rt.hipStreamSynchronize(stream), "hipStreamSynchronize")
+    ok(rt.hipEventRecord(events[0], stream), "hipEventRecord")
+    for _ in range(args.steps):
+        launch()
+    ok(rt.hipEventRecord(events[1], stream), "hipEventRecord")
+    ok(rt.hipEventSynchronize(events[1]), "hipEventSynchronize")
+    elapsed = ctypes.c_float()
+    ok(rt.hipEventElapsedTime(ctypes.byref(elapsed), events[0], events[1]), "hipEventElapsedTime")
+    step_s = elapsed.value * 1e-3 / args.steps
+    flops = 2.0 * m * n * k
+    value = flops / step_s / 1e12
+    log(f"{args.steps} launches: {step_s * 1e6:.1f} us each = {value:.1f} TFLOP/s")
+
+    # One launch from the initial C, checked on every element.
+    ok(rt.hipMemcpy(pc, c_host.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(c_host.nbytes), 1),
+       "hipMemcpy")
+    launch()
+    ok(rt.hipStreamSynchronize(stream), "hipStreamSynchronize")
+    out = np.empty_like(c_host)
+    ok(rt.hipMemcpy(out.ctypes.data_as(ctypes.c_void_p), pc, ctypes.c_size_t(out.nbytes), 2),
+       "hipMemcpy")
+    for ptr in (pa, pb, pc):
+        ok(rt.hipFree(ptr), "hipFree")
+    for e in events:
+        ok(rt.hipEventDestroy(e), "hipEventDestroy")
+    ok(rt.hipStreamDestroy(stream), "hipStreamDestroy")
+
+    import oracle
+
+    def logical(host, rows, cols, ld, op):
+        st = host.reshape(cols, ld)[:, :rows].T
+        return np.asfortranarray(st if op == OP_N else st.T)
+
+    c0 = np.asfortranarray(c_host.reshape(n, ldc)[:, :m].T)
+    ref, absab = oracle.sgemm_f64(logical(a_host, a_rows, a_cols, lda, op_a),
+                                  logical(b_host, b_rows, b_cols, ldb, op_b), alpha, beta, c0)
+    bad, _, ratio = oracle.check_bound(np.asfortranarray(out.reshape(n, ldc)[:, :m].T), k, ref,
+                                       absab)
+    log(f"check: {m * n} elements, violations={bad} err/bound={ratio:.3e}")
+    frac = value / FP32_MFMA_PEAK_TFLOPS
+    result = {
+        "metric": "out-of-core FP32 SGEMM TFLOP/s at 3x VRAM budget; H2D GB/s vs link peak",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded U[-1,1) operands, counter-based generator)",
+        "config": {"workload": args.workload, "m": m, "n": n, "k": k, "op_a": "NT"[op_a],
+                   "op_b": "NT"[op_b], "alpha": alpha, "beta": beta,
+                   "description": "one GEMM on device memory through sgemm_device "
+                                  "(split-K launch and its reduction)",
+                   "step": "one sgemm_device call; the K calls are enqueued back to back on "
+                           "one stream and timed with HIP events on it",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(value, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(frac, 4), "traffic": None},
+        "cpu_baseline": None,
+        "check": {"elements": m * n, "violations": bad, "max_err_over_bound": ratio},
+    }
+    print(json.dumps(result), flush=True)
+    return 0 if bad == 0 else 1
+
+
 # ---- main ----------------------------------------------------------------------------
 
 def main() -> int:
@@ -591,7 +721,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + [CHAIN["name"]], default=DEFAULT)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + [CHAIN["name"]] + sorted(DEVICE),
+                    default=DEFAULT)
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -620,6 +751,11 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
+    if args.workload in DEVICE:
+        import xvram_amd as xv
+
+        log(f"workload {args.workload}")
+        return run_device(args, xv, xv.load(), synth_lib())
     trace_path = os.path.join(tempfile.mkdtemp(prefix="xvram_bench_"), "trace.jsonl")
     os.environ["XVRAM_TRACE_FILE"] = trace_path
 

@@ -2,18 +2,19 @@
 memory the caller owns, enqueued on the caller's HIP stream, through the C ABI
 (extension table), against the FP64 oracle.
 
-* Config 1's shape (1024^3 N/N: 16 tiles, so K splits into 4 ranges) with the
+* Config 1's shape (1024^3 N/N: 16 tiles, so K splits into 16 ranges) with the
   library's stream-ordered workspace and with a workspace of the caller's:
   the same bits both ways, within the FP64 bound.
 * The config-5 launch shape in every form (4096 x 256 x 4096, 16 ranges) with
   alpha, beta and a per-row bias + ReLU: within the bound.
 * Shapes that do not split (256 tiles; K too shallow for two ranges).
 * Config 2's ragged shape (3001 x 2047 x 4099, alpha 1.5, beta 0.5): 12 x 16
-  tiles of 256 x 128 split into 2 ranges, with the library's workspace and
-  with the caller's: the same bits both ways, within the bound.
+  tiles of 256 x 128 split into 5 ranges (960 workgroups: two rounds of the
+  kernel's workgroup slots), with the library's workspace and with the
+  caller's: the same bits both ways, within the bound.
 * Interior 256 x 256 tiles whose operand panel the ring kernels cannot
   address: op-T A with a leading dimension of 2^20 floats (a 2 GiB panel,
-  beyond their 32-bit buffer offsets), 512 x 512 x 2048 in 8 ranges on the
+  beyond their 32-bit buffer offsets), 512 x 512 x 2048 in 32 ranges on the
   256 x 128 kernel, within the bound.
 * Inside a transaction callback, on the resolved addresses of a session's
   allocations and the callback's native_stream (the use the entry point is
@@ -175,9 +176,9 @@ def test_config1_shape_library_and_caller_workspace(lib, hip, oracle_mod):
     bad, _, ratio = oracle_mod.check_bound(np.asfortranarray(outs[0]), k, ref, absab)
     log(f"1024^3 NN, library workspace: violations {bad}, err/bound {ratio:.3e}")
     assert bad == 0
-    # Four 4 MiB partials in a workspace of the caller's: the same split, the same bits.
+    # Sixteen 4 MiB partials in a workspace of the caller's: the same split, the same bits.
     mine, _, _ = run_device_gemm(lib, hip, oracle_mod, m, n, k, FORMS["NN"], 501,
-                                 workspace_bytes=16 * MiB)
+                                 workspace_bytes=64 * MiB)
     assert np.array_equal(mine[0].view(np.uint32), outs[0].view(np.uint32))
 
 
@@ -209,9 +210,9 @@ def test_config2_ragged_split(lib, hip, oracle_mod, form):
     log(f"config 2 {m}x{n}x{k} {form}, library workspace: violations {bad}, "
         f"err/bound {ratio:.3e}")
     assert bad == 0
-    # Two partials of 3004 x 2047 floats in a workspace of the caller's.
+    # Five partials of 3004 x 2047 floats in a workspace of the caller's.
     mine, _, _ = run_device_gemm(lib, hip, oracle_mod, m, n, k, FORMS[form], 541, alpha=1.5,
-                                 beta=0.5, workspace_bytes=2 * 3004 * 2047 * 4)
+                                 beta=0.5, workspace_bytes=5 * 3004 * 2047 * 4)
     assert np.array_equal(mine[0].view(np.uint32), outs[0].view(np.uint32))
 
 
@@ -219,7 +220,7 @@ def test_split_on_the_256x128_kernel(lib, hip, oracle_mod):
     """op-T A stored k x m with lda = 2^20: the panel of A spans m * lda * 4 =
     2 GiB, which the ring kernels' 32-bit buffer offsets cannot reach, so the
     launch of 2 x 2 interior 256 x 256 tiles splits on the 256 x 128 kernel
-    instead: 2 x 4 of its tiles, K in 8 ranges."""
+    instead: 2 x 4 of its tiles, K in 32 ranges of 64."""
     m, n, k = 512, 512, 2048
     lda = 1 << 20
     a_op = np.asfortranarray(oracle_mod.fill_uniform(m * k, 551).reshape(k, m).T)

@@ -9,20 +9,22 @@ and applies alpha, beta and the epilogue.
 * The config-5 launch shape (4096 x 256 x 4096 under 64 MiB frames: 16 tiles,
   16 ranges of 256, the partials filling the frame exactly), all four forms:
   the analytic pattern, every element bit-exact.
-* A K tail (4096 x 256 x 4000: 14 ranges of 288, the last 256) with alpha,
+* A K tail (4096 x 256 x 4000: 16 ranges of 256, the last 160) with alpha,
   beta and a per-column bias + ReLU, seeded U[-1,1) operands: every element
   within the FP64 bound, and two executions bit-identical (the reduction
   order is fixed).
 * A resident config-5 layer with the weights resident (16384 x 256 x 16384
   T/N under 1 GiB frames: 64 tiles, 4 ranges of 4096): pattern bit-exact.
-* Config 1's shape (1024^3 N/N, 16 tiles, 4 ranges): every element within the
+* Config 1's shape (1024^3 N/N, 16 tiles, 16 ranges of 64): every element within the
   FP64 bound.
 * Launches that are not whole 256 x 256 tiles split on the 256 x 128 kernel:
-  501 x 200 x 2048 (2 x 2 tiles, 8 ranges; partials of leading dimension 504)
-  bit-exact on the pattern in all four forms; 501 x 200 x 1000 (three ranges,
+  501 x 200 x 2048 (2 x 2 tiles, 32 ranges; partials of leading dimension 504)
+  bit-exact on the pattern in all four forms; 501 x 200 x 1000 (eleven ranges,
   a K tail) with alpha, beta and a per-row or per-column bias + ReLU within the
-  bound, two executions bit-identical; config 2's shape (3001 x 2047 x 4099,
-  2 ranges) in all four forms with alpha 1.5, beta 0.5 within the bound.
+  bound, two executions bit-identical; config 2's shape (3001 x 2047 x 4099)
+  in all four forms with alpha 1.5, beta 0.5 within the bound, under 64 MiB
+  frames (the partials' frame holds 2 ranges) and 128 MiB frames (5 ranges,
+  two rounds of the kernel's workgroup slots).
 
 Tolerance: |C - C_ref| <= 4*K*2^-24*(|alpha||A||B| + |beta C0| + |bias|)_ij."""
 import ctypes
@@ -259,13 +261,16 @@ def test_ragged_split_k_tail_beta_epilogue(lib, synth, oracle_mod, form, axis):
         closed(s)
 
 
+@pytest.mark.parametrize("frame_mib", [64, 128])
 @pytest.mark.parametrize("form", sorted(FORMS))
-def test_config2_shape_split(lib, synth, oracle_mod, form):
+def test_config2_shape_split(lib, synth, oracle_mod, form, frame_mib):
     """Config 2 (3001 x 2047 x 4099, alpha 1.5, beta 0.5) resident: one launch of
-    12 x 16 tiles of 256 x 128 that splits K into 2 ranges."""
+    12 x 16 tiles of 256 x 128 that splits K into as many ranges as the
+    partials' frame holds up to the rule's 5: 2 under 64 MiB frames, 5 under
+    128 MiB."""
     m, n, k = 3001, 2047, 4099
     alpha, beta = 1.5, 0.5
-    s = xv.Session(lib, chunk_size_bytes=64 * MiB, cache_target_bytes=2 * GiB)
+    s = xv.Session(lib, chunk_size_bytes=frame_mib * MiB, cache_target_bytes=2 * GiB)
     try:
         g = Gemm(s, m, n, k, FORMS[form], alpha, beta)
         assert g.plan.info().tile_count == 1
@@ -280,7 +285,8 @@ def test_config2_shape_split(lib, synth, oracle_mod, form):
         ref, absab = oracle_mod.sgemm_f64(np.asfortranarray(a_op), np.asfortranarray(b_op),
                                           alpha, beta, np.asfortranarray(c0.reshape(n, m).T))
         bad, _, ratio = oracle_mod.check_bound(np.asfortranarray(got), k, ref, absab)
-        log(f"config 2 {m}x{n}x{k} {form}: violations {bad}, err/bound {ratio:.3e}")
+        log(f"config 2 {m}x{n}x{k} {form}, {frame_mib} MiB frames: violations {bad}, "
+            f"err/bound {ratio:.3e}")
         assert bad == 0
         g.plan.release()
     finally:

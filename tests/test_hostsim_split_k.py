@@ -1,8 +1,9 @@
 """CPU tests of split-K launches over libxvram_hostsim.so.
 
 A launch that would leave workgroup slots idle cuts its K into ranges
-(kernels::split_k_shape: as many as fill the chip, each at least 256 deep, in
-multiples of 32), accumulates each range into a partial held in one frame of
+(kernels::split_k_shape: on the ring kernels as many as one round of the CUs
+takes, on the 256 x 128 kernel the count its timing model rates fastest; each
+at least 64 deep, in multiples of 32), accumulates each range into a partial held in one frame of
 the pool (leading dimension m rounded up to 4), and adds the partials in range
 order before alpha, beta and the epilogue. Launches of interior 256 x 256 tiles
 split on the ring kernels (one workgroup per CU); the others on the 256 x 128
@@ -88,21 +89,21 @@ def session(lib, frame_mib=16, frames=12):
 
 @pytest.mark.parametrize("form", sorted(FORMS))
 def test_split_pattern_is_exact(sim, oracle_mod, form):
-    """512 x 256 x 2048: two tiles, so eight K ranges of 256 (one launch)."""
+    """512 x 256 x 2048: two tiles, so 32 K ranges of 64 (one launch)."""
     m, n, k = 512, 256, 2048
     a_op, b_op = pattern_operands(m, n, k)
     with session(sim) as s:
         (out,), info = run(s, a_op, b_op, FORMS[form])
     assert (info.tile_m, info.tile_n, info.tile_k, info.tile_count) == (m, n, k, 1)
     assert info.maximum_working_set_bytes == 4 * 16 * MiB  # C, A, B and the partials' frame
-    assert split_stats(sim) == (1, 8)
+    assert split_stats(sim) == (1, 32)
     assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))
 
 
 @pytest.mark.parametrize("form", sorted(FORMS))
 def test_split_with_k_tail_beta_and_epilogue(sim, oracle_mod, form):
-    """K = 1000: three ranges of 352, 352 and 296 (a tail that is no multiple
-    of 32); alpha, beta and a per-column bias with ReLU after the reduction.
+    """K = 1000: eleven ranges, ten of 96 and a tail of 40 (no multiple of
+    32); alpha, beta and a per-column bias with ReLU after the reduction.
     Within the FP64 bound, and the same bits on every run."""
     m, n, k = 512, 256, 1000
     a_op = uniform(oracle_mod, m, k, 71)
@@ -112,7 +113,7 @@ def test_split_with_k_tail_beta_and_epilogue(sim, oracle_mod, form):
     with session(sim) as s:
         outs, _ = run(s, a_op, b_op, FORMS[form], c0, alpha=-0.75, beta=0.5, bias=bias,
                       relu=True, repeat=2)
-    assert split_stats(sim) == (2, 3)
+    assert split_stats(sim) == (2, 11)
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
     a64, b64 = a_op.astype(np.float64), b_op.astype(np.float64)
     ref = np.maximum(-0.75 * (a64 @ b64) + 0.5 * c0 + bias[None, :], 0.0)
@@ -135,8 +136,8 @@ def test_split_across_k_panels(sim, oracle_mod):
 
 
 def test_no_split_when_k_is_shallow(sim, oracle_mod):
-    """K = 384 leaves fewer than two ranges of 256: unsplit."""
-    m, n, k = 512, 256, 384
+    """K = 120 leaves fewer than two ranges of 64: unsplit."""
+    m, n, k = 512, 256, 120
     a_op, b_op = pattern_operands(m, n, k)
     with session(sim) as s:
         (out,), info = run(s, a_op, b_op, FORMS["NN"])
@@ -148,23 +149,30 @@ MiB_ = 1 << 20
 
 
 @pytest.mark.parametrize("m,n,k,nt,ring,ws,expect", [
-    # the C5 chain's launch: 16 tiles of 256 x 256 -> 16 ranges of 256 (ring kernels)
+    # the C5 chain's launch: 16 tiles of 256 x 256 -> 16 ranges of 256 (ring kernels,
+    # one round of the CUs)
     (4096, 256, 4096, False, True, 64 * MiB_, (16, 256, 0)),
     # the resident C5 layer: 64 tiles -> 4 ranges of 4096
     (16384, 256, 16384, False, True, 1 << 30, (4, 4096, 0)),
-    # config 1: 16 tiles; K / 256 limits it to 4 ranges
-    (1024, 1024, 1024, False, True, 64 * MiB_, (4, 256, 0)),
-    # config 2: ragged, 12 x 16 tiles of 256 x 128 -> 2 ranges on the 256 x 128 kernel
+    # config 1: 16 tiles -> 16 ranges of 64
+    (1024, 1024, 1024, False, True, 64 * MiB_, (16, 64, 0)),
+    # config 2: ragged, 12 x 16 tiles of 256 x 128 on the 256 x 128 kernel: 5 ranges
+    # (960 workgroups, two rounds of its 512 slots); 64 MiB hold only 2 partials
+    (3001, 2047, 4099, False, True, 128 * MiB_, (5, 832, 1)),
     (3001, 2047, 4099, False, True, 64 * MiB_, (2, 2080, 1)),
+    # 16 x 24 tiles of 256 x 128 fill 3/4 of the slots unsplit; 2 ranges run faster
+    (4000, 3000, 2000, True, True, 1 << 30, (2, 1024, 1)),
     # 256 tiles of 256 x 256 fill the chip
     (4096, 4096, 4096, True, True, 64 * MiB_, (1, 0, 0)),
     # ragged, but 17 x 16 tiles of 256 x 256: the general 256 x 256 kernel, unsplit
     (4100, 4096, 4096, True, True, 64 * MiB_, (1, 0, 0)),
     # interior but K not a multiple of 8 (N/N): the 256 x 128 kernel; N/T splits on the ring
-    (1024, 1024, 1004, False, True, 64 * MiB_, (3, 352, 1)),
-    (1024, 1024, 1004, True, True, 64 * MiB_, (3, 352, 0)),
+    (1024, 1024, 1004, False, True, 64 * MiB_, (8, 128, 1)),
+    (1024, 1024, 1004, True, True, 64 * MiB_, (11, 96, 0)),
     # operand panels the ring kernels cannot address: the 256 x 128 kernel
-    (1024, 1024, 1024, False, False, 64 * MiB_, (4, 256, 1)),
+    (1024, 1024, 1024, False, False, 64 * MiB_, (8, 128, 1)),
+    # K below two ranges of 64: unsplit
+    (1024, 1024, 120, False, True, 64 * MiB_, (1, 0, 0)),
     # the workspace holds 3 partials: 3 ranges; 1 partial: unsplit
     (4096, 256, 4096, False, True, 12 * MiB_, (3, 1376, 0)),
     (4096, 256, 4096, False, True, 4 * MiB_, (1, 0, 0)),
@@ -185,7 +193,7 @@ def test_split_rule(sim, m, n, k, nt, ring, ws, expect):
 @pytest.mark.parametrize("form", sorted(FORMS))
 def test_ragged_split_pattern_is_exact(sim, oracle_mod, form):
     """501 x 200 x 2048: not whole 256 x 256 tiles, so the 256 x 128 kernel's
-    2 x 2 tiles split K into 8 ranges of 256; the partials' leading dimension
+    2 x 2 tiles split K into 32 ranges of 64; the partials' leading dimension
     is 504 (m rounded up to 4) and the reduction's last quad of each column
     holds one row."""
     m, n, k = 501, 200, 2048
@@ -193,14 +201,14 @@ def test_ragged_split_pattern_is_exact(sim, oracle_mod, form):
     with session(sim) as s:
         (out,), info = run(s, a_op, b_op, FORMS[form])
     assert info.tile_count == 1
-    assert split_stats(sim) == (1, 8) and narrow_splits(sim) == 1
+    assert split_stats(sim) == (1, 32) and narrow_splits(sim) == 1
     assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))
 
 
 @pytest.mark.parametrize("axis", [abi.BIAS_PER_ROW, abi.BIAS_PER_COLUMN], ids=["row", "col"])
 @pytest.mark.parametrize("form", sorted(FORMS))
 def test_ragged_split_with_k_tail_beta_and_epilogue(sim, oracle_mod, form, axis):
-    """501 x 200 x 1000 on the 256 x 128 kernel: three ranges (352, 352, 296),
+    """501 x 200 x 1000 on the 256 x 128 kernel: eleven ranges (ten of 96, 40),
     alpha, beta and a per-row or per-column bias with ReLU after the
     reduction. Within the FP64 bound, and the same bits on every run."""
     m, n, k = 501, 200, 1000
@@ -212,7 +220,7 @@ def test_ragged_split_with_k_tail_beta_and_epilogue(sim, oracle_mod, form, axis)
     with session(sim) as s:
         outs, _ = run(s, a_op, b_op, FORMS[form], c0, alpha=1.25, beta=-0.5, bias=bias,
                       relu=True, repeat=2, axis=axis)
-    assert split_stats(sim) == (2, 3) and narrow_splits(sim) == 2
+    assert split_stats(sim) == (2, 11) and narrow_splits(sim) == 2
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
     a64, b64 = a_op.astype(np.float64), b_op.astype(np.float64)
     badd = bias[:, None] if axis == abi.BIAS_PER_ROW else bias[None, :]

@@ -39,13 +39,15 @@ def test_no_alloc_matches_sgemm_device(lib, oracle_mod):
     hip = Hip()
     s = hip.stream()
     try:
-        # 16 tiles x 16 ranges (64 MiB of partials: the whole scratch), then
-        # 8 tiles x 8 ranges (16 MiB) over what the first call left there,
-        # then a ragged launch (2 x 2 tiles of 256 x 128, 8 ranges, partials
-        # of leading dimension 504).
+        # 16 tiles x 16 ranges (64 MiB of partials), then 8 tiles x 32 ranges
+        # (64 MiB) over what the first call left there, then a ragged launch
+        # (2 x 2 tiles of 256 x 128, 32 ranges, partials of leading dimension
+        # 504), then config 2's shape (192 tiles of 256 x 128, 5 ranges: 117
+        # MiB of partials, most of the 128 MiB scratch).
         for call, (m, n, k, form, seed) in enumerate([(4096, 256, 4096, "NN", 601),
                                                       (1024, 512, 2048, "NT", 602),
-                                                      (501, 200, 2048, "TN", 603)]):
+                                                      (501, 200, 2048, "TN", 603),
+                                                      (3001, 2047, 4099, "NN", 604)]):
             ops = FORMS[form]
             a_op = np.asfortranarray(oracle_mod.fill_uniform(m * k, seed).reshape(k, m).T)
             b_op = np.asfortranarray(oracle_mod.fill_uniform(k * n, seed + 1).reshape(n, k).T)

@@ -18,13 +18,13 @@ namespace {
 // GPU in this file's code object, held until the process ends and shared by
 // every call on that GPU (calls that overlap on one GPU race on it). A split
 // never wants more: at most one 256 x 256 partial tile per CU (ring kernels)
-// or one 256 x 128 tile per workgroup slot (the 256 x 128 kernel, two per
-// CU). Every partial element the reduction uses is written before it is read
-// (the padding rows of a ragged partial are read but not used), so nothing in
-// the array needs clearing between calls.
-constexpr uint64_t kScratchBytes = 64ull << 20;
+// or one 256 x 128 tile per workgroup of two rounds of two per CU (the 256 x
+// 128 kernel). Every partial element the reduction uses is written before it
+// is read (the padding rows of a ragged partial are read but not used), so
+// nothing in the array needs clearing between calls.
+constexpr uint64_t kScratchBytes = 128ull << 20;
 static_assert(kScratchBytes >= uint64_t(kernels::kComputeUnits) * 256 * 256 * 4 &&
-                  kScratchBytes >= uint64_t(2 * kernels::kComputeUnits) * 256 * 128 * 4,
+                  kScratchBytes >= kernels::kSplitMaxPartialBytes,
               "the scratch holds the largest split");
 static __device__ __align__(256) float scratch[kScratchBytes / 4];
 

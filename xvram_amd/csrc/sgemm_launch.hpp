@@ -30,8 +30,8 @@
 // 256 tiles (m and n multiples of 256, K a multiple of 4 for N/T and of 8 for
 // the other forms) split on the ring kernels when they have fewer tiles than
 // the chip has CUs; other launches with fewer than 256 tiles of 256 x 256
-// split on the 256 x 128 kernel (two workgroups per CU) when they have fewer
-// of its tiles than it has slots. The order of the additions is fixed, so C
+// split on the 256 x 128 kernel (two workgroups per CU) when a split runs
+// faster by narrow_time. The order of the additions is fixed, so C
 // is the same from run to run. Without a workspace large enough for two
 // partials the launch runs unsplit. One K panel only.
 //
@@ -43,6 +43,7 @@
 // executor passes none and derives starts from the events a launch follows.
 #pragma once
 
+#include <algorithm>
 #include <cstdint>
 
 namespace xvram::kernels {
@@ -72,9 +73,14 @@ struct SgemmLaunch {
 // MI355X: 256 compute units; a launch with fewer tiles than this leaves CUs
 // idle unless its K is split.
 constexpr int64_t kComputeUnits = 256;
-// K per workgroup of a split launch, at least (a range this deep keeps the
-// ring kernels' prologue and the partial's store small next to its MFMA work).
-constexpr int64_t kSplitMinDepth = 256;
+// K per workgroup of a split launch, at least (a shallower range spends more
+// of its time on its first loads and on storing its partial than on MFMAs).
+constexpr int64_t kSplitMinDepth = 64;
+// Workgroups of one split launch on the 256 x 128 kernel, at most: two rounds
+// of its two workgroups per CU. Its partials then hold at most this many
+// 256 x 128 tiles (kSplitMaxPartialBytes).
+constexpr int64_t kNarrowMaxGroups = 4 * kComputeUnits;
+constexpr uint64_t kSplitMaxPartialBytes = uint64_t(kNarrowMaxGroups) * 256 * 128 * 4;
 
 struct SplitK {
   int splits = 1;      // 1 = not split
@@ -86,37 +92,76 @@ struct SplitK {
 // so every column starts 16-byte aligned.
 inline int64_t split_partial_ld(int64_t m) { return (m + 3) / 4 * 4; }
 
+// K ranges of `depth` (ceil(k / s) rounded up to 32) covering k.
+inline SplitK split_ranges(int64_t k, int64_t s, bool narrow) {
+  const int64_t depth = ((k + s - 1) / s + 31) / 32 * 32;
+  return SplitK{static_cast<int>((k + depth - 1) / depth), static_cast<int>(depth), narrow};
+}
+
+// Time of an m x n x k launch on the 256 x 128 kernel as `groups` equal
+// workgroups of K depth `depth` writing `splits` partials (1 = unsplit, no
+// partials), in tenths of the time a workgroup paired with another on its CU
+// takes per unit of K. The dispatcher fills every CU's two slots round after
+// round, so full rounds of 2 x CUs workgroups each take a pair's time, and so
+// does a last round that pairs workgroups on some CUs; a last round of at
+// most one workgroup per CU runs each alone, in 0.7 of a pair's time. Each
+// workgroup pays a fixed cost worth 32 units of K, and each partial one
+// 8e-6 units per element to write and read back. Fitted to config 2 and
+// seven other ragged launches of 4 to 384 tiles (each split count measured
+// from unsplit to three rounds): the rule's choice ran within 0.6 % of the
+// fastest measured split on every one.
+inline int64_t narrow_time(int64_t m, int64_t n, int64_t groups, int64_t depth, int64_t splits) {
+  constexpr int64_t slots = 2 * kComputeUnits;
+  const int64_t full = (groups - 1) / slots;
+  const int64_t last = groups - full * slots;
+  const int64_t partials = splits > 1 ? splits * m * n / 12500 : 0;
+  return (depth + 32) * (10 * full + (last > kComputeUnits ? 10 : 7)) + partials;
+}
+
 // The split of an m x n x k launch of form `nt` (A op N, B op T) or not,
-// given a workspace of `workspace_bytes` (see "Split K" above): as many ranges
-// as fill the chip's workgroup slots, each at least kSplitMinDepth deep, at
-// most as many partials as the workspace holds. `ring` = the ring kernels can
-// address the operand panels (each spans less than 2^31 bytes).
+// given a workspace of `workspace_bytes` (see "Split K" above). Ranges are at
+// least kSplitMinDepth deep and the workspace holds all their partials.
+// `ring` = the ring kernels can address the operand panels (each spans less
+// than 2^31 bytes).
+//  - Interior tiles on the ring kernels (one workgroup per CU): as many
+//    ranges as one round of the CUs takes (more rounds only add each
+//    range's fixed costs).
+//  - Otherwise, on the 256 x 128 kernel, when the launch has fewer than
+//    kComputeUnits tiles of 256 x 256: the number of ranges, within two rounds
+//    of its workgroup slots (kNarrowMaxGroups), that narrow_time rates
+//    fastest, the unsplit launch included (ties go to fewer ranges).
 inline SplitK split_k_shape(int64_t m, int64_t n, int64_t k, bool nt, bool ring,
                             uint64_t workspace_bytes) {
   if (m <= 0 || n <= 0 || k <= 0) return {};
   const bool interior = ring && m % 256 == 0 && n % 256 == 0 && k % (nt ? 4 : 8) == 0;
-  int64_t tiles = 0, slots = 0;
-  if (interior) {
-    tiles = (m / 256) * (n / 256);
-    slots = kComputeUnits;
-  } else {
-    // At least one 256 x 256 tile per CU runs a 256 x 256 kernel unsplit.
-    if (((m + 255) / 256) * ((n + 255) / 256) >= kComputeUnits) return {};
-    tiles = ((m + 255) / 256) * ((n + 127) / 128);
-    slots = 2 * kComputeUnits;
-  }
-  if (tiles >= slots) return {};
   const int64_t partial = split_partial_ld(m) * n * 4;
-  int64_t s = slots / tiles;
-  if (k / kSplitMinDepth < s) s = k / kSplitMinDepth;
-  if (static_cast<int64_t>(workspace_bytes / partial) < s)
-    s = static_cast<int64_t>(workspace_bytes / partial);
-  if (s < 2) return {};
-  const int64_t depth = (k + s - 1) / s;
-  const int64_t depth32 = (depth + 31) / 32 * 32;
-  const int64_t splits = (k + depth32 - 1) / depth32;
-  if (splits < 2) return {};
-  return SplitK{static_cast<int>(splits), static_cast<int>(depth32), !interior};
+  int64_t most = k / kSplitMinDepth;
+  if (static_cast<int64_t>(workspace_bytes / partial) < most)
+    most = static_cast<int64_t>(workspace_bytes / partial);
+  if (most < 2) return {};
+  if (interior) {
+    const int64_t tiles = (m / 256) * (n / 256);
+    const int64_t s = std::min(most, kComputeUnits / tiles);
+    if (s < 2) return {};
+    const SplitK sk = split_ranges(k, s, false);
+    return sk.splits >= 2 ? sk : SplitK{};
+  }
+  // At least one 256 x 256 tile per CU runs a 256 x 256 kernel unsplit.
+  if (((m + 255) / 256) * ((n + 255) / 256) >= kComputeUnits) return {};
+  const int64_t tiles = ((m + 255) / 256) * ((n + 127) / 128);
+  SplitK best{};
+  int64_t best_time = narrow_time(m, n, tiles, k, 1);
+  for (int64_t s = 2; s <= most; ++s) {
+    const SplitK sk = split_ranges(k, s, true);
+    if (sk.splits < 2 || sk.splits == best.splits) continue;
+    if (tiles * sk.splits > kNarrowMaxGroups) break;
+    const int64_t t = narrow_time(m, n, tiles * sk.splits, sk.depth, sk.splits);
+    if (t < best_time) {
+      best = sk;
+      best_time = t;
+    }
+  }
+  return best;
 }
 
 // The split a launch takes given room for `workspace_bytes` of partials: none
