@@ -15,7 +15,8 @@ and applies alpha, beta and the epilogue.
   order is fixed).
 * A resident config-5 layer with the weights resident (16384 x 256 x 16384
   T/N under 1 GiB frames: 64 tiles, 4 ranges of 4096): pattern bit-exact.
-* Config 1's shape (1024^3 N/N, 16 tiles, 16 ranges of 64): every element within the
+* Config 1's shape (1024^3 N/N: its ring split would take 64-deep ranges, so
+  32 tiles of 256 x 128 in 8 ranges of 128): every element within the
   FP64 bound.
 * Launches that are not whole 256 x 256 tiles split on the 256 x 128 kernel:
   501 x 200 x 2048 (2 x 2 tiles, 32 ranges; partials of leading dimension 504)

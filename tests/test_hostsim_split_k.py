@@ -2,8 +2,9 @@
 
 A launch that would leave workgroup slots idle cuts its K into ranges
 (kernels::split_k_shape: on the ring kernels as many as one round of the CUs
-takes, on the 256 x 128 kernel the count its timing model rates fastest; each
-at least 64 deep, in multiples of 32), accumulates each range into a partial held in one frame of
+takes when those are at least 256 deep, else on the 256 x 128 kernel the count
+its timing model rates fastest; each at least 64 deep, in multiples of 32),
+accumulates each range into a partial held in one frame of
 the pool (leading dimension m rounded up to 4), and adds the partials in range
 order before alpha, beta and the epilogue. Launches of interior 256 x 256 tiles
 split on the ring kernels (one workgroup per CU); the others on the 256 x 128
@@ -89,16 +90,32 @@ def session(lib, frame_mib=16, frames=12):
 
 @pytest.mark.parametrize("form", sorted(FORMS))
 def test_split_pattern_is_exact(sim, oracle_mod, form):
-    """512 x 256 x 2048: two tiles, so 32 K ranges of 64 (one launch)."""
+    """512 x 256 x 2048: two 256 x 256 tiles, whose ring split would take
+    64-deep ranges, so the 256 x 128 kernel's 2 x 2 tiles split K into 32
+    ranges of 64 (one launch)."""
     m, n, k = 512, 256, 2048
     a_op, b_op = pattern_operands(m, n, k)
     with session(sim) as s:
         (out,), info = run(s, a_op, b_op, FORMS[form])
     assert (info.tile_m, info.tile_n, info.tile_k, info.tile_count) == (m, n, k, 1)
     assert info.maximum_working_set_bytes == 4 * 16 * MiB  # C, A, B and the partials' frame
-    assert split_stats(sim) == (1, 32)
+    assert split_stats(sim) == (1, 32) and narrow_splits(sim) == 1
     assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))
 
+
+
+@pytest.mark.parametrize("form", ["NN", "NT"])
+def test_ring_split_pattern_is_exact(sim, oracle_mod, form):
+    """1024 x 512 x 8192 under 64 MiB frames: eight 256 x 256 tiles whose K
+    splits into 32 ranges of 256 on the ring kernels (one round of the CUs;
+    the 32 partials of 2 MiB fill the partials' frame)."""
+    m, n, k = 1024, 512, 8192
+    a_op, b_op = pattern_operands(m, n, k)
+    with session(sim, frame_mib=64, frames=8) as s:
+        (out,), info = run(s, a_op, b_op, FORMS[form])
+    assert (info.tile_m, info.tile_n, info.tile_k, info.tile_count) == (m, n, k, 1)
+    assert split_stats(sim) == (1, 32) and narrow_splits(sim) == 0
+    assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))
 
 @pytest.mark.parametrize("form", sorted(FORMS))
 def test_split_with_k_tail_beta_and_epilogue(sim, oracle_mod, form):
@@ -154,8 +171,11 @@ MiB_ = 1 << 20
     (4096, 256, 4096, False, True, 64 * MiB_, (16, 256, 0)),
     # the resident C5 layer: 64 tiles -> 4 ranges of 4096
     (16384, 256, 16384, False, True, 1 << 30, (4, 4096, 0)),
-    # config 1: 16 tiles -> 16 ranges of 64
-    (1024, 1024, 1024, False, True, 64 * MiB_, (16, 64, 0)),
+    # config 1: 16 tiles, whose ring split would take 16 ranges of 64: the 256 x 128
+    # kernel's 32 tiles in 8 ranges of 128 instead
+    (1024, 1024, 1024, False, True, 64 * MiB_, (8, 128, 1)),
+    # 8 tiles, 32 ranges of 256 in one round: the ring kernels
+    (1024, 512, 8192, True, True, 64 * MiB_, (32, 256, 0)),
     # config 2: ragged, 12 x 16 tiles of 256 x 128 on the 256 x 128 kernel: 5 ranges
     # (960 workgroups, two rounds of its 512 slots); 64 MiB hold only 2 partials
     (3001, 2047, 4099, False, True, 128 * MiB_, (5, 832, 1)),
@@ -168,7 +188,7 @@ MiB_ = 1 << 20
     (4100, 4096, 4096, True, True, 64 * MiB_, (1, 0, 0)),
     # interior but K not a multiple of 8 (N/N): the 256 x 128 kernel; N/T splits on the ring
     (1024, 1024, 1004, False, True, 64 * MiB_, (8, 128, 1)),
-    (1024, 1024, 1004, True, True, 64 * MiB_, (11, 96, 0)),
+    (1024, 1024, 1004, True, True, 64 * MiB_, (8, 128, 1)),
     # operand panels the ring kernels cannot address: the 256 x 128 kernel
     (1024, 1024, 1024, False, False, 64 * MiB_, (8, 128, 1)),
     # K below two ranges of 64: unsplit
@@ -246,3 +266,45 @@ def test_split_frame_is_returned_to_the_pool(sim, oracle_mod):
     assert t.mappings == t.unmaps and t.unsafe_transitions == 0 and t.unsafe_remaps == 0
     assert t.physical_handles_created == t.physical_handles_released
     s.release()
+
+
+def test_split_rule_properties(sim):
+    """Over a grid of shapes, forms and panel limits: every split covers K with
+    ranges of at least 64 in multiples of 32, keeps to one round of the CUs
+    (ring kernels: partials <= 64 MiB) or two rounds of the 256 x 128 kernel's
+    slots (partials <= 128 MiB), and a launch given exactly the workspace its
+    split wants (split_k_bytes_wanted) takes the same split, family included;
+    one byte less takes fewer ranges on the same family."""
+    fn = sim.dll.xvram_hostsim_split_shape
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                   ctypes.c_uint64, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]
+
+    def split(m, n, k, nt, ring, ws):
+        depth, narrow = ctypes.c_int(0), ctypes.c_int(0)
+        s = fn(m, n, k, int(nt), int(ring), ws, ctypes.byref(depth), ctypes.byref(narrow))
+        return s, depth.value, narrow.value
+
+    checked = 0
+    dims = [200, 256, 501, 512, 768, 1000, 1024, 2048, 3001, 4096, 5000]
+    for m in dims:
+        for n in dims:
+            for k in (96, 128, 500, 1024, 2048, 4099, 8192, 16384):
+                for nt in (False, True):
+                    for ring in (False, True):
+                        s, depth, narrow = split(m, n, k, nt, ring, (1 << 64) - 1)
+                        if s == 1:
+                            continue
+                        checked += 1
+                        assert depth % 32 == 0 and depth >= 64 and (s - 1) * depth < k <= s * depth
+                        partial = (m + 3) // 4 * 4 * n * 4
+                        if narrow:
+                            tiles = -(-m // 256) * -(-n // 128)
+                            assert tiles * s <= 1024 and s * partial <= 128 * MiB
+                        else:
+                            assert m % 256 == 0 and n % 256 == 0 and ring
+                            assert (m // 256) * (n // 256) * s <= 256 and s * partial <= 64 * MiB
+                        assert split(m, n, k, nt, ring, s * partial) == (s, depth, narrow)
+                        s2, _, narrow2 = split(m, n, k, nt, ring, s * partial - 1)
+                        assert s2 < s and (s2 == 1 or narrow2 == narrow)
+    assert checked > 500

@@ -39,8 +39,9 @@ def test_no_alloc_matches_sgemm_device(lib, oracle_mod):
     hip = Hip()
     s = hip.stream()
     try:
-        # 16 tiles x 16 ranges (64 MiB of partials), then 8 tiles x 32 ranges
-        # (64 MiB) over what the first call left there, then a ragged launch
+        # 16 tiles x 16 ranges on the ring kernels (64 MiB of partials), then
+        # 16 tiles of 256 x 128 x 16 ranges (32 MiB) over what the first call
+        # left there, then a ragged launch
         # (2 x 2 tiles of 256 x 128, 32 ranges, partials of leading dimension
         # 504), then config 2's shape (192 tiles of 256 x 128, 5 ranges: 117
         # MiB of partials, most of the 128 MiB scratch).

@@ -76,6 +76,14 @@ constexpr int64_t kComputeUnits = 256;
 // K per workgroup of a split launch, at least (a shallower range spends more
 // of its time on its first loads and on storing its partial than on MFMAs).
 constexpr int64_t kSplitMinDepth = 64;
+// K per workgroup of a split on the ring kernels, at least: shallower ranges
+// of interior tiles run faster as the 256 x 128 kernel's split (1024^3, 64
+// deep on the ring kernels: 44.4 against 55.0 us; 512 x 512 x 4096, 64:
+// 46.7 against 63.9; 1024 x 1024 x 3072, 192: 76.1 against 82.0), deeper
+// ones on the ring kernels (1536^3, 224: 91.3 against 94.1 us; 2048 x 2048 x
+// 1024, 256: 99.8 against 102.6; 1024 x 1024 x 8192, 512: 151.2 against
+// 159.6).
+constexpr int64_t kRingSplitMinDepth = 224;
 // Workgroups of one split launch on the 256 x 128 kernel, at most: two rounds
 // of its two workgroups per CU. Its partials then hold at most this many
 // 256 x 128 tiles (kSplitMaxPartialBytes).
@@ -100,22 +108,23 @@ inline SplitK split_ranges(int64_t k, int64_t s, bool narrow) {
 
 // Time of an m x n x k launch on the 256 x 128 kernel as `groups` equal
 // workgroups of K depth `depth` writing `splits` partials (1 = unsplit, no
-// partials), in tenths of the time a workgroup paired with another on its CU
-// takes per unit of K. The dispatcher fills every CU's two slots round after
-// round, so full rounds of 2 x CUs workgroups each take a pair's time, and so
-// does a last round that pairs workgroups on some CUs; a last round of at
-// most one workgroup per CU runs each alone, in 0.7 of a pair's time. Each
-// workgroup pays a fixed cost worth 32 units of K, and each partial one
-// 8e-6 units per element to write and read back. Fitted to config 2 and
-// seven other ragged launches of 4 to 384 tiles (each split count measured
-// from unsplit to three rounds): the rule's choice ran within 0.6 % of the
-// fastest measured split on every one.
+// partials), in hundredths of the time a workgroup paired with another on its
+// CU takes per unit of K. The dispatcher fills every CU's two slots round
+// after round, so full rounds of 2 x CUs workgroups each take a pair's time,
+// and so does a last round that pairs workgroups on some CUs; a last round of
+// at most one workgroup per CU runs each alone, in 0.65 of a pair's time.
+// Each workgroup pays a fixed cost worth 32 units of K, and each partial one
+// 8e-6 units per element to write and read back. Fitted to sixteen launches
+// of 4 to 384 tiles of 256 x 128 (config 2, seven other ragged shapes and
+// eight of interior tiles, each at four to nine split counts from unsplit to
+// three rounds): the rule's choice ran within 1.6 % of the fastest measured
+// count on every one.
 inline int64_t narrow_time(int64_t m, int64_t n, int64_t groups, int64_t depth, int64_t splits) {
   constexpr int64_t slots = 2 * kComputeUnits;
   const int64_t full = (groups - 1) / slots;
   const int64_t last = groups - full * slots;
-  const int64_t partials = splits > 1 ? splits * m * n / 12500 : 0;
-  return (depth + 32) * (10 * full + (last > kComputeUnits ? 10 : 7)) + partials;
+  const int64_t partials = splits > 1 ? splits * m * n / 1250 : 0;
+  return (depth + 32) * (100 * full + (last > kComputeUnits ? 100 : 65)) + partials;
 }
 
 // The split of an m x n x k launch of form `nt` (A op N, B op T) or not,
@@ -125,7 +134,7 @@ inline int64_t narrow_time(int64_t m, int64_t n, int64_t groups, int64_t depth, 
 // than 2^31 bytes).
 //  - Interior tiles on the ring kernels (one workgroup per CU): as many
 //    ranges as one round of the CUs takes (more rounds only add each
-//    range's fixed costs).
+//    range's fixed costs), when those are at least kRingSplitMinDepth deep.
 //  - Otherwise, on the 256 x 128 kernel, when the launch has fewer than
 //    kComputeUnits tiles of 256 x 256: the number of ranges, within two rounds
 //    of its workgroup slots (kNarrowMaxGroups), that narrow_time rates
@@ -135,16 +144,21 @@ inline SplitK split_k_shape(int64_t m, int64_t n, int64_t k, bool nt, bool ring,
   if (m <= 0 || n <= 0 || k <= 0) return {};
   const bool interior = ring && m % 256 == 0 && n % 256 == 0 && k % (nt ? 4 : 8) == 0;
   const int64_t partial = split_partial_ld(m) * n * 4;
-  int64_t most = k / kSplitMinDepth;
-  if (static_cast<int64_t>(workspace_bytes / partial) < most)
-    most = static_cast<int64_t>(workspace_bytes / partial);
+  const int64_t deepest = k / kSplitMinDepth;
+  const int64_t most =
+      std::min(deepest, static_cast<int64_t>(std::min<uint64_t>(workspace_bytes / partial, 1 << 30)));
   if (most < 2) return {};
   if (interior) {
+    // The kernel family follows from the shape alone, not from the
+    // workspace: a launch given exactly the workspace its split wants
+    // (split_k_bytes_wanted) takes that same split.
     const int64_t tiles = (m / 256) * (n / 256);
-    const int64_t s = std::min(most, kComputeUnits / tiles);
-    if (s < 2) return {};
-    const SplitK sk = split_ranges(k, s, false);
-    return sk.splits >= 2 ? sk : SplitK{};
+    const int64_t one_round = std::min(deepest, kComputeUnits / tiles);
+    if (one_round < 2) return {};
+    if (split_ranges(k, one_round, false).depth >= kRingSplitMinDepth) {
+      const SplitK sk = split_ranges(k, std::min(one_round, most), false);
+      return sk.splits >= 2 ? sk : SplitK{};
+    }
   }
   // At least one 256 x 256 tile per CU runs a 256 x 256 kernel unsplit.
   if (((m + 255) / 256) * ((n + 255) / 256) >= kComputeUnits) return {};
