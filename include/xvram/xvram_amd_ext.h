@@ -147,11 +147,11 @@ typedef struct xvram_amd_ext_v1 {
      cannot allocate (code under stream capture, tight serving loops). No
      counterpart in the reference. A split that desc->workspace cannot hold
      uses the library's static per-GPU scratch of 128 MiB (the most any split
-     wants: one 256 x 256 partial tile per CU, or one 256 x 128 tile per
-     workgroup of two rounds of the 256 x 128 kernel's slots), held until the
-     process ends and shared by every call on that GPU: calls that overlap on
-     one GPU race. A split wanting more returns INVALID_ARGUMENT. Same results
-     as sgemm_device. */
+     wants: one 256 x 256 partial tile per CU, two for a tail split, or one
+     256 x 128 tile per workgroup of two rounds of the 256 x 128 kernel's
+     slots), held until the process ends and shared by every call on that
+     GPU: calls that overlap on one GPU race. A split wanting more returns
+     INVALID_ARGUMENT. Same results as sgemm_device. */
   xvram_status(XVRAM_CALL* sgemm_device_no_alloc)(const xvram_amd_sgemm_v1* desc,
                                                   void* hip_stream);
   uint64_t reserved[1];

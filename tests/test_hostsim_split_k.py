@@ -308,3 +308,91 @@ def test_split_rule_properties(sim):
                         s2, _, narrow2 = split(m, n, k, nt, ring, s * partial - 1)
                         assert s2 < s and (s2 == 1 or narrow2 == narrow)
     assert checked > 500
+
+
+def tail_rule(lib):
+    fn = lib.dll.xvram_hostsim_tail_split_shape
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                   ctypes.c_uint64, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int)]
+
+    def tail(m, n, k, nt, ring, ws):
+        head, depth = ctypes.c_int64(0), ctypes.c_int(0)
+        s = fn(m, n, k, int(nt), int(ring), ws, ctypes.byref(head), ctypes.byref(depth))
+        return s, head.value, depth.value
+    return tail
+
+
+ANY = (1 << 64) - 1
+
+
+@pytest.mark.parametrize("m,n,k,nt,ring,ws,expect", [
+    # 17 x 17 tiles: 2 rounds for 289 tiles -> a head of 15 rows (255 tiles, one round)
+    # and a tail of 2 rows in 7 ranges of 640
+    (4352, 4352, 4352, True, True, ANY, (7, 3840, 640)),
+    # 17 x 16: a head of 16 rows, the last row in 5 ranges of 224
+    (4352, 4096, 1024, False, True, ANY, (5, 4096, 224)),
+    # 20 x 20: a head of 12 rows, 8 rows in 3 ranges (two rounds of the CUs); 64 MiB
+    # hold only 1 partial of the tail: no tail split
+    (5120, 5120, 5120, True, True, ANY, (3, 3072, 1728)),
+    (5120, 5120, 5120, True, True, 64 * MiB_, (1, 0, 0)),
+    # whole rounds already; too shallow to gain; ragged; panels the ring kernels
+    # cannot address; K not a multiple of 8 (N/N)
+    (4096, 4096, 4096, True, True, ANY, (1, 0, 0)),
+    (4352, 4352, 512, True, True, ANY, (1, 0, 0)),
+    (4353, 4352, 4352, True, True, ANY, (1, 0, 0)),
+    (4352, 4352, 4352, True, False, ANY, (1, 0, 0)),
+    (4352, 4352, 4356, False, True, ANY, (1, 0, 0)),
+])
+def test_tail_split_rule(sim, m, n, k, nt, ring, ws, expect):
+    assert tail_rule(sim)(m, n, k, nt, ring, ws) == expect
+
+
+def test_tail_split_properties(sim):
+    """Over a grid of interior shapes of 256 to 1600 tiles: a tail split keeps
+    whole tile rows in the head, ranges at least 224 deep in multiples of 32
+    covering K, at most two rounds of the CUs in the tail (partials <= 128 MiB),
+    never coincides with an ordinary split, and a launch given exactly the
+    workspace the tail wants takes the same tail split."""
+    tail = tail_rule(sim)
+    fn = sim.dll.xvram_hostsim_split_shape
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                   ctypes.c_uint64, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]
+    taken = 0
+    for tm in range(16, 41, 3):
+        for tn in range(16, 41, 5):
+            for k in (512, 1024, 2048, 4096, 8192):
+                m, n = 256 * tm, 256 * tn
+                for nt in (False, True):
+                    s, head, depth = tail(m, n, k, nt, True, ANY)
+                    assert fn(m, n, k, int(nt), 1, ANY, None, None) == 1
+                    if s == 1:
+                        assert head == 0
+                        continue
+                    taken += 1
+                    assert head % 256 == 0 and 0 < head < m
+                    assert depth % 32 == 0 and depth >= 224 and (s - 1) * depth < k <= s * depth
+                    assert (m - head) // 256 * tn * s <= 512
+                    wanted = s * (m - head) * n * 4
+                    assert wanted <= 128 * MiB
+                    assert tail(m, n, k, nt, True, wanted) == (s, head, depth)
+    assert taken > 100
+
+
+@pytest.mark.parametrize("m,frames", [(4352, 4), (4096, 3)])
+def test_planner_reserves_a_frame_for_a_tail_split(sim, m, frames):
+    """4352 x 4096 x 1024 under 256 MiB frames is one launch whose last tile
+    row runs as a split tail: the plan counts the partials' frame in its
+    working set (C, A, B and the partials); 4096 x 4096 x 1024 fills whole
+    rounds and needs none. Planned only (nothing executes)."""
+    n, k = 4096, 1024
+    with session(sim, frame_mib=256, frames=8) as s:
+        A, B, C = s.allocation(m * k * 4), s.allocation(k * n * 4), s.allocation(m * n * 4)
+        plan = xv.GemmPlan(s, xv.matrix(A, m, k, m), xv.matrix(B, k, n, k), xv.matrix(C, m, n, m))
+        info = plan.info()
+        plan.release()
+        for h in (A, B, C):
+            h.release()
+    assert info.tile_count == 1
+    assert info.maximum_working_set_bytes == frames * 256 * MiB

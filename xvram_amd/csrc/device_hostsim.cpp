@@ -62,7 +62,8 @@ struct SimState {
   uint64_t kernel_launches = 0;
   uint64_t split_launches = 0;  // launches that split K (kernels::split_k_plan)
   uint64_t narrow_splits = 0;   // of those, split on the 256 x 128 kernel
-  int last_splits = 0;          // K ranges of the last split launch
+  int last_splits = 0;          // K ranges of the last split launch (or tail split)
+  uint64_t tail_splits = 0;     // launches that ran as a head and a split tail
   int device_count = 1;       // simulated devices 0 .. device_count-1
   int current_device = 0;     // what the calling thread sees as current (-1: none)
   int last_init_ordinal = -1; // the device the last session set up on
@@ -282,38 +283,57 @@ public:
     if ((l.bias_row && !accessible(reinterpret_cast<uint64_t>(l.bias_row), l.m * 4ull)) ||
         (l.bias_col && !accessible(reinterpret_cast<uint64_t>(l.bias_col), l.n * 4ull)))
       return kSimBadAccess;
-    // A split launch writes its partials to the workspace (sgemm_launch.hpp).
+    // A split launch writes its partials to the workspace (sgemm_launch.hpp);
+    // a tail split runs its head rows unsplit and splits its tail rows.
     const kernels::SplitK sk = two ? kernels::SplitK{} : kernels::split_k_plan(l);
-    const int64_t ldp = kernels::split_partial_ld(l.m);
-    const int64_t partial = ldp * l.n;
-    if (sk.splits > 1 && !accessible(reinterpret_cast<uint64_t>(l.workspace),
-                                     static_cast<uint64_t>(sk.splits * partial * 4)))
-      return kSimBadAccess;
+    const kernels::TailSplit ts =
+        two || sk.splits > 1 ? kernels::TailSplit{} : kernels::tail_split_plan(l);
+    struct Rows {
+      int64_t first, count;
+      kernels::SplitK split;
+    };
+    std::vector<Rows> segments;
+    if (ts.head_m > 0)
+      segments = {Rows{0, ts.head_m, kernels::SplitK{}}, Rows{ts.head_m, l.m - ts.head_m, ts.tail}};
+    else
+      segments = {Rows{0, l.m, sk}};
+    for (const Rows& r : segments) {
+      const int64_t partial = kernels::split_partial_ld(r.count) * l.n;
+      if (r.split.splits > 1 && !accessible(reinterpret_cast<uint64_t>(l.workspace),
+                                            static_cast<uint64_t>(r.split.splits * partial * 4)))
+        return kSimBadAccess;
+    }
     // Events attached to the dispatch are stamped around the kernel itself.
     if (l.start_event) recorded_[l.start_event] = std::chrono::steady_clock::now();
     // Column by column; each element accumulates its K products in order
     // (p ascending, the second panel after the first), in FP32. A split
-    // launch accumulates each K range into its partial, then adds the
-    // partials in range order.
+    // launch (or tail) accumulates each K range into its partial, then adds
+    // the partials in range order.
     std::vector<float> acc(static_cast<size_t>(l.m));
     for (int64_t j = 0; j < l.n; ++j) {
       std::fill(acc.begin(), acc.end(), 0.f);
-      for (int s = 0; s < sk.splits && sk.splits > 1; ++s) {
-        float* part = l.workspace + s * partial + j * ldp;
-        std::fill(part, part + l.m, 0.f);
-        const int64_t p_end = std::min<int64_t>(l.k, int64_t{s + 1} * sk.depth);
-        for (int64_t p = int64_t{s} * sk.depth; p < p_end; ++p) {
-          const float y = l.b_ncontig ? l.b[j + p * l.ldb] : l.b[p + j * l.ldb];
-          for (int64_t i = 0; i < l.m; ++i)
-            part[i] += (l.a_kcontig ? l.a[p + i * l.lda] : l.a[i + p * l.lda]) * y;
+      for (const Rows& r : segments) {
+        const int64_t ldp = kernels::split_partial_ld(r.count);
+        const int64_t partial = ldp * l.n;
+        const int64_t i0 = r.first, i1 = r.first + r.count;
+        for (int s = 0; s < r.split.splits && r.split.splits > 1; ++s) {
+          float* part = l.workspace + s * partial + j * ldp;
+          std::fill(part, part + r.count, 0.f);
+          const int64_t p_end = std::min<int64_t>(l.k, int64_t{s + 1} * r.split.depth);
+          for (int64_t p = int64_t{s} * r.split.depth; p < p_end; ++p) {
+            const float y = l.b_ncontig ? l.b[j + p * l.ldb] : l.b[p + j * l.ldb];
+            for (int64_t i = i0; i < i1; ++i)
+              part[i - i0] += (l.a_kcontig ? l.a[p + i * l.lda] : l.a[i + p * l.lda]) * y;
+          }
+          for (int64_t i = i0; i < i1; ++i)
+            acc[i] = s == 0 ? part[i - i0] : acc[i] + part[i - i0];
         }
-        for (int64_t i = 0; i < l.m; ++i) acc[i] = s == 0 ? part[i] : acc[i] + part[i];
-      }
-      for (int64_t p = 0; p < k1 && sk.splits == 1; ++p) {
-        const float y = l.b_ncontig ? l.b[j + p * l.ldb] : l.b[p + j * l.ldb];
-        for (int64_t i = 0; i < l.m; ++i) {
-          const float x = l.a_kcontig ? l.a[p + i * l.lda] : l.a[i + p * l.lda];
-          acc[i] += x * y;
+        for (int64_t p = 0; p < k1 && r.split.splits == 1; ++p) {
+          const float y = l.b_ncontig ? l.b[j + p * l.ldb] : l.b[p + j * l.ldb];
+          for (int64_t i = i0; i < i1; ++i) {
+            const float x = l.a_kcontig ? l.a[p + i * l.lda] : l.a[i + p * l.lda];
+            acc[i] += x * y;
+          }
         }
       }
       for (int64_t p = 0; p < k2; ++p) { // second panel
@@ -339,6 +359,10 @@ public:
       ++g_sim.split_launches;
       if (sk.narrow) ++g_sim.narrow_splits;
       g_sim.last_splits = sk.splits;
+    }
+    if (ts.head_m > 0) {
+      ++g_sim.tail_splits;
+      g_sim.last_splits = ts.tail.splits;
     }
     return 0;
   }
@@ -451,6 +475,7 @@ extern "C" __attribute__((visibility("default"))) void xvram_hostsim_reset() {
   g_sim.split_launches = 0;
   g_sim.narrow_splits = 0;
   g_sim.last_splits = 0;
+  g_sim.tail_splits = 0;
   g_sim.device_count = 1;
   g_sim.current_device = 0;
   g_sim.last_init_ordinal = -1;
@@ -506,6 +531,26 @@ extern "C" __attribute__((visibility("default"))) int xvram_hostsim_split_shape(
 
 // Of those, the launches whose ranges ran on the 256 x 128 kernel (tiles that
 // are not all interior 256 x 256 ones).
+// The tail split rule (kernels::tail_split_shape) for a launch shape: returns
+// the number of K ranges of the tail (1 = no tail split), *head_m the head's
+// rows and *depth the tail's range depth.
+extern "C" __attribute__((visibility("default"))) int xvram_hostsim_tail_split_shape(
+    int64_t m, int64_t n, int64_t k, int nt, int ring, uint64_t workspace_bytes, int64_t* head_m,
+    int* depth) {
+  const xvram::kernels::TailSplit ts =
+      xvram::kernels::tail_split_shape(m, n, k, nt != 0, ring != 0, workspace_bytes);
+  if (head_m != nullptr) *head_m = ts.head_m;
+  if (depth != nullptr) *depth = ts.head_m > 0 ? ts.tail.depth : 0;
+  return ts.head_m > 0 ? ts.tail.splits : 1;
+}
+
+// Launches that ran as a head and a split tail since the last reset.
+extern "C" __attribute__((visibility("default"))) uint64_t xvram_hostsim_tail_split_launches() {
+  using namespace xvram;
+  std::lock_guard<std::mutex> lock(g_sim.mutex);
+  return g_sim.tail_splits;
+}
+
 extern "C" __attribute__((visibility("default"))) uint64_t xvram_hostsim_narrow_split_launches() {
   using namespace xvram;
   std::lock_guard<std::mutex> lock(g_sim.mutex);

@@ -413,14 +413,18 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   out.tiles_m = ceil_div(p.m, tm);
   out.tiles_n = ceil_div(p.n, tn);
   out.panels_k = ceil_div(p.k, bk);
-  // A launch that leaves workgroup slots idle splits its K, its partials in
-  // one frame of the pool (kernels::split_k_shape for the plan's tile and
-  // panel; its panels are below 2^31 bytes): that frame is taken from the
-  // schedule's.
-  out.scratch = frame_count >= 4 &&
-                kernels::split_k_shape(static_cast<int64_t>(tm), static_cast<int64_t>(tn),
-                                       static_cast<int64_t>(bk), !p.a.transposed && p.b.transposed,
-                                       true, F).splits > 1;
+  // A launch that leaves workgroup slots idle splits its K (or its tail
+  // rows' K), its partials in one frame of the pool (kernels::split_k_shape
+  // and kernels::tail_split_shape for the plan's tile and panel; its panels
+  // are below 2^31 bytes): that frame is taken from the schedule's.
+  {
+    const int64_t sm = static_cast<int64_t>(tm), sn = static_cast<int64_t>(tn),
+                  sk = static_cast<int64_t>(bk);
+    const bool nt_form = !p.a.transposed && p.b.transposed;
+    out.scratch = frame_count >= 4 &&
+                  (kernels::split_k_shape(sm, sn, sk, nt_form, true, F).splits > 1 ||
+                   kernels::tail_split_shape(sm, sn, sk, nt_form, true, F).head_m > 0);
+  }
   if (out.scratch) --frame_count;
 
   // Lookahead: launches whose panels are acquired (and pinned) before they are
@@ -462,13 +466,15 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   // executor keeps the panels of the coming pass out of victim selection
   // (Runtime::set_protected), without which such a tight budget evicted panels
   // before their last use (32768^3 under 2 GiB of 64 MiB frames: 23 % more H2D).
+  // Not with a partials frame: a launch whose tiles leave a last round mostly
+  // idle gains more from a tail split than from a second panel.
   uint32_t panels = 1;
   const double one_panel_flops = launch_flops(tm, tn, bk);
   const bool nt = !p.a.transposed && p.b.transposed;
   const bool two_panel_kernel = tm % 256 == 0 && tn % 256 == 0 &&
                                 (tm / 256) * (tn / 256) >= 256 && p.m % tm == 0 &&
                                 p.n % tn == 0 && bk % 32 == 0 && p.k % (nt ? 4 : 8) == 0 &&
-                                out.panels_k >= 2;
+                                out.panels_k >= 2 && !out.scratch;
   if (two_panel_kernel && one_panel_flops <= kTwoPanelMaxFlops &&
       (max_launch_flops == 0 || 2.0 * one_panel_flops <= static_cast<double>(max_launch_flops))) {
     const uint32_t ahead2 = std::max<uint32_t>(1, lookahead / 2);

@@ -17,13 +17,13 @@ namespace {
 // The split-K workspace of the allocation-free entry point: one array per
 // GPU in this file's code object, held until the process ends and shared by
 // every call on that GPU (calls that overlap on one GPU race on it). A split
-// never wants more: at most one 256 x 256 partial tile per CU (ring kernels)
-// or one 256 x 128 tile per workgroup of two rounds of two per CU (the 256 x
-// 128 kernel). Every partial element the reduction uses is written before it
+// never wants more: at most one 256 x 256 partial tile per CU (ring kernels;
+// two per CU for a tail split) or one 256 x 128 tile per workgroup of two
+// rounds of two per CU (the 256 x 128 kernel). Every partial element the reduction uses is written before it
 // is read (the padding rows of a ragged partial are read but not used), so
 // nothing in the array needs clearing between calls.
 constexpr uint64_t kScratchBytes = 128ull << 20;
-static_assert(kScratchBytes >= uint64_t(kernels::kComputeUnits) * 256 * 256 * 4 &&
+static_assert(kScratchBytes >= uint64_t(2 * kernels::kComputeUnits) * 256 * 256 * 4 &&
                   kScratchBytes >= kernels::kSplitMaxPartialBytes,
               "the scratch holds the largest split");
 static __device__ __align__(256) float scratch[kScratchBytes / 4];

@@ -33,7 +33,9 @@
 // split on the 256 x 128 kernel (two workgroups per CU) when a split runs
 // faster by narrow_time. The order of the additions is fixed, so C
 // is the same from run to run. Without a workspace large enough for two
-// partials the launch runs unsplit. One K panel only.
+// partials the launch runs unsplit. One K panel only. A launch of at least
+// 256 interior tiles whose last round would leave CUs idle may run as a
+// head and a split tail instead (tail_split_plan below).
 //
 // start_event / stop_event (hipEvent_t, optional) are recorded by the dispatch
 // itself (hipExtLaunchKernelGGL): no separate marker packets run between
@@ -196,13 +198,78 @@ inline SplitK split_k_plan(const SgemmLaunch& l) {
   return split_k_for(l, l.workspace_bytes);
 }
 
-// Bytes of partials a launch's split wants when the workspace is not the
-// limit (0: it does not split).
+// Tail split. A launch of at least kComputeUnits interior 256 x 256 tiles
+// runs in rounds of one workgroup per CU, and a last round that fills few
+// CUs costs as much as a full one (17 x 17 tiles: 2 rounds for 289 tiles).
+// It may run instead as a head, tile rows [0, head_m) unsplit in whole
+// rounds, followed by a tail, rows [head_m, m), whose K is split on the ring
+// kernels (up to two rounds of ranges at least kRingSplitMinDepth deep, the
+// partials in the workspace), when the model below rates that at most 0.9
+// of the unsplit launch. Time is counted in units of K of one round: the head
+// takes its rounds x K, the tail its rounds x (range depth + 48), plus 128 for
+// its extra launch and the reduction.
+struct TailSplit {
+  int64_t head_m = 0; // rows of the head (a multiple of 256); 0 = no tail split
+  SplitK tail;        // the split of the tail's m - head_m rows
+};
+
+inline TailSplit tail_split_shape(int64_t m, int64_t n, int64_t k, bool nt, bool ring,
+                                  uint64_t workspace_bytes) {
+  if (!ring || m <= 0 || n <= 0 || k <= 0 || m % 256 != 0 || n % 256 != 0 || k % (nt ? 4 : 8) != 0)
+    return {};
+  const int64_t tiles_m = m / 256, tiles_n = n / 256, tiles = tiles_m * tiles_n;
+  if (tiles < kComputeUnits) return {};
+  const auto rounds = [](int64_t groups) { return (groups + kComputeUnits - 1) / kComputeUnits; };
+  const int64_t unsplit = rounds(tiles) * k;
+  TailSplit best{};
+  int64_t best_time = unsplit;
+  for (int64_t t = 1; t < tiles_m && 2 * t * tiles_n <= 2 * kComputeUnits; ++t) {
+    const int64_t tail_tiles = t * tiles_n;
+    const uint64_t partial = uint64_t(t) * 256 * uint64_t(n) * 4;
+    const int64_t head_time = rounds((tiles_m - t) * tiles_n) * k;
+    for (int64_t s = 2; s <= k / kSplitMinDepth; ++s) {
+      const SplitK sk = split_ranges(k, s, false);
+      if (sk.depth < kRingSplitMinDepth || tail_tiles * sk.splits > 2 * kComputeUnits ||
+          uint64_t(sk.splits) * partial > workspace_bytes)
+        break;
+      const int64_t time = head_time + rounds(tail_tiles * sk.splits) * (sk.depth + 48) + 128;
+      if (time < best_time) {
+        best_time = time;
+        best = TailSplit{(tiles_m - t) * 256, sk};
+      }
+    }
+  }
+  return 10 * best_time <= 9 * unsplit ? best : TailSplit{};
+}
+
+// The tail split a launch takes given room for `workspace_bytes` of
+// partials: none for a two-panel launch or panels the ring kernels cannot
+// address, else tail_split_shape.
+inline TailSplit tail_split_for(const SgemmLaunch& l, uint64_t workspace_bytes) {
+  constexpr int64_t kLimit = int64_t(1) << 31;
+  if (l.a2 != nullptr || l.b2 != nullptr) return {};
+  const int64_t a_bytes = (l.a_kcontig ? int64_t{l.m} : int64_t{l.k}) * l.lda * 4;
+  const int64_t b_bytes = (l.b_ncontig ? int64_t{l.k} : int64_t{l.n}) * l.ldb * 4;
+  return tail_split_shape(l.m, l.n, l.k, !l.a_kcontig && l.b_ncontig,
+                          a_bytes < kLimit && b_bytes < kLimit, workspace_bytes);
+}
+
+// The tail split of one launch with its own 16-byte aligned workspace.
+inline TailSplit tail_split_plan(const SgemmLaunch& l) {
+  if (l.workspace == nullptr || reinterpret_cast<uintptr_t>(l.workspace) % 16 != 0) return {};
+  return tail_split_for(l, l.workspace_bytes);
+}
+
+// Bytes of partials a launch's split (or tail split) wants when the
+// workspace is not the limit (0: it does not split).
 inline uint64_t split_k_bytes_wanted(const SgemmLaunch& l) {
   const SplitK sk = split_k_for(l, ~uint64_t{0});
-  return sk.splits > 1
-             ? static_cast<uint64_t>(sk.splits) * uint64_t(split_partial_ld(l.m)) * uint64_t(l.n) * 4
-             : 0;
+  if (sk.splits > 1)
+    return static_cast<uint64_t>(sk.splits) * uint64_t(split_partial_ld(l.m)) * uint64_t(l.n) * 4;
+  const TailSplit ts = tail_split_for(l, ~uint64_t{0});
+  return ts.head_m > 0 ? static_cast<uint64_t>(ts.tail.splits) * uint64_t(l.m - ts.head_m) *
+                             uint64_t(l.n) * 4
+                       : 0;
 }
 
 // Enqueues the launch on `stream` (a hipStream_t); returns a hipError_t.

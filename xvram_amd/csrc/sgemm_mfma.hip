@@ -368,6 +368,30 @@ int launch_sgemm(const SgemmLaunch& launch, void* stream) {
     if (err != hipSuccess) return static_cast<int>(err);
     return static_cast<int>(launch_splitk_reduce(p, s, e1));
   }
+  // A last round of 256 x 256 tiles that would fill few CUs: the head's
+  // tile rows unsplit, then the tail's rows split (sgemm_launch.hpp); the
+  // start event rides on the head's dispatch, the stop event on the tail's
+  // reduction.
+  if (const TailSplit ts = tail_split_plan(launch); ts.head_m > 0) {
+    Params head = p;
+    head.m = static_cast<int>(ts.head_m);
+    head.tiles_m = static_cast<int>(ts.head_m / wide_tile());
+    head.tiles_n = launch.n / wide_tile();
+    if (const hipError_t e = launch_wide(head, launch.a_kcontig, launch.b_ncontig, s, e0, nullptr);
+        e != hipSuccess)
+      return static_cast<int>(e);
+    Params tail = p;
+    tail.a = launch.a_kcontig ? launch.a + ts.head_m * launch.lda : launch.a + ts.head_m;
+    tail.c = launch.c + ts.head_m;
+    if (tail.bias_row != nullptr) tail.bias_row += ts.head_m;
+    tail.m = launch.m - static_cast<int>(ts.head_m);
+    tail.tiles_m = tail.m / wide_tile();
+    tail.tiles_n = launch.n / wide_tile();
+    tail.splits = ts.tail.splits;
+    tail.split_depth = ts.tail.depth;
+    tail.partial = launch.workspace;
+    return static_cast<int>(launch_wide(tail, launch.a_kcontig, launch.b_ncontig, s, nullptr, e1));
+  }
   if (wide_fits(launch)) {
     p.tiles_m = (launch.m + wide_tile() - 1) / wide_tile();
     p.tiles_n = (launch.n + wide_tile() - 1) / wide_tile();
