@@ -94,8 +94,9 @@ for _oa, _ob in ((OP_N, OP_N), (OP_N, OP_T), (OP_T, OP_N), (OP_T, OP_T)):
     DEVICE[f"device_c2_{'nt'[_oa]}{'nt'[_ob]}"] = (3001, 2047, 4099, _oa, _ob, 1.5, 0.5)
 # Square GEMMs whose 256 x 256 tiles leave a last round of the CUs mostly
 # idle (4352^3: 289 tiles; 4608^3: 324; 6144^3: 576), which run as a head and
-# a split tail, beside 4096^3 (256 tiles, whole rounds).
-for _s in (4096, 4352, 4608, 6144):
+# a split tail, beside 4096^3 (256 tiles, whole rounds); and ragged ones
+# (5000^3, 7000^3), which run as their interior tiles and two edge strips.
+for _s in (4096, 4352, 4608, 6144, 5000, 7000):
     DEVICE[f"device_{_s}_nt"] = (_s, _s, _s, OP_N, OP_T, 1.0, 0.0)
 DEFAULT = "ns65536_nt_16g"
 # Config 5: 8 x [Y = ReLU(X W^T + b)], X 256 x 16384 ~ N(0,1), W 16384 x 16384 and

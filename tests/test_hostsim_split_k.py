@@ -396,3 +396,52 @@ def test_planner_reserves_a_frame_for_a_tail_split(sim, m, frames):
             h.release()
     assert info.tile_count == 1
     assert info.maximum_working_set_bytes == frames * 256 * MiB
+
+
+def edge_rule(lib):
+    fn = lib.dll.xvram_hostsim_edge_split_shape
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                   ctypes.POINTER(ctypes.c_int)]
+
+    def edge(m, n, k, nt):
+        wants = ctypes.c_int(0)
+        return fn(m, n, k, int(nt), ctypes.byref(wants)), wants.value
+    return edge
+
+
+@pytest.mark.parametrize("m,n,k,nt,expect", [
+    # 20 x 20 tiles, ragged: interior 19 x 19 (tail split) and two strips, which split
+    (5000, 5000, 5000, True, (1, 1)),
+    (8191, 8191, 2048, True, (1, 1)),
+    (4100, 4100, 1024, False, (1, 1)),
+    # one full round already: the strips' cost outweighs the edge tiles'
+    (4000, 4000, 12000, True, (0, 0)),
+    # K not a multiple of 8 (N/N; N/T takes it), fewer than 256 tiles, interior, too shallow
+    (4500, 4500, 4500, False, (0, 0)),
+    (4500, 4500, 4500, True, (1, 1)),
+    (2000, 2000, 2000, True, (0, 0)),
+    (4096, 4096, 4096, True, (0, 0)),
+    (4100, 4100, 240, False, (0, 0)),
+])
+def test_edge_split_rule(sim, m, n, k, nt, expect):
+    assert edge_rule(sim)(m, n, k, nt) == expect
+
+
+def test_edge_split_pattern_is_exact(sim, oracle_mod):
+    """4100 x 4100 x 248 under 128 MiB frames, one launch of 17 x 17 ragged
+    tiles: it runs as the 16 x 16 interior tiles, the right strip (4096 x 4)
+    and the bottom strip (4 x 4100), each a launch of its own (the strips
+    split K in the partials' frame the planner reserved); every element of C
+    bit-exact on the analytic pattern."""
+    m, n, k = 4100, 4100, 248
+    a_op, b_op = pattern_operands(m, n, k)
+    sim.dll.xvram_hostsim_edge_split_launches.restype = ctypes.c_uint64
+    sim.dll.xvram_hostsim_kernel_launches.restype = ctypes.c_uint64
+    with session(sim, frame_mib=128, frames=8) as s:
+        (out,), info = run(s, a_op, b_op, FORMS["NN"])
+    assert info.tile_count == 1
+    assert info.maximum_working_set_bytes == 4 * 128 * MiB  # C, A, B and the partials' frame
+    assert sim.dll.xvram_hostsim_edge_split_launches() == 1
+    assert sim.dll.xvram_hostsim_kernel_launches() == 3
+    assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))

@@ -45,12 +45,14 @@ def test_no_alloc_matches_sgemm_device(lib, oracle_mod):
         # (2 x 2 tiles of 256 x 128, 32 ranges, partials of leading dimension
         # 504), then config 2's shape (192 tiles of 256 x 128, 5 ranges: 117
         # MiB of partials, most of the 128 MiB scratch), then a tail split
-        # (17 x 16 tiles: 16 rows unsplit, the last row in 5 ranges).
+        # (17 x 16 tiles: 16 rows unsplit, the last row in 5 ranges), then an
+        # edge split (4100 x 4100: the 16 x 16 interior and two split strips).
         for call, (m, n, k, form, seed) in enumerate([(4096, 256, 4096, "NN", 601),
                                                       (1024, 512, 2048, "NT", 602),
                                                       (501, 200, 2048, "TN", 603),
                                                       (3001, 2047, 4099, "NN", 604),
-                                                      (4352, 4096, 1024, "TT", 605)]):
+                                                      (4352, 4096, 1024, "TT", 605),
+                                                      (4100, 4100, 1024, "NT", 606)]):
             ops = FORMS[form]
             a_op = np.asfortranarray(oracle_mod.fill_uniform(m * k, seed).reshape(k, m).T)
             b_op = np.asfortranarray(oracle_mod.fill_uniform(k * n, seed + 1).reshape(n, k).T)

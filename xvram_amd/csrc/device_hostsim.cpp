@@ -64,6 +64,7 @@ struct SimState {
   uint64_t narrow_splits = 0;   // of those, split on the 256 x 128 kernel
   int last_splits = 0;          // K ranges of the last split launch (or tail split)
   uint64_t tail_splits = 0;     // launches that ran as a head and a split tail
+  uint64_t edge_splits = 0;     // launches that ran as an interior and edge strips
   int device_count = 1;       // simulated devices 0 .. device_count-1
   int current_device = 0;     // what the calling thread sees as current (-1: none)
   int last_init_ordinal = -1; // the device the last session set up on
@@ -256,6 +257,18 @@ public:
 
   int launch_sgemm(const kernels::SgemmLaunch& l, Stream) override {
     if (int f = fault(kLaunch)) return f;
+    // An edge split runs its parts one after another (sgemm_launch.hpp).
+    if (const kernels::EdgeParts e = kernels::edge_parts(l); e.count > 0) {
+      for (int i = 0; i < e.count; ++i)
+        if (const int rc = run_launch(e.part[i]); rc != 0) return rc;
+      std::lock_guard<std::mutex> lock(g_sim.mutex);
+      ++g_sim.edge_splits;
+      return 0;
+    }
+    return run_launch(l);
+  }
+
+  int run_launch(const kernels::SgemmLaunch& l) {
     // Same launch contract as the gfx950 kernel (sgemm_launch.hpp).
     const bool aligned = reinterpret_cast<uintptr_t>(l.a) % 16 == 0 &&
                          reinterpret_cast<uintptr_t>(l.b) % 16 == 0 &&
@@ -476,6 +489,7 @@ extern "C" __attribute__((visibility("default"))) void xvram_hostsim_reset() {
   g_sim.narrow_splits = 0;
   g_sim.last_splits = 0;
   g_sim.tail_splits = 0;
+  g_sim.edge_splits = 0;
   g_sim.device_count = 1;
   g_sim.current_device = 0;
   g_sim.last_init_ordinal = -1;
@@ -542,6 +556,23 @@ extern "C" __attribute__((visibility("default"))) int xvram_hostsim_tail_split_s
   if (head_m != nullptr) *head_m = ts.head_m;
   if (depth != nullptr) *depth = ts.head_m > 0 ? ts.tail.depth : 0;
   return ts.head_m > 0 ? ts.tail.splits : 1;
+}
+
+// The edge split rule for a launch shape (panels the ring kernels can
+// address): 1 if kernels::edge_split_rated_faster takes it, and *wants = 1 if
+// one of its parts would split (kernels::edge_split_wants_workspace).
+extern "C" __attribute__((visibility("default"))) int xvram_hostsim_edge_split_shape(
+    int64_t m, int64_t n, int64_t k, int nt, int* wants) {
+  if (wants != nullptr)
+    *wants = xvram::kernels::edge_split_wants_workspace(m, n, k, nt != 0) ? 1 : 0;
+  return xvram::kernels::edge_split_rated_faster(m, n, k, nt != 0) ? 1 : 0;
+}
+
+// Launches that ran as an interior and edge strips since the last reset.
+extern "C" __attribute__((visibility("default"))) uint64_t xvram_hostsim_edge_split_launches() {
+  using namespace xvram;
+  std::lock_guard<std::mutex> lock(g_sim.mutex);
+  return g_sim.edge_splits;
 }
 
 // Launches that ran as a head and a split tail since the last reset.

@@ -414,16 +414,18 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   out.tiles_n = ceil_div(p.n, tn);
   out.panels_k = ceil_div(p.k, bk);
   // A launch that leaves workgroup slots idle splits its K (or its tail
-  // rows' K), its partials in one frame of the pool (kernels::split_k_shape
-  // and kernels::tail_split_shape for the plan's tile and panel; its panels
-  // are below 2^31 bytes): that frame is taken from the schedule's.
+  // rows' K, or that of the parts of its edge split), its partials in one
+  // frame of the pool (kernels::split_k_shape, tail_split_shape and
+  // edge_split_wants_workspace for the plan's tile and panel; its panels are
+  // below 2^31 bytes): that frame is taken from the schedule's.
   {
     const int64_t sm = static_cast<int64_t>(tm), sn = static_cast<int64_t>(tn),
                   sk = static_cast<int64_t>(bk);
     const bool nt_form = !p.a.transposed && p.b.transposed;
     out.scratch = frame_count >= 4 &&
                   (kernels::split_k_shape(sm, sn, sk, nt_form, true, F).splits > 1 ||
-                   kernels::tail_split_shape(sm, sn, sk, nt_form, true, F).head_m > 0);
+                   kernels::tail_split_shape(sm, sn, sk, nt_form, true, F).head_m > 0 ||
+                   kernels::edge_split_wants_workspace(sm, sn, sk, nt_form));
   }
   if (out.scratch) --frame_count;
 

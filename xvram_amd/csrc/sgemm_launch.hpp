@@ -213,33 +213,47 @@ struct TailSplit {
   SplitK tail;        // the split of the tail's m - head_m rows
 };
 
-inline TailSplit tail_split_shape(int64_t m, int64_t n, int64_t k, bool nt, bool ring,
-                                  uint64_t workspace_bytes) {
-  if (!ring || m <= 0 || n <= 0 || k <= 0 || m % 256 != 0 || n % 256 != 0 || k % (nt ? 4 : 8) != 0)
-    return {};
-  const int64_t tiles_m = m / 256, tiles_n = n / 256, tiles = tiles_m * tiles_n;
-  if (tiles < kComputeUnits) return {};
-  const auto rounds = [](int64_t groups) { return (groups + kComputeUnits - 1) / kComputeUnits; };
-  const int64_t unsplit = rounds(tiles) * k;
+// The rounds of one workgroup per CU that `groups` workgroups take.
+inline int64_t cu_rounds(int64_t groups) { return (groups + kComputeUnits - 1) / kComputeUnits; }
+
+// The tail split of an interior m x n x k launch (none: head_m 0) and, in
+// *time, the model's time of the launch as it then runs (tail split or not).
+inline TailSplit tail_split_timed(int64_t m, int64_t n, int64_t k, uint64_t workspace_bytes,
+                                  int64_t* time) {
+  const int64_t tiles_m = m / 256, tiles_n = n / 256;
+  const int64_t unsplit = cu_rounds(tiles_m * tiles_n) * k;
   TailSplit best{};
   int64_t best_time = unsplit;
   for (int64_t t = 1; t < tiles_m && 2 * t * tiles_n <= 2 * kComputeUnits; ++t) {
     const int64_t tail_tiles = t * tiles_n;
     const uint64_t partial = uint64_t(t) * 256 * uint64_t(n) * 4;
-    const int64_t head_time = rounds((tiles_m - t) * tiles_n) * k;
+    const int64_t head_time = cu_rounds((tiles_m - t) * tiles_n) * k;
     for (int64_t s = 2; s <= k / kSplitMinDepth; ++s) {
       const SplitK sk = split_ranges(k, s, false);
       if (sk.depth < kRingSplitMinDepth || tail_tiles * sk.splits > 2 * kComputeUnits ||
           uint64_t(sk.splits) * partial > workspace_bytes)
         break;
-      const int64_t time = head_time + rounds(tail_tiles * sk.splits) * (sk.depth + 48) + 128;
+      const int64_t time = head_time + cu_rounds(tail_tiles * sk.splits) * (sk.depth + 48) + 128;
       if (time < best_time) {
         best_time = time;
         best = TailSplit{(tiles_m - t) * 256, sk};
       }
     }
   }
-  return 10 * best_time <= 9 * unsplit ? best : TailSplit{};
+  if (10 * best_time > 9 * unsplit) {
+    best = TailSplit{};
+    best_time = unsplit;
+  }
+  if (time != nullptr) *time = best_time;
+  return best;
+}
+
+inline TailSplit tail_split_shape(int64_t m, int64_t n, int64_t k, bool nt, bool ring,
+                                  uint64_t workspace_bytes) {
+  if (!ring || m <= 0 || n <= 0 || k <= 0 || m % 256 != 0 || n % 256 != 0 || k % (nt ? 4 : 8) != 0)
+    return {};
+  if ((m / 256) * (n / 256) < kComputeUnits) return {};
+  return tail_split_timed(m, n, k, workspace_bytes, nullptr);
 }
 
 // The tail split a launch takes given room for `workspace_bytes` of
@@ -262,7 +276,7 @@ inline TailSplit tail_split_plan(const SgemmLaunch& l) {
 
 // Bytes of partials a launch's split (or tail split) wants when the
 // workspace is not the limit (0: it does not split).
-inline uint64_t split_k_bytes_wanted(const SgemmLaunch& l) {
+inline uint64_t split_k_bytes_wanted_whole(const SgemmLaunch& l) {
   const SplitK sk = split_k_for(l, ~uint64_t{0});
   if (sk.splits > 1)
     return static_cast<uint64_t>(sk.splits) * uint64_t(split_partial_ld(l.m)) * uint64_t(l.n) * 4;
@@ -270,6 +284,119 @@ inline uint64_t split_k_bytes_wanted(const SgemmLaunch& l) {
   return ts.head_m > 0 ? static_cast<uint64_t>(ts.tail.splits) * uint64_t(l.m - ts.head_m) *
                              uint64_t(l.n) * 4
                        : 0;
+}
+
+// Edge split. A launch whose m or n is not a multiple of 256 and that has at
+// least kComputeUnits tiles of 256 x 256 runs every tile on the general 256 x
+// 256 kernel, whose ragged edge tiles take its predicated loop (5000^3: 2.70-
+// 2.76 ms, 91 TFLOP/s). It may run instead as up to three launches of its own,
+// one after another on its stream: the interior rows [0, mi) x columns
+// [0, ni) (mi, ni = m, n rounded down to 256; ring kernels, or their tail
+// split), the right strip rows [0, mi) x columns [ni, n) and the bottom strip
+// rows [mi, m) x columns [0, n), each split by the rules above (the strips on
+// the 256 x 128 kernel), sharing the workspace. Every element of C is computed
+// by one of them. Taken when a model rates it faster, in units of K of one
+// round: the whole launch takes its rounds x K x 5/4 (the edge tiles' cost,
+// measured 1.16-1.5 on six shapes); the split takes the interior's time
+// (tail_split_timed, one round for fewer than kComputeUnits tiles), plus the
+// strips' 256 x 128 tiles x K x 3.5 / 512 (their split launches, reductions
+// and mostly empty tiles, measured on 4000 x 4000 x 12000 and 8191 x 8191 x
+// 2048), plus 280 for the two extra launches. The model's times came within
+// 6 % of the split launches measured on 4100^2 x 4096, 5000^3, 7000^3 and
+// 10000^2 x 4000.
+// Only for one-panel launches with K a multiple of 4 (N/T) or 8 (the other
+// forms), so that the interior runs on the ring kernels (with K ragged the
+// general kernel's interior tiles gain nothing: 6000 x 6000 x 6002 ran 1-3 %
+// slower split), and panels below 2^31 bytes; when a part would split, only
+// with a workspace (a strip unsplit would leave most CUs idle).
+inline bool edge_split_rated_faster(int64_t m, int64_t n, int64_t k, bool nt) {
+  if (m <= 0 || n <= 0 || k <= 0 || k % (nt ? 4 : 8) != 0) return false;
+  const int64_t mi = m / 256 * 256, ni = n / 256 * 256;
+  const int64_t whole_tiles = ((m + 255) / 256) * ((n + 255) / 256);
+  if ((mi == m && ni == n) || whole_tiles < kComputeUnits || mi == 0 || ni == 0) return false;
+  const int64_t whole = cu_rounds(whole_tiles) * k * 5 / 4;
+  const int64_t interior_tiles = (mi / 256) * (ni / 256);
+  int64_t interior = cu_rounds(interior_tiles) * k;
+  if (interior_tiles >= kComputeUnits) tail_split_timed(mi, ni, k, ~uint64_t{0}, &interior);
+  // The strips' 256 x 128 tiles (the bottom strip's one row of them, the
+  // right strip's column of them).
+  const int64_t strip_tiles = (m > mi ? (n + 127) / 128 : 0) + (mi / 256) * ((n - ni + 127) / 128);
+  const int64_t split = interior + 7 * k * strip_tiles / (4 * kComputeUnits) + 280;
+  return split < whole;
+}
+
+struct EdgeParts {
+  int count = 0; // 0 = no edge split
+  SgemmLaunch part[3];
+};
+
+// Rows [r0, r0 + rows) x columns [c0, c0 + cols) of a launch as a launch of
+// its own (no events).
+inline SgemmLaunch sub_launch(const SgemmLaunch& l, int64_t r0, int rows, int64_t c0, int cols) {
+  SgemmLaunch s = l;
+  s.a = l.a_kcontig ? l.a + r0 * l.lda : l.a + r0;
+  s.b = l.b_ncontig ? l.b + c0 : l.b + c0 * l.ldb;
+  s.c = l.c + r0 + c0 * l.ldc;
+  if (s.bias_row != nullptr) s.bias_row += r0;
+  if (s.bias_col != nullptr) s.bias_col += c0;
+  s.m = rows;
+  s.n = cols;
+  s.start_event = nullptr;
+  s.stop_event = nullptr;
+  return s;
+}
+
+// The parts of a launch's edge split by shape alone (count 0: none).
+inline EdgeParts edge_parts_shape(const SgemmLaunch& l) {
+  constexpr int64_t kLimit = int64_t(1) << 31;
+  EdgeParts e;
+  if (l.a2 != nullptr || l.b2 != nullptr || l.m <= 0 || l.n <= 0 || l.k <= 0) return e;
+  const bool nt = !l.a_kcontig && l.b_ncontig;
+  const int64_t a_bytes = (l.a_kcontig ? int64_t{l.m} : int64_t{l.k}) * l.lda * 4;
+  const int64_t b_bytes = (l.b_ncontig ? int64_t{l.k} : int64_t{l.n}) * l.ldb * 4;
+  if (a_bytes >= kLimit || b_bytes >= kLimit || !edge_split_rated_faster(l.m, l.n, l.k, nt))
+    return e;
+  const int mi = l.m / 256 * 256, ni = l.n / 256 * 256;
+  e.part[e.count++] = sub_launch(l, 0, mi, 0, ni);
+  if (ni < l.n) e.part[e.count++] = sub_launch(l, 0, mi, ni, l.n - ni);
+  if (mi < l.m) e.part[e.count++] = sub_launch(l, mi, l.m - mi, 0, l.n);
+  e.part[0].start_event = l.start_event;
+  e.part[e.count - 1].stop_event = l.stop_event;
+  return e;
+}
+
+// The parts of a launch's edge split (count 0: none): by shape, and without a
+// workspace only when no part would split.
+inline EdgeParts edge_parts(const SgemmLaunch& l) {
+  const EdgeParts e = edge_parts_shape(l);
+  if (e.count == 0 || l.workspace != nullptr) return e;
+  for (int i = 0; i < e.count; ++i)
+    if (split_k_bytes_wanted_whole(e.part[i]) > 0) return {};
+  return e;
+}
+
+// Whether an m x n x k launch of form `nt` whose panels the ring kernels can
+// address would take an edge split one of whose parts splits (the planner
+// then gives its launches a workspace).
+inline bool edge_split_wants_workspace(int64_t m, int64_t n, int64_t k, bool nt) {
+  if (!edge_split_rated_faster(m, n, k, nt)) return false;
+  const int64_t mi = m / 256 * 256, ni = n / 256 * 256;
+  constexpr uint64_t kAny = ~uint64_t{0};
+  return split_k_shape(mi, ni, k, nt, true, kAny).splits > 1 ||
+         tail_split_shape(mi, ni, k, nt, true, kAny).head_m > 0 ||
+         (ni < n && split_k_shape(mi, n - ni, k, nt, true, kAny).splits > 1) ||
+         (mi < m && split_k_shape(m - mi, n, k, nt, true, kAny).splits > 1);
+}
+
+// Bytes of partials a launch wants when the workspace is not the limit: the
+// most any part of its edge split wants (they run one after another on the
+// stream, so they share it), else its own split's (0: it does not split).
+inline uint64_t split_k_bytes_wanted(const SgemmLaunch& l) {
+  const EdgeParts e = edge_parts_shape(l);
+  if (e.count == 0) return split_k_bytes_wanted_whole(l);
+  uint64_t most = 0;
+  for (int i = 0; i < e.count; ++i) most = std::max(most, split_k_bytes_wanted_whole(e.part[i]));
+  return most;
 }
 
 // Enqueues the launch on `stream` (a hipStream_t); returns a hipError_t.
