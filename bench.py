@@ -98,6 +98,9 @@ for _oa, _ob in ((OP_N, OP_N), (OP_N, OP_T), (OP_T, OP_N), (OP_T, OP_T)):
 # (5000^3, 7000^3), which run as their interior tiles and two edge strips.
 for _s in (4096, 4352, 4608, 6144, 5000, 7000):
     DEVICE[f"device_{_s}_nt"] = (_s, _s, _s, OP_N, OP_T, 1.0, 0.0)
+# 4500^3 N/N: K not a multiple of 8, so the launch runs over K = 4496 (an edge
+# split) and then the last 4 K rows.
+DEVICE["device_4500_nn"] = (4500, 4500, 4500, OP_N, OP_N, 1.0, 0.0)
 DEFAULT = "ns65536_nt_16g"
 # Config 5: 8 x [Y = ReLU(X W^T + b)], X 256 x 16384 ~ N(0,1), W 16384 x 16384 and
 # b ~ N(0, 1/16384), 2 GiB budget of 64 MiB frames; one step = one 8-layer forward.

@@ -153,3 +153,22 @@ def test_edge_split_in_a_session(lib, synth, oracle_mod, form):
     bad = int(np.count_nonzero(got != expect))
     log(f"session pattern {m}x{n}x{k} {form}: {bad} of {m * n} differ")
     assert bad == 0
+
+
+@pytest.mark.parametrize("m,n,k,form", [(4100, 4100, 1028, "NN"), (4352, 4096, 1027, "TT"),
+                                        (4100, 4100, 1030, "NT")],
+                         ids=["edge-NN", "tail-TT", "edge-NT"])
+def test_k_remainder_within_bound(lib, hip, oracle_mod, m, n, k, form):
+    """K not a multiple of 8 (N/N, T/T) or 4 (N/T): the launch runs over the
+    rounded K (an edge or tail split, no epilogue) and then over the last 2-4
+    K rows onto that result (beta 1, the epilogue): alpha, beta, a per-row
+    bias and ReLU, every element within the FP64 bound, repeats bit-identical."""
+    from test_gpu_sgemm_device import run_device_gemm
+
+    outs, ref, absab = run_device_gemm(lib, hip, oracle_mod, m, n, k, FORMS[form], 811,
+                                       alpha=0.75, beta=-1.25, bias_rows=True, relu=True,
+                                       repeat=2)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    bad, _, ratio = oracle_mod.check_bound(np.asfortranarray(outs[0]), k, ref, absab)
+    log(f"{m}x{n}x{k} {form} (K remainder): violations {bad}, err/bound {ratio:.3e}")
+    assert bad == 0

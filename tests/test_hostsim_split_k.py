@@ -445,3 +445,39 @@ def test_edge_split_pattern_is_exact(sim, oracle_mod):
     assert sim.dll.xvram_hostsim_edge_split_launches() == 1
     assert sim.dll.xvram_hostsim_kernel_launches() == 3
     assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))
+
+
+@pytest.mark.parametrize("m,n,k,nt,expect", [
+    # K % 8 = 4 (N/N): the rounded 4096 takes an edge split -> a K remainder
+    (5000, 5000, 4100, False, 4096),
+    # the same K for N/T is a multiple of 4: no remainder needed
+    (5000, 5000, 4100, True, 0),
+    # interior 17 x 17 tiles, K % 8 = 3: the rounded K takes a tail split
+    (4352, 4352, 4099, False, 4096),
+    # the rounded K would gain nothing (whole rounds), too shallow, or fewer than 256 tiles
+    (4096, 4096, 4099, False, 0),
+    (5000, 5000, 507, False, 0),
+    (3001, 2047, 4099, False, 0),
+])
+def test_k_remainder_rule(sim, m, n, k, nt, expect):
+    fn = sim.dll.xvram_hostsim_k_remainder_shape
+    fn.restype = ctypes.c_int64
+    fn.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int]
+    assert fn(m, n, k, int(nt)) == expect
+
+
+def test_k_remainder_pattern_is_exact(sim, oracle_mod):
+    """4100 x 4100 x 516 N/N under 128 MiB frames: K % 8 = 4, and the rounded
+    512 takes an edge split, so the launch runs as the 512-deep edge split
+    (no epilogue) and a 4-deep launch onto its result; every element of C
+    bit-exact on the analytic pattern."""
+    m, n, k = 4100, 4100, 516
+    a_op, b_op = pattern_operands(m, n, k)
+    sim.dll.xvram_hostsim_k_remainder_launches.restype = ctypes.c_uint64
+    sim.dll.xvram_hostsim_edge_split_launches.restype = ctypes.c_uint64
+    with session(sim, frame_mib=128, frames=8) as s:
+        (out,), info = run(s, a_op, b_op, FORMS["NN"])
+    assert info.tile_count == 1 and info.maximum_working_set_bytes == 4 * 128 * MiB
+    assert sim.dll.xvram_hostsim_k_remainder_launches() == 1
+    assert sim.dll.xvram_hostsim_edge_split_launches() == 1
+    assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))

@@ -65,6 +65,7 @@ struct SimState {
   int last_splits = 0;          // K ranges of the last split launch (or tail split)
   uint64_t tail_splits = 0;     // launches that ran as a head and a split tail
   uint64_t edge_splits = 0;     // launches that ran as an interior and edge strips
+  uint64_t k_remainders = 0;    // launches that ran as a rounded K and its remainder
   int device_count = 1;       // simulated devices 0 .. device_count-1
   int current_device = 0;     // what the calling thread sees as current (-1: none)
   int last_init_ordinal = -1; // the device the last session set up on
@@ -257,7 +258,19 @@ public:
 
   int launch_sgemm(const kernels::SgemmLaunch& l, Stream) override {
     if (int f = fault(kLaunch)) return f;
-    // An edge split runs its parts one after another (sgemm_launch.hpp).
+    // A K remainder runs its two launches one after another, and so does an
+    // edge split its parts (sgemm_launch.hpp).
+    if (const kernels::KParts kp = kernels::k_remainder_parts(l); kp.count > 0) {
+      for (int i = 0; i < kp.count; ++i)
+        if (const int rc = dispatch(kp.part[i]); rc != 0) return rc;
+      std::lock_guard<std::mutex> lock(g_sim.mutex);
+      ++g_sim.k_remainders;
+      return 0;
+    }
+    return dispatch(l);
+  }
+
+  int dispatch(const kernels::SgemmLaunch& l) {
     if (const kernels::EdgeParts e = kernels::edge_parts(l); e.count > 0) {
       for (int i = 0; i < e.count; ++i)
         if (const int rc = run_launch(e.part[i]); rc != 0) return rc;
@@ -490,6 +503,7 @@ extern "C" __attribute__((visibility("default"))) void xvram_hostsim_reset() {
   g_sim.last_splits = 0;
   g_sim.tail_splits = 0;
   g_sim.edge_splits = 0;
+  g_sim.k_remainders = 0;
   g_sim.device_count = 1;
   g_sim.current_device = 0;
   g_sim.last_init_ordinal = -1;
@@ -566,6 +580,19 @@ extern "C" __attribute__((visibility("default"))) int xvram_hostsim_edge_split_s
   if (wants != nullptr)
     *wants = xvram::kernels::edge_split_wants_workspace(m, n, k, nt != 0) ? 1 : 0;
   return xvram::kernels::edge_split_rated_faster(m, n, k, nt != 0) ? 1 : 0;
+}
+
+// Launches that ran as a rounded K and its remainder since the last reset.
+extern "C" __attribute__((visibility("default"))) uint64_t xvram_hostsim_k_remainder_launches() {
+  using namespace xvram;
+  std::lock_guard<std::mutex> lock(g_sim.mutex);
+  return g_sim.k_remainders;
+}
+
+// The K remainder rule for a launch shape: the rounded K (0: none).
+extern "C" __attribute__((visibility("default"))) int64_t xvram_hostsim_k_remainder_shape(
+    int64_t m, int64_t n, int64_t k, int nt) {
+  return xvram::kernels::k_remainder_shape(m, n, k, nt != 0);
 }
 
 // Launches that ran as an interior and edge strips since the last reset.

@@ -414,9 +414,10 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
   out.tiles_n = ceil_div(p.n, tn);
   out.panels_k = ceil_div(p.k, bk);
   // A launch that leaves workgroup slots idle splits its K (or its tail
-  // rows' K, or that of the parts of its edge split), its partials in one
-  // frame of the pool (kernels::split_k_shape, tail_split_shape and
-  // edge_split_wants_workspace for the plan's tile and panel; its panels are
+  // rows' K, or that of the parts of its edge split, or of the first part of
+  // its K remainder), its partials in one frame of the pool
+  // (kernels::split_k_shape, tail_split_shape, edge_split_wants_workspace and
+  // k_remainder_wants_workspace for the plan's tile and panel; its panels are
   // below 2^31 bytes): that frame is taken from the schedule's.
   {
     const int64_t sm = static_cast<int64_t>(tm), sn = static_cast<int64_t>(tn),
@@ -425,7 +426,8 @@ Error make_gemm_plan(const GemmSpec& spec, uint64_t frame_bytes, uint64_t total_
     out.scratch = frame_count >= 4 &&
                   (kernels::split_k_shape(sm, sn, sk, nt_form, true, F).splits > 1 ||
                    kernels::tail_split_shape(sm, sn, sk, nt_form, true, F).head_m > 0 ||
-                   kernels::edge_split_wants_workspace(sm, sn, sk, nt_form));
+                   kernels::edge_split_wants_workspace(sm, sn, sk, nt_form) ||
+                   kernels::k_remainder_wants_workspace(sm, sn, sk, nt_form));
   }
   if (out.scratch) --frame_count;
 

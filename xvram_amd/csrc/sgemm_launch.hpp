@@ -388,15 +388,88 @@ inline bool edge_split_wants_workspace(int64_t m, int64_t n, int64_t k, bool nt)
          (mi < m && split_k_shape(m - mi, n, k, nt, true, kAny).splits > 1);
 }
 
+// K remainder. The ring kernels need K a multiple of 4 (N/T) or 8 (the other
+// forms), and so do the tail and edge splits. A launch whose K is not, and
+// whose K rounded down to that multiple (at least 512) would take a tail or
+// an edge split, runs as two launches of its own: the first over the rounded
+// K with alpha and beta and no epilogue, the second over the remaining 1 to 7
+// K rows with alpha and beta 1 onto the first's result, then the epilogue
+// (one more read and write of C: 4500^3 N/N, 2.30 ms as one launch on the
+// general kernel, gains far more from the split first part). Returns the
+// rounded K (0: no K remainder).
+inline int64_t k_remainder_shape(int64_t m, int64_t n, int64_t k, bool nt) {
+  if (m <= 0 || n <= 0 || k <= 0) return 0;
+  const int64_t k1 = k - k % (nt ? 4 : 8);
+  if (k1 == k || k1 < 512) return 0;
+  const bool interior = m % 256 == 0 && n % 256 == 0;
+  const bool gains = interior ? tail_split_shape(m, n, k1, nt, true, ~uint64_t{0}).head_m > 0
+                              : edge_split_rated_faster(m, n, k1, nt);
+  return gains ? k1 : 0;
+}
+
+struct KParts {
+  int count = 0; // 0 = no K remainder
+  SgemmLaunch part[2];
+};
+
+// The two launches of a K remainder by shape (count 0: none); one-panel
+// launches whose panels the ring kernels can address only.
+inline KParts k_remainder_parts_shape(const SgemmLaunch& l) {
+  constexpr int64_t kLimit = int64_t(1) << 31;
+  KParts r;
+  if (l.a2 != nullptr || l.b2 != nullptr) return r;
+  const int64_t a_bytes = (l.a_kcontig ? int64_t{l.m} : int64_t{l.k}) * l.lda * 4;
+  const int64_t b_bytes = (l.b_ncontig ? int64_t{l.k} : int64_t{l.n}) * l.ldb * 4;
+  if (a_bytes >= kLimit || b_bytes >= kLimit) return r;
+  const int64_t k1 = k_remainder_shape(l.m, l.n, l.k, !l.a_kcontig && l.b_ncontig);
+  if (k1 == 0) return r;
+  SgemmLaunch first = l;
+  first.k = static_cast<int>(k1);
+  first.bias_row = nullptr;
+  first.bias_col = nullptr;
+  first.relu = false;
+  first.stop_event = nullptr;
+  SgemmLaunch rest = l;
+  rest.k = l.k - static_cast<int>(k1);
+  rest.a = l.a_kcontig ? l.a + k1 : l.a + k1 * l.lda;
+  rest.b = l.b_ncontig ? l.b + k1 * l.ldb : l.b + k1;
+  rest.beta = 1.f;
+  rest.start_event = nullptr;
+  r.part[0] = first;
+  r.part[1] = rest;
+  r.count = 2;
+  return r;
+}
+
 // Bytes of partials a launch wants when the workspace is not the limit: the
-// most any part of its edge split wants (they run one after another on the
-// stream, so they share it), else its own split's (0: it does not split).
+// first part's of a K remainder; else the most any part of its edge split
+// wants (they run one after another on the stream, so they share it); else
+// its own split's (0: it does not split).
 inline uint64_t split_k_bytes_wanted(const SgemmLaunch& l) {
-  const EdgeParts e = edge_parts_shape(l);
-  if (e.count == 0) return split_k_bytes_wanted_whole(l);
+  const KParts kp = k_remainder_parts_shape(l);
+  const SgemmLaunch& base = kp.count > 0 ? kp.part[0] : l;
+  const EdgeParts e = edge_parts_shape(base);
+  if (e.count == 0) return split_k_bytes_wanted_whole(base);
   uint64_t most = 0;
   for (int i = 0; i < e.count; ++i) most = std::max(most, split_k_bytes_wanted_whole(e.part[i]));
   return most;
+}
+
+// The two launches of a K remainder (count 0: none): by shape, and without a
+// workspace only when the first part would not split.
+inline KParts k_remainder_parts(const SgemmLaunch& l) {
+  const KParts kp = k_remainder_parts_shape(l);
+  if (kp.count == 0 || l.workspace != nullptr || split_k_bytes_wanted(kp.part[0]) == 0) return kp;
+  return {};
+}
+
+// Whether a plan's m x n x k launch of form `nt` would take a K remainder
+// whose first part splits (the planner then gives its launches a workspace).
+inline bool k_remainder_wants_workspace(int64_t m, int64_t n, int64_t k, bool nt) {
+  const int64_t k1 = k_remainder_shape(m, n, k, nt);
+  if (k1 == 0) return false;
+  return tail_split_shape(m, n, k1, nt, true, ~uint64_t{0}).head_m > 0 ||
+         edge_split_wants_workspace(m, n, k1, nt);
 }
 
 // Enqueues the launch on `stream` (a hipStream_t); returns a hipError_t.

@@ -314,6 +314,13 @@ int launch_sgemm(const SgemmLaunch& launch, void* stream) {
   // out-of-memory hipMemCreate the cache already handled, for one): consume
   // that first so it is not reported as a launch failure.
   (void)hipGetLastError();
+  // K not a multiple of the ring kernels' step where a tail or edge split
+  // would pay: the rounded K, then the rest (sgemm_launch.hpp).
+  if (const KParts kp = k_remainder_parts(launch); kp.count > 0) {
+    for (int i = 0; i < kp.count; ++i)
+      if (const int rc = launch_sgemm(kp.part[i], stream); rc != 0) return rc;
+    return 0;
+  }
   // Ragged m or n over many tiles: the interior and the edge strips as
   // launches of their own (sgemm_launch.hpp), one after another.
   if (const EdgeParts e = edge_parts(launch); e.count > 0) {
