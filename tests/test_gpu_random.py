@@ -5,7 +5,10 @@ Each case draws m, n, k, the N/T forms, the storage layout of A, B and C
 beta, and a cache configuration: resident (whole operands in one frame) or
 out of core (small frames, so the planner tiles C and splits K and the panels
 stream through a few frames). A quarter of the cases are large enough that
-their launches run a 256 x 256 kernel; the rest run the 256 x 128 kernel,
+their launches run a 256 x 256 kernel (ragged ones of more than one round of
+tiles as an edge split: ring interior, strips on the 256 x 128 kernel, and
+with K not a multiple of 8 possibly a K remainder); the rest run the 256 x
+128 kernel,
 many with ragged edges in every dimension. Six more cases are N/T with m and n
 multiples of 256, so their large launches run the barrier-free N/T kernel, and
 six are N/N, T/N or T/T with such m and n and K a multiple of 8 (the

@@ -19,6 +19,11 @@ into LDS in 8-deep slots): the NN, TN and TT interior and pattern cases above
 run it, and the ring8 cases add its slot tails, alpha/beta and the shapes
 that fall back to sgemm_wide_kernel.
 
+Ragged launches of more than one round of tiles mostly take an edge split
+(interior on the ring kernels, strips apart; tests/test_gpu_edge_split.py), and
+interior ones of K not a multiple of 8 a K remainder; the ragged cases here are
+one round of 16 x 16 tiles, which stay whole on sgemm_wide_kernel.
+
 Random cases are checked element by element against the FP64 oracle on three
 column ranges (first, middle and last tile columns, every row) with the bound
 |C - C_ref| <= 4*K*2^-24*(|alpha|(|A||B|)_ij + |beta*C0_ij|); the analytic
@@ -87,8 +92,10 @@ def test_wide_interior(resident, oracle_mod, ops):
 
 @pytest.mark.parametrize("ops", OPS, ids=OP_IDS)
 def test_wide_edges_alpha_beta(resident, oracle_mod, ops):
-    """4100 x 3950 x 1001: edge tiles on both sides and a partial last K stage."""
-    m, n, k = 4100, 3950, 1001
+    """4000 x 3950 x 1001: edge tiles on both sides and a partial last K stage
+    (16 x 16 tiles: one round, so the launch stays whole on this kernel rather
+    than taking an edge split)."""
+    m, n, k = 4000, 3950, 1001
     prob = Problem(uniform(oracle_mod, m, k, 1201), uniform(oracle_mod, k, n, 1202),
                    uniform(oracle_mod, m, n, 1203), op_a=ops[0], op_b=ops[1],
                    alpha=-1.25, beta=0.75)
@@ -129,12 +136,13 @@ def test_ring_k_tails_pattern(resident, oracle_mod, k):
     assert np.array_equal(out.astype(np.float64), expected)
 
 
-@pytest.mark.parametrize("m,n,k", [(4096, 4096, 1001), (4100, 4096, 1040), (4096, 4352 + 8, 1040)],
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 1001), (4000, 4096, 1040), (4096, 4000, 1040)],
                          ids=["k%4", "m%256", "n%256"])
 def test_ring_fallback_shapes_pattern(resident, oracle_mod, m, n, k):
     """N/T launches just outside the barrier-free kernel's conditions (K not a
-    multiple of 4, or m or n not a multiple of 256) run sgemm_wide_kernel:
-    bit-exact pattern."""
+    multiple of 4, or m or n not a multiple of 256, in one round of 16 x 16
+    tiles, which no edge split or K remainder would speed up) run
+    sgemm_wide_kernel: bit-exact pattern."""
     a_op, b_op = pattern_operands(m, n, k)
     prob = Problem(a_op, b_op, op_b=abi.OP_T)
     out = prob.run(resident)
@@ -173,11 +181,12 @@ def test_ring8_alpha_beta(resident, oracle_mod, ops):
     sampled_check(oracle_mod, prob, out, f"ring8 alpha/beta {ops}")
 
 
-@pytest.mark.parametrize("ops,m,k", [(OPS[0], 4096, 1004), (OPS[2], 4100, 1040), (OPS[3], 4096, 1020)],
+@pytest.mark.parametrize("ops,m,k", [(OPS[0], 4096, 1004), (OPS[2], 4000, 1040), (OPS[3], 4096, 1020)],
                          ids=["NN-k%8", "TN-m%256", "TT-k%8"])
 def test_ring8_fallback_shapes_pattern(resident, oracle_mod, ops, m, k):
     """Launches just outside that kernel's conditions (K not a multiple of 8,
-    m not a multiple of 256) run sgemm_wide_kernel: bit-exact pattern."""
+    m not a multiple of 256; one round of 16 x 16 tiles) run sgemm_wide_kernel:
+    bit-exact pattern."""
     n = 4096
     a_op, b_op = pattern_operands(m, n, k)
     prob = Problem(a_op, b_op, op_a=ops[0], op_b=ops[1])
@@ -194,7 +203,7 @@ def test_ring_alpha_beta(resident, oracle_mod):
     sampled_check(oracle_mod, prob, out, "ring alpha/beta")
 
 
-@pytest.mark.parametrize("n", [4200, 4096], ids=["wide", "ring"])
+@pytest.mark.parametrize("n", [4000, 4096], ids=["wide", "ring"])
 @pytest.mark.parametrize("axis", [abi.BIAS_PER_ROW, abi.BIAS_PER_COLUMN], ids=["row", "col"])
 def test_wide_epilogue(lib, oracle_mod, axis, n):
     m, k = 4096, 800

@@ -184,7 +184,7 @@ MiB_ = 1 << 20
     (4000, 3000, 2000, True, True, 1 << 30, (2, 1024, 1)),
     # 256 tiles of 256 x 256 fill the chip
     (4096, 4096, 4096, True, True, 64 * MiB_, (1, 0, 0)),
-    # ragged, but 17 x 16 tiles of 256 x 256: the general 256 x 256 kernel, unsplit
+    # ragged, but 17 x 16 tiles of 256 x 256: no split K (an edge split, if any, is its own rule)
     (4100, 4096, 4096, True, True, 64 * MiB_, (1, 0, 0)),
     # interior but K not a multiple of 8 (N/N): the 256 x 128 kernel; N/T splits on the ring
     (1024, 1024, 1004, False, True, 64 * MiB_, (8, 128, 1)),

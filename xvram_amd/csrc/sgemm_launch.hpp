@@ -198,6 +198,10 @@ inline SplitK split_k_plan(const SgemmLaunch& l) {
   return split_k_for(l, l.workspace_bytes);
 }
 
+// K below this runs on a plain kernel (each thread four rows of one column of
+// C), not the MFMA tiles: a K remainder's last 1-7 rows, or any such launch.
+constexpr int kThinK = 8;
+
 // Tail split. A launch of at least kComputeUnits interior 256 x 256 tiles
 // runs in rounds of one workgroup per CU, and a last round that fills few
 // CUs costs as much as a full one (17 x 17 tiles: 2 rounds for 289 tiles).

@@ -58,6 +58,8 @@ int wide_tile();
 hipError_t launch_wide(const device::Params& p, bool a_kcontig, bool b_ncontig,
                        hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 hipError_t launch_splitk_reduce(const device::Params& p, hipStream_t stream, hipEvent_t stop);
+hipError_t launch_thin_k(const device::Params& p, bool a_kcontig, bool b_ncontig,
+                         hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 
 namespace {
 
@@ -360,6 +362,9 @@ int launch_sgemm(const SgemmLaunch& launch, void* stream) {
     return static_cast<int>(launch_wide(p, launch.a_kcontig, launch.b_ncontig, s, e0, e1));
   }
   p.k_split = 0;
+  // K below 8: no MFMA tiles (sgemm_wide.hip, thin_k_kernel).
+  if (launch.k < kThinK)
+    return static_cast<int>(launch_thin_k(p, launch.a_kcontig, launch.b_ncontig, s, e0, e1));
   // Fewer tiles than workgroup slots: split K when a workspace is given
   // (fixed-order reduction; sgemm_launch.hpp), on the ring kernels for
   // interior 256 x 256 tiles, else on the 256 x 128 kernel.

@@ -899,6 +899,65 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(Params p) {
   }
 }
 
+// A launch of K below 8 (a K remainder's last rows): too little work for the
+// MFMA tiles, whose prologue and C round trip it would pay in full, so each
+// thread forms four rows of one column of the product with FP32
+// multiply-adds in K order and applies the tile epilogue's arithmetic
+// (alpha, beta, bias, ReLU), reading and writing C as 16-byte vectors.
+// HBM-bound: about 8 bytes of C per element.
+template <bool AK, bool BN>
+__global__ __launch_bounds__(kThreads) void thin_k_kernel(Params p) {
+  const int64_t per_col = ((int64_t)p.m + 3) / 4;
+  const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (idx >= per_col * p.n) return;
+  const int col = (int)(idx / per_col);
+  const int row = (int)(idx - (int64_t)col * per_col) * 4;
+  const int rows = min(4, p.m - row);
+  float sum[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < p.k; ++q) {
+    const float y = BN ? p.b[col + (int64_t)q * p.ldb] : p.b[q + (int64_t)col * p.ldb];
+    if (!AK && rows == 4) {
+      const float4 x = *reinterpret_cast<const float4*>(p.a + row + (int64_t)q * p.lda);
+      sum[0] += x.x * y;
+      sum[1] += x.y * y;
+      sum[2] += x.z * y;
+      sum[3] += x.w * y;
+    } else {
+      for (int t = 0; t < rows; ++t)
+        sum[t] += (AK ? p.a[q + (int64_t)(row + t) * p.lda] : p.a[row + t + (int64_t)q * p.lda]) * y;
+    }
+  }
+  float* cp = p.c + (int64_t)col * p.ldc + row;
+  const bool extra = p.bias_row != nullptr || p.bias_col != nullptr || p.relu != 0;
+  const float bias_c = p.bias_col != nullptr ? p.bias_col[col] : 0.f;
+  const auto finish = [&](float v, int r) {
+    if (p.bias_row != nullptr) v += p.bias_row[r];
+    v += bias_c;
+    return (p.relu != 0 && v < 0.f) ? 0.f : v;
+  };
+  if (rows == 4) {
+    float r[4] = {p.alpha * sum[0], p.alpha * sum[1], p.alpha * sum[2], p.alpha * sum[3]};
+    if (p.beta != 0.f) {
+      const float4 old = *reinterpret_cast<const float4*>(cp);
+      r[0] = p.alpha * sum[0] + p.beta * old.x;
+      r[1] = p.alpha * sum[1] + p.beta * old.y;
+      r[2] = p.alpha * sum[2] + p.beta * old.z;
+      r[3] = p.alpha * sum[3] + p.beta * old.w;
+    }
+    if (extra) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) r[t] = finish(r[t], row + t);
+    }
+    *reinterpret_cast<float4*>(cp) = make_float4(r[0], r[1], r[2], r[3]);
+    return;
+  }
+  for (int t = 0; t < rows; ++t) {
+    const float val = p.alpha * sum[t];
+    const float out = p.beta != 0.f ? val + p.beta * cp[t] : val;
+    cp[t] = extra ? finish(out, row + t) : out;
+  }
+}
+
 } // namespace
 
 int wide_tile() { return kTile; }
@@ -910,6 +969,23 @@ hipError_t launch_splitk_reduce(const Params& p, hipStream_t stream, hipEvent_t 
   const int64_t quads = (((int64_t)p.m + 3) / 4) * p.n;
   const dim3 grid(static_cast<unsigned>((quads + kThreads - 1) / kThreads));
   hipExtLaunchKernelGGL(splitk_reduce_kernel, grid, dim3(kThreads), 0, stream, nullptr, stop, 0, p);
+  return hipGetLastError();
+}
+
+// Launches thin_k_kernel for `p` (K below 8); start / stop (optional) are
+// recorded by the dispatch.
+hipError_t launch_thin_k(const Params& p, bool a_kcontig, bool b_ncontig, hipStream_t stream,
+                         hipEvent_t start, hipEvent_t stop) {
+  const int64_t quads = (((int64_t)p.m + 3) / 4) * p.n;
+  const dim3 grid(static_cast<unsigned>((quads + kThreads - 1) / kThreads)), block(kThreads);
+  if (!a_kcontig && !b_ncontig)
+    hipExtLaunchKernelGGL((thin_k_kernel<false, false>), grid, block, 0, stream, start, stop, 0, p);
+  else if (!a_kcontig && b_ncontig)
+    hipExtLaunchKernelGGL((thin_k_kernel<false, true>), grid, block, 0, stream, start, stop, 0, p);
+  else if (a_kcontig && !b_ncontig)
+    hipExtLaunchKernelGGL((thin_k_kernel<true, false>), grid, block, 0, stream, start, stop, 0, p);
+  else
+    hipExtLaunchKernelGGL((thin_k_kernel<true, true>), grid, block, 0, stream, start, stop, 0, p);
   return hipGetLastError();
 }
 
