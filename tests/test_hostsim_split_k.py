@@ -481,3 +481,32 @@ def test_k_remainder_pattern_is_exact(sim, oracle_mod):
     assert sim.dll.xvram_hostsim_k_remainder_launches() == 1
     assert sim.dll.xvram_hostsim_edge_split_launches() == 1
     assert np.array_equal(out.astype(np.float64), oracle_mod.pattern_expected_matrix(m, n, k))
+
+
+def test_partials_never_exceed_the_allocation_free_scratch(sim):
+    """Over seeded random launch shapes (small to 16384 wide, ragged or not, K
+    down to 1, every form, panels near and past the ring kernels' 2^31-byte
+    limit): the partials any launch wants -- its split, tail split, the
+    largest part of its edge split or the first part of its K remainder --
+    fit the allocation-free entry's 128 MiB scratch."""
+    fn = sim.dll.xvram_hostsim_bytes_wanted
+    fn.restype = ctypes.c_uint64
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                   ctypes.c_int64, ctypes.c_int64]
+    rng = np.random.default_rng(97)
+    most, split = 0, 0
+    for _ in range(20000):
+        scale = int(rng.choice([512, 4096, 16384]))
+        m, n = (int(v) for v in rng.integers(1, scale + 1, 2))
+        k = int(rng.integers(1, 3 * scale))
+        if rng.random() < 0.5:
+            m, n = 256 * max(1, m // 256), 256 * max(1, n // 256)
+        ak, bn = (bool(v) for v in rng.integers(0, 2, 2))
+        lda = (k if ak else m) + 4 * int(rng.integers(0, 3))
+        ldb = (n if bn else k) + 4 * int(rng.integers(0, 3))
+        lda, ldb = (lda + 3) // 4 * 4, (ldb + 3) // 4 * 4
+        wanted = fn(m, n, k, int(ak), int(bn), lda, ldb)
+        most = max(most, wanted)
+        split += wanted > 0
+        assert wanted <= 128 * MiB, (m, n, k, ak, bn, wanted)
+    assert split > 1000 and most > 64 * MiB

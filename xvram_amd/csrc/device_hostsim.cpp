@@ -595,6 +595,22 @@ extern "C" __attribute__((visibility("default"))) int64_t xvram_hostsim_k_remain
   return xvram::kernels::k_remainder_shape(m, n, k, nt != 0);
 }
 
+// The partials' bytes a launch wants (kernels::split_k_bytes_wanted) for a
+// launch of that shape, form and leading dimensions (pointers unused).
+extern "C" __attribute__((visibility("default"))) uint64_t xvram_hostsim_bytes_wanted(
+    int m, int n, int k, int a_kcontig, int b_ncontig, int64_t lda, int64_t ldb) {
+  xvram::kernels::SgemmLaunch l;
+  l.m = m;
+  l.n = n;
+  l.k = k;
+  l.a_kcontig = a_kcontig != 0;
+  l.b_ncontig = b_ncontig != 0;
+  l.lda = lda;
+  l.ldb = ldb;
+  l.ldc = m;
+  return xvram::kernels::split_k_bytes_wanted(l);
+}
+
 // Launches that ran as an interior and edge strips since the last reset.
 extern "C" __attribute__((visibility("default"))) uint64_t xvram_hostsim_edge_split_launches() {
   using namespace xvram;
