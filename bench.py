@@ -98,9 +98,15 @@ for _oa, _ob in ((OP_N, OP_N), (OP_N, OP_T), (OP_T, OP_N), (OP_T, OP_T)):
 # (5000^3, 7000^3), which run as their interior tiles and two edge strips.
 for _s in (4096, 4352, 4608, 6144, 5000, 7000):
     DEVICE[f"device_{_s}_nt"] = (_s, _s, _s, OP_N, OP_T, 1.0, 0.0)
-# 4500^3 N/N: K not a multiple of 8, so the launch runs over K = 4496 (an edge
-# split) and then the last 4 K rows.
+# 4500^3 N/N and T/N: K not a multiple of 8, so the launch runs over K = 4496
+# (an edge split) and then the last 4 K rows (thin-K kernel).
 DEVICE["device_4500_nn"] = (4500, 4500, 4500, OP_N, OP_N, 1.0, 0.0)
+DEVICE["device_4500_tn"] = (4500, 4500, 4500, OP_T, OP_N, 1.0, 0.0)
+# Ragged with whole rounds of 256 x 256 tiles (32 x 32 tiles: 4 rounds): the
+# whole launch on the ring kernels' edge instances; with K = 8190 (N/N) first
+# over K = 8184, then the last 6 K rows.
+DEVICE["device_8191_nt"] = (8191, 8191, 8192, OP_N, OP_T, 1.0, 0.0)
+DEVICE["device_8191k_nn"] = (8191, 8191, 8190, OP_N, OP_N, 1.0, 0.0)
 DEFAULT = "ns65536_nt_16g"
 # Config 5: 8 x [Y = ReLU(X W^T + b)], X 256 x 16384 ~ N(0,1), W 16384 x 16384 and
 # b ~ N(0, 1/16384), 2 GiB budget of 64 MiB frames; one step = one 8-layer forward.
@@ -621,10 +627,15 @@ def run_device(args, xv, lib, synth) -> int:
             raise RuntimeError(f"{what} failed: hipError {rc}")
 
     def stored(rows, cols, seed):
+        # Element (r, c) is draw c * rows + r of the seeded stream whatever the
+        # padding (so the spread check can regenerate it); padding rows are 0.
         ld = (rows + 3) // 4 * 4
-        host = np.empty(ld * cols, dtype=np.float32)
-        synth.synth_fill_uniform(host.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
-                                 host.size, seed, 0)
+        vals = np.empty(rows * cols, dtype=np.float32)
+        synth.synth_fill_uniform(vals.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                 vals.size, seed, 0)
+        host = np.zeros((cols, ld), dtype=np.float32)
+        host[:, :rows] = vals.reshape(cols, rows)
+        host = host.reshape(-1)
         ptr = ctypes.c_void_p()
         ok(rt.hipMalloc(ctypes.byref(ptr), ctypes.c_size_t(host.nbytes)), "hipMalloc")
         ok(rt.hipMemcpy(ptr, host.ctypes.data_as(ctypes.c_void_p), ctypes.c_size_t(host.nbytes),
@@ -683,8 +694,8 @@ def run_device(args, xv, lib, synth) -> int:
 
     import oracle
 
-    if flops <= 2e10:
-        # Every element against the FP64 oracle.
+    if flops <= 6e10 or (alpha, beta) != (1.0, 0.0):
+        # Every element against the FP64 oracle (configs 1 and 2 among them).
         def logical(host, rows, cols, ld, op):
             st = host.reshape(cols, ld)[:, :rows].T
             return np.asfortranarray(st if op == OP_N else st.T)
@@ -697,11 +708,10 @@ def run_device(args, xv, lib, synth) -> int:
         elements = m * n
     else:
         # The spread sample (one full column per tile column, one full row per
-        # tile row, seeded random elements) of an alpha 1, beta 0 product
-        # whose operands have no padding rows.
+        # tile row, seeded random elements) of an alpha 1, beta 0 product.
         from oracle.sample import SeededOperand, spread_check
 
-        assert alpha == 1.0 and beta == 0.0 and lda == a_rows and ldb == b_rows and ldc == m
+        assert alpha == 1.0 and beta == 0.0
         check = spread_check(SeededOperand(1, a_rows, a_cols, op_a == OP_T),
                              SeededOperand(2, b_rows, b_cols, op_b == OP_T),
                              lambda j0, j1: out.reshape(n, ldc)[j0:j1, :m].T, 256, 256, seed=7,

@@ -4,9 +4,11 @@ ABI (the extension's sgemm_device on device memory), every element checked.
 The shapes are drawn so that each of the dispatch rules of sgemm_launch.hpp
 fires several times: split K on the ring kernels and on the 256 x 128 kernel
 (fewer tiles than CUs, one or two rounds of ranges), the tail split (interior
-launches of at least 256 tiles whose last round would leave CUs idle) and the
+launches of at least 256 tiles whose last round would leave CUs idle), the
 edge split (ragged launches of at least 256 tiles: interior, right strip,
-bottom strip), in random N/T forms, with K a multiple of 8 and, for some, not.
+bottom strip) and the whole ragged launch on the ring kernels' edge instances
+(6981 x 4328 x 3928 here), in random N/T forms, with K a multiple of 8 and,
+for some, not.
 Operands are the analytic pattern (examples' gemm_bench pattern: exact in FP32
 for these K), so every element of C must equal its closed form bit for bit,
 whichever split, order of ranges or part computed it."""

@@ -19,10 +19,12 @@ into LDS in 8-deep slots): the NN, TN and TT interior and pattern cases above
 run it, and the ring8 cases add its slot tails, alpha/beta and the shapes
 that fall back to sgemm_wide_kernel.
 
-Ragged launches of more than one round of tiles mostly take an edge split
-(interior on the ring kernels, strips apart; tests/test_gpu_edge_split.py), and
-interior ones of K not a multiple of 8 a K remainder; the ragged cases here are
-one round of 16 x 16 tiles, which stay whole on sgemm_wide_kernel.
+Ragged launches whose K is a multiple of 4 (N/T) or 8 run whole on the ring
+kernels' edge instances (tests/test_gpu_edge_ring.py) or take an edge split
+(interior on the ring kernels, strips apart; tests/test_gpu_edge_split.py),
+and those whose K is not, with K rounded down at least 512, a K remainder; the
+ragged random case here has K = 501 and stays whole on sgemm_wide_kernel, and
+the ragged pattern cases of the ring tests below run the edge instances.
 
 Random cases are checked element by element against the FP64 oracle on three
 column ranges (first, middle and last tile columns, every row) with the bound
@@ -92,10 +94,11 @@ def test_wide_interior(resident, oracle_mod, ops):
 
 @pytest.mark.parametrize("ops", OPS, ids=OP_IDS)
 def test_wide_edges_alpha_beta(resident, oracle_mod, ops):
-    """4000 x 3950 x 1001: edge tiles on both sides and a partial last K stage
-    (16 x 16 tiles: one round, so the launch stays whole on this kernel rather
-    than taking an edge split)."""
-    m, n, k = 4000, 3950, 1001
+    """4000 x 3950 x 501: edge tiles on both sides and a partial last K stage
+    (16 x 16 tiles: one round, no edge split; K rounded down to a multiple of 4
+    or 8 is below 512, so no K remainder: the launch stays whole on this
+    kernel)."""
+    m, n, k = 4000, 3950, 501
     prob = Problem(uniform(oracle_mod, m, k, 1201), uniform(oracle_mod, k, n, 1202),
                    uniform(oracle_mod, m, n, 1203), op_a=ops[0], op_b=ops[1],
                    alpha=-1.25, beta=0.75)
@@ -137,12 +140,13 @@ def test_ring_k_tails_pattern(resident, oracle_mod, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(4096, 4096, 1001), (4000, 4096, 1040), (4096, 4000, 1040)],
-                         ids=["k%4", "m%256", "n%256"])
+                         ids=["k%4-wide", "m%256-edge", "n%256-edge"])
 def test_ring_fallback_shapes_pattern(resident, oracle_mod, m, n, k):
-    """N/T launches just outside the barrier-free kernel's conditions (K not a
-    multiple of 4, or m or n not a multiple of 256, in one round of 16 x 16
-    tiles, which no edge split or K remainder would speed up) run
-    sgemm_wide_kernel: bit-exact pattern."""
+    """N/T launches just outside the interior barrier-free kernel's conditions:
+    K not a multiple of 4 (one round of interior tiles, which neither a tail
+    split nor a K remainder would speed up: sgemm_wide_kernel), or m or n not a
+    multiple of 256 (one round of 16 x 16 tiles, which no edge split would
+    speed up: the ring kernel's edge instance). Bit-exact pattern."""
     a_op, b_op = pattern_operands(m, n, k)
     prob = Problem(a_op, b_op, op_b=abi.OP_T)
     out = prob.run(resident)
@@ -182,11 +186,11 @@ def test_ring8_alpha_beta(resident, oracle_mod, ops):
 
 
 @pytest.mark.parametrize("ops,m,k", [(OPS[0], 4096, 1004), (OPS[2], 4000, 1040), (OPS[3], 4096, 1020)],
-                         ids=["NN-k%8", "TN-m%256", "TT-k%8"])
+                         ids=["NN-k%8-wide", "TN-m%256-edge", "TT-k%8-wide"])
 def test_ring8_fallback_shapes_pattern(resident, oracle_mod, ops, m, k):
-    """Launches just outside that kernel's conditions (K not a multiple of 8,
-    m not a multiple of 256; one round of 16 x 16 tiles) run sgemm_wide_kernel:
-    bit-exact pattern."""
+    """Launches just outside that kernel's interior conditions in one round of
+    16 x 16 tiles: K not a multiple of 8 (sgemm_wide_kernel) or m not a
+    multiple of 256 (its edge instance). Bit-exact pattern."""
     n = 4096
     a_op, b_op = pattern_operands(m, n, k)
     prob = Problem(a_op, b_op, op_a=ops[0], op_b=ops[1])

@@ -411,18 +411,29 @@ def edge_rule(lib):
 
 
 @pytest.mark.parametrize("m,n,k,nt,expect", [
-    # 20 x 20 tiles, ragged: interior 19 x 19 (tail split) and two strips, which split
+    # ragged, a last round that would fill few CUs: the interior (20 x 20 tiles: 19 x 19 with
+    # a tail split) and two strips, which split
     (5000, 5000, 5000, True, (1, 1)),
-    (8191, 8191, 2048, True, (1, 1)),
+    (7000, 7000, 7000, False, (1, 1)),
     (4100, 4100, 1024, False, (1, 1)),
-    # one full round already: the strips' cost outweighs the edge tiles'
+    (4100, 4100, 240, False, (1, 1)),
+    (5000, 5000, 2048, False, (1, 1)),
+    (6312, 6275, 2176, False, (1, 1)),
+    # whole rounds (nearly) full: the whole launch on the ring kernels' edge instances
+    (8191, 8191, 2048, True, (0, 0)),
+    (8191, 8191, 8192, False, (0, 0)),
+    (8100, 8100, 4096, False, (0, 0)),
     (4000, 4000, 12000, True, (0, 0)),
-    # K not a multiple of 8 (N/N; N/T takes it), fewer than 256 tiles, interior, too shallow
+    (4001, 3999, 1024, False, (0, 0)),
+    (4001, 4093, 2048, True, (0, 0)),
+    (3900, 4096, 1000, False, (0, 0)),
+    (6981, 4328, 3928, True, (0, 0)),
+    (11500, 11000, 1024, False, (0, 0)),
+    # K not a multiple of 8 (N/N; N/T takes it), fewer than 256 tiles, interior
     (4500, 4500, 4500, False, (0, 0)),
     (4500, 4500, 4500, True, (1, 1)),
     (2000, 2000, 2000, True, (0, 0)),
     (4096, 4096, 4096, True, (0, 0)),
-    (4100, 4100, 240, False, (0, 0)),
 ])
 def test_edge_split_rule(sim, m, n, k, nt, expect):
     assert edge_rule(sim)(m, n, k, nt) == expect
@@ -454,7 +465,14 @@ def test_edge_split_pattern_is_exact(sim, oracle_mod):
     (5000, 5000, 4100, True, 0),
     # interior 17 x 17 tiles, K % 8 = 3: the rounded K takes a tail split
     (4352, 4352, 4099, False, 4096),
-    # the rounded K would gain nothing (whole rounds), too shallow, or fewer than 256 tiles
+    # ragged tiles, whole rounds full: the rounded K runs whole on the ring kernels' edge
+    # instances instead of the general kernel's predicated edge tiles
+    (8191, 8191, 8190, False, 8184),
+    (8191, 8191, 8190, True, 8188),
+    (4001, 3999, 1030, False, 1024),
+    (4001, 3999, 1030, True, 1028),
+    # interior tiles in whole rounds (the general kernel's interior loop), too shallow, or
+    # fewer than 256 tiles
     (4096, 4096, 4099, False, 0),
     (5000, 5000, 507, False, 0),
     (3001, 2047, 4099, False, 0),

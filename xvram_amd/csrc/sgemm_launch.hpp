@@ -291,41 +291,41 @@ inline uint64_t split_k_bytes_wanted_whole(const SgemmLaunch& l) {
 }
 
 // Edge split. A launch whose m or n is not a multiple of 256 and that has at
-// least kComputeUnits tiles of 256 x 256 runs every tile on the general 256 x
-// 256 kernel, whose ragged edge tiles take its predicated loop (5000^3: 2.70-
-// 2.76 ms, 91 TFLOP/s). It may run instead as up to three launches of its own,
-// one after another on its stream: the interior rows [0, mi) x columns
-// [0, ni) (mi, ni = m, n rounded down to 256; ring kernels, or their tail
-// split), the right strip rows [0, mi) x columns [ni, n) and the bottom strip
-// rows [mi, m) x columns [0, n), each split by the rules above (the strips on
-// the 256 x 128 kernel), sharing the workspace. Every element of C is computed
-// by one of them. Taken when a model rates it faster, in units of K of one
-// round: the whole launch takes its rounds x K x 5/4 (the edge tiles' cost,
-// measured 1.16-1.5 on six shapes); the split takes the interior's time
-// (tail_split_timed, one round for fewer than kComputeUnits tiles), plus the
-// strips' 256 x 128 tiles x K x 3.5 / 512 (their split launches, reductions
-// and mostly empty tiles, measured on 4000 x 4000 x 12000 and 8191 x 8191 x
-// 2048), plus 280 for the two extra launches. The model's times came within
-// 6 % of the split launches measured on 4100^2 x 4096, 5000^3, 7000^3 and
-// 10000^2 x 4000.
+// least kComputeUnits tiles of 256 x 256 runs every tile on the ring kernels'
+// edge instances (K a multiple of 4 for N/T, of 8 for the other forms), whose
+// K loop is the interior one: rounds x (K x 26/25 + 50) in units of K of one
+// round, within 4 % of 17 shapes measured. Its last round may fill few CUs. It
+// may run instead as up to three launches of its own, one after another on
+// its stream: the interior rows [0, mi) x columns [0, ni) (mi, ni = m, n
+// rounded down to 256; ring kernels, or their tail split), the right strip
+// rows [0, mi) x columns [ni, n) and the bottom strip rows [mi, m) x columns
+// [0, n), each split by the rules above (the strips on the 256 x 128 kernel),
+// sharing the workspace. Every element of C is computed by one of them. The
+// split is modelled as the interior's time (tail_split_timed, one round for
+// fewer than kComputeUnits tiles), plus the strips' 256 x 128 tiles x K x
+// 2.7 over the 256 x 128 kernel's 512 slots (their split launches' first
+// loads, partial stores and reductions, and mostly empty tiles: least squares
+// over 20 shapes), plus 150 for the two extra launches, and taken when it
+// models faster. On 22 shapes from 4100^2 x 240 to 11500 x 11000 x 1024 the
+// model's split / whole ratio came within 7 % of the measured one and picked
+// the faster plan every time (split 4100^2 x 4096 1.74x, 7000^3 1.31x, 5000^2
+// x 2048 1.09x; whole 8191^2 x 8192 1.17x, 8100^2 x 4096 1.15x, 8000^3 1.07x).
 // Only for one-panel launches with K a multiple of 4 (N/T) or 8 (the other
-// forms), so that the interior runs on the ring kernels (with K ragged the
-// general kernel's interior tiles gain nothing: 6000 x 6000 x 6002 ran 1-3 %
-// slower split), and panels below 2^31 bytes; when a part would split, only
-// with a workspace (a strip unsplit would leave most CUs idle).
+// forms), and panels below 2^31 bytes; when a part would split, only with a
+// workspace (a strip unsplit would leave most CUs idle).
 inline bool edge_split_rated_faster(int64_t m, int64_t n, int64_t k, bool nt) {
   if (m <= 0 || n <= 0 || k <= 0 || k % (nt ? 4 : 8) != 0) return false;
   const int64_t mi = m / 256 * 256, ni = n / 256 * 256;
   const int64_t whole_tiles = ((m + 255) / 256) * ((n + 255) / 256);
   if ((mi == m && ni == n) || whole_tiles < kComputeUnits || mi == 0 || ni == 0) return false;
-  const int64_t whole = cu_rounds(whole_tiles) * k * 5 / 4;
+  const int64_t whole = cu_rounds(whole_tiles) * (k * 26 / 25 + 50);
   const int64_t interior_tiles = (mi / 256) * (ni / 256);
   int64_t interior = cu_rounds(interior_tiles) * k;
   if (interior_tiles >= kComputeUnits) tail_split_timed(mi, ni, k, ~uint64_t{0}, &interior);
   // The strips' 256 x 128 tiles (the bottom strip's one row of them, the
   // right strip's column of them).
   const int64_t strip_tiles = (m > mi ? (n + 127) / 128 : 0) + (mi / 256) * ((n - ni + 127) / 128);
-  const int64_t split = interior + 7 * k * strip_tiles / (4 * kComputeUnits) + 280;
+  const int64_t split = interior + 27 * k * strip_tiles / (20 * kComputeUnits) + 150;
   return split < whole;
 }
 
@@ -393,21 +393,24 @@ inline bool edge_split_wants_workspace(int64_t m, int64_t n, int64_t k, bool nt)
 }
 
 // K remainder. The ring kernels need K a multiple of 4 (N/T) or 8 (the other
-// forms), and so do the tail and edge splits. A launch whose K is not, and
-// whose K rounded down to that multiple (at least 512) would take a tail or
-// an edge split, runs as two launches of its own: the first over the rounded
-// K with alpha and beta and no epilogue, the second over the remaining 1 to 7
-// K rows with alpha and beta 1 onto the first's result, then the epilogue
-// (one more read and write of C: 4500^3 N/N, 2.30 ms as one launch on the
-// general kernel, gains far more from the split first part). Returns the
-// rounded K (0: no K remainder).
+// forms), and so do the tail and edge splits. A launch whose K is not, whose
+// K rounded down to that multiple is at least 512, and which either has
+// interior tiles and would take a tail split over the rounded K, or has
+// ragged tiles, at least kComputeUnits of them (the rounded K then runs on
+// the ring kernels' edge instances or takes an edge split, not the general
+// kernel's predicated edge tiles), runs as two launches of its own: the first
+// over the rounded K with alpha and beta and no epilogue, the second over the
+// remaining 1 to 7 K rows with alpha and beta 1 onto the first's result, then
+// the epilogue (one more read and write of C: 4500^3 N/N, 2.30 ms as one
+// launch on the general kernel, gains far more from the split first part).
+// Returns the rounded K (0: no K remainder).
 inline int64_t k_remainder_shape(int64_t m, int64_t n, int64_t k, bool nt) {
   if (m <= 0 || n <= 0 || k <= 0) return 0;
   const int64_t k1 = k - k % (nt ? 4 : 8);
   if (k1 == k || k1 < 512) return 0;
   const bool interior = m % 256 == 0 && n % 256 == 0;
   const bool gains = interior ? tail_split_shape(m, n, k1, nt, true, ~uint64_t{0}).head_m > 0
-                              : edge_split_rated_faster(m, n, k1, nt);
+                              : ((m + 255) / 256) * ((n + 255) / 256) >= kComputeUnits;
   return gains ? k1 : 0;
 }
 

@@ -375,10 +375,16 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_wide_kernel(Params p) {
 // have completed. Loads complete in order, so before reading pair q+1 the wave
 // waits until at most the loads of pairs q+2 .. q+kAhead-1 are outstanding.
 //
-// Used only for launches whose tiles are all interior (m and n multiples of
-// 256) and whose K is a multiple of 4: every load then stays inside the tile's
-// rows and columns and inside the K extent (the last load of the last pair ends
-// at or before the panel's record count), so no predication is needed.
+// K must be a multiple of 4. In the instances for interior tiles (m and n
+// multiples of 256) every load stays inside the tile's rows and columns and
+// inside the K extent (the last load of the last pair ends at or before the
+// panel's record count), so no predication is needed. Edge instance (kEdge,
+// one panel, unsplit): a tile may reach past row m or column n. A lane whose
+// four elements would start past the operand's last whole float4 (rows up to
+// m rounded up to 4, which the leading dimension covers) loads that float4
+// instead; the copies feed only rows or columns of C past m or n, which the
+// predicated store leaves alone. The loads of a lane keep one offset over
+// the whole K loop, so the K loop is the interior one.
 //
 // Two-panel instance (kTwo): the launch's K rows come from two separately
 // stored panels with the same leading dimensions, [0, k_split) from a / b and
@@ -407,9 +413,21 @@ struct RingSource {
   int rotate = 0; // sgemm_ring8_kernel: slot loaded first (< count)
 };
 
-template <bool kTwo, bool kSplit>
+// First element of a lane's float4 in an extent-contiguous operand half:
+// element w + 4*lrow of the tile, or, for an edge tile with `extent` elements
+// left in the operand, at most the last whole float4 below extent rounded up
+// to 4 (extent >= 1).
+template <bool kEdge>
+__device__ __forceinline__ int lane_elem(int w, int lrow, int extent) {
+  const int e = w + 4 * lrow;
+  if constexpr (kEdge) return min(e, ((extent + 3) & ~3) - 4);
+  else return e;
+}
+
+template <bool kTwo, bool kSplit, bool kEdge>
 __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
   static_assert(!(kTwo && kSplit), "a two-panel launch never splits");
+  static_assert(!(kEdge && (kTwo || kSplit)), "edge tiles run one-panel, unsplit launches");
   __shared__ __attribute__((aligned(16))) float lds[4 * kRing * kSlot];
   asm volatile("; accumulators in AGPRs" ::: "a0");
 
@@ -457,11 +475,13 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
   // Load h of a pair: lane l brings k-row 2h + l/32 of the pair, elements
   // 4*(l%32) .. +3 of the wave's half; it lands at LDS byte 1024*h + 16*l of
   // the operand's part of the slot, i.e. row-major 4 x 128.
+  const int ea = lane_elem<kEdge>(wm, lrow, p.m - m0);
+  const int eb = lane_elem<kEdge>(wn, lrow, p.n - n0);
   uint32_t vo_a[2], vo_b[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    vo_a[h] = (uint32_t)(((int64_t)(2 * h + lhalf) * p.lda + wm + 4 * lrow) * 4);
-    vo_b[h] = (uint32_t)(((int64_t)(2 * h + lhalf) * p.ldb + wn + 4 * lrow) * 4);
+    vo_a[h] = (uint32_t)(((int64_t)(2 * h + lhalf) * p.lda + ea) * 4);
+    vo_b[h] = (uint32_t)(((int64_t)(2 * h + lhalf) * p.ldb + eb) * 4);
   }
   const uint32_t pair_a = (uint32_t)(16 * p.lda);
   const uint32_t pair_b = (uint32_t)(16 * p.ldb);
@@ -580,10 +600,11 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
     }(std::make_integer_sequence<int, kRing>{});
   }
 
-  // Every tile is interior: two columns of C per batch of loads. A split
-  // launch stores its range's raw sums instead.
+  // Interior tiles: two columns of C per batch of loads. A split launch
+  // stores its range's raw sums instead. Edge tiles: only elements of C.
   const Params out = kSplit ? partial_target(p, split) : p;
-  store_c_interior<4, 2, true>(out, acc, m0 + wm, n0 + wn, lrow, lhalf);
+  if constexpr (kEdge) store_c_tile<4, false>(out, acc, m0 + wm, n0 + wn, lrow, lhalf);
+  else store_c_interior<4, 2, true>(out, acc, m0 + wm, n0 + wn, lrow, lhalf);
 }
 
 // ---- barrier-free kernel for layouts with a k-contiguous operand ------------
@@ -613,9 +634,13 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring_kernel(Params p) {
 // next block, so with k_split a multiple of 8 * kRing8 (two-panel instance,
 // as in sgemm_ring_kernel) each block's loads come from one K panel.
 //
-// Used only for launches whose tiles are all interior (m and n multiples of
-// 256) and whose K is a multiple of 8: every load then stays inside the
-// tile's lines and the K extent, so no predication is needed.
+// K must be a multiple of 8. In the instances for interior tiles (m and n
+// multiples of 256) every load stays inside the tile's lines and the K
+// extent, so no predication is needed. Edge instance (kEdge, one panel,
+// unsplit): an extent-contiguous half clamps its lanes' elements as
+// sgemm_ring_kernel does, a k-contiguous half its lines to the operand's last
+// line (m - 1 or n - 1), and that half's descriptor ends after the last line;
+// the copies feed only rows or columns of C that the predicated store skips.
 constexpr int kRing8 = 4;       // slots per wave
 constexpr int kSlotK = 8;       // k values per slot
 constexpr int kHalf8 = 1024;    // floats of one operand half per slot (128 x 8)
@@ -641,9 +666,10 @@ __device__ __forceinline__ void wait_slots(int after) {
   else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template <bool kAKC, bool kBKC, bool kTwo, bool kSplit>
+template <bool kAKC, bool kBKC, bool kTwo, bool kSplit, bool kEdge>
 __global__ __launch_bounds__(kThreads, 1) void sgemm_ring8_kernel(Params p) {
   static_assert(!(kTwo && kSplit), "a two-panel launch never splits");
+  static_assert(!(kEdge && (kTwo || kSplit)), "edge tiles run one-panel, unsplit launches");
   __shared__ __attribute__((aligned(16))) float lds[4 * kRing8 * 2 * kHalf8];
   asm volatile("; accumulators in AGPRs" ::: "a0");
 
@@ -679,8 +705,12 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring8_kernel(Params p) {
   // X(e, k) = x[e + k*ld] spans (kk*ld - e0) floats from x + e0 (to the end of
   // k-row kk-1), a k-contiguous X(e, k) = x[k + e*ld] spans 255*ld + kk
   // floats from x + e0*ld (the tile's 256 lines, kk values each).
-  const auto rsrc = [](const float* x, int64_t ld, int e0, int kk, bool kc) {
-    return kc ? panel_rsrc(x + (int64_t)e0 * ld, (uint32_t)((255 * ld + kk) * 4))
+  // Edge tiles: a k-contiguous panel ends after its last line (`lines` of
+  // the tile's 256 lie inside the operand).
+  const int a_lines = kEdge ? min(kTile, p.m - m0) : kTile;
+  const int b_lines = kEdge ? min(kTile, p.n - n0) : kTile;
+  const auto rsrc = [](const float* x, int64_t ld, int e0, int kk, bool kc, int lines) {
+    return kc ? panel_rsrc(x + (int64_t)e0 * ld, (uint32_t)(((lines - 1) * ld + kk) * 4))
               : panel_rsrc(x + e0, (uint32_t)(((int64_t)kk * ld - e0) * 4));
   };
   // Rotated K order (op-T A): the tile row's slots are visited from slot
@@ -693,28 +723,32 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring8_kernel(Params p) {
   // kTurnSlots slots of one another. Each tile sums its slots in one fixed
   // order.
   const int turn = kAKC ? (tile_m % kTurnClasses) * kTurnSlots : 0;
-  RingSource lo{rsrc(p.a, p.lda, m0, k1, kAKC), rsrc(p.b, p.ldb, n0, k1, kBKC), 0};
+  RingSource lo{rsrc(p.a, p.lda, m0, k1, kAKC, a_lines), rsrc(p.b, p.ldb, n0, k1, kBKC, b_lines), 0};
   lo.count = kTwo ? q_split : slots;
   lo.rotate = turn % lo.count;
   RingSource hi = lo;
   if constexpr (kTwo) {
     const int k2 = p.k - k1;
-    hi = RingSource{rsrc(p.a2, p.lda, m0, k2, kAKC), rsrc(p.b2, p.ldb, n0, k2, kBKC), q_split};
+    hi = RingSource{rsrc(p.a2, p.lda, m0, k2, kAKC, a_lines), rsrc(p.b2, p.ldb, n0, k2, kBKC, b_lines),
+                    q_split};
     hi.count = slots - q_split;
     hi.rotate = turn % hi.count;
   }
   // Lane offsets of load I of a half in its panel's first slot: k-row 2I + h,
   // elements w + 4*lrow .. +3 (extent-contiguous), or line w + 4*lrow + I, k
   // values 4h .. 4h+3 (k-contiguous). A slot advances K by 8 rows / values.
-  const auto voff = [&](int64_t ld, int w, int i, bool kc) {
-    return kc ? (uint32_t)(((int64_t)(w + 4 * lrow + i) * ld + 4 * lhalf) * 4)
-              : (uint32_t)(((int64_t)(2 * i + lhalf) * ld + w + 4 * lrow) * 4);
+  // Edge tiles: elements and lines clamped to the operand (`lines` inside).
+  const auto voff = [&](int64_t ld, int w, int i, bool kc, int lines) {
+    int line = w + 4 * lrow + i;
+    if constexpr (kEdge) line = min(line, lines - 1);
+    return kc ? (uint32_t)(((int64_t)line * ld + 4 * lhalf) * 4)
+              : (uint32_t)(((int64_t)(2 * i + lhalf) * ld + lane_elem<kEdge>(w, lrow, lines)) * 4);
   };
   uint32_t vo_a[4], vo_b[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    vo_a[i] = voff(p.lda, wm, i, kAKC);
-    vo_b[i] = voff(p.ldb, wn, i, kBKC);
+    vo_a[i] = voff(p.lda, wm, i, kAKC, a_lines);
+    vo_b[i] = voff(p.ldb, wn, i, kBKC, b_lines);
   }
   const uint32_t adv_a = kAKC ? kSlotK * 4 : (uint32_t)(kSlotK * 4 * p.lda);
   const uint32_t adv_b = kBKC ? kSlotK * 4 : (uint32_t)(kSlotK * 4 * p.ldb);
@@ -837,7 +871,8 @@ __global__ __launch_bounds__(kThreads, 1) void sgemm_ring8_kernel(Params p) {
   int lane_e;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_e));
   const Params out = kSplit ? partial_target(p, split) : p;
-  store_c_interior<4, 2, true>(out, acc, m0 + wm, n0 + wn, lane_e & 31, lane_e >> 5);
+  if constexpr (kEdge) store_c_tile<4, false>(out, acc, m0 + wm, n0 + wn, lane_e & 31, lane_e >> 5);
+  else store_c_interior<4, 2, true>(out, acc, m0 + wm, n0 + wn, lane_e & 31, lane_e >> 5);
 }
 
 // ---- split-K reduction --------------------------------------------------------
@@ -900,61 +935,87 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(Params p) {
 }
 
 // A launch of K below 8 (a K remainder's last rows): too little work for the
-// MFMA tiles, whose prologue and C round trip it would pay in full, so each
-// thread forms four rows of one column of the product with FP32
-// multiply-adds in K order and applies the tile epilogue's arithmetic
+// MFMA tiles, whose prologue and C round trip it would pay in full. Each
+// workgroup takes 4 * kThreads rows of C and kThinCols of its columns; each
+// thread reads its four rows of the K columns of op(A) once into registers
+// (an op-T A's rows are lines, read value by value) and then, column by
+// column, forms the four sums with FP32 multiply-adds in K order (B(q, col)
+// is the same for every lane) and applies the tile epilogue's arithmetic
 // (alpha, beta, bias, ReLU), reading and writing C as 16-byte vectors.
 // HBM-bound: about 8 bytes of C per element.
+constexpr int kThinCols = 16;
+
 template <bool AK, bool BN>
 __global__ __launch_bounds__(kThreads) void thin_k_kernel(Params p) {
-  const int64_t per_col = ((int64_t)p.m + 3) / 4;
-  const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (idx >= per_col * p.n) return;
-  const int col = (int)(idx / per_col);
-  const int row = (int)(idx - (int64_t)col * per_col) * 4;
+  constexpr int kMaxK = 7;
+  const int row_blocks = (p.m + 4 * kThreads - 1) / (4 * kThreads);
+  const int block_row = (int)(blockIdx.x % (unsigned)row_blocks);
+  const int col0 = (int)(blockIdx.x / (unsigned)row_blocks) * kThinCols;
+  const int row = block_row * 4 * kThreads + 4 * (int)threadIdx.x;
+  if (row >= p.m) return;
   const int rows = min(4, p.m - row);
-  float sum[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int q = 0; q < p.k; ++q) {
-    const float y = BN ? p.b[col + (int64_t)q * p.ldb] : p.b[q + (int64_t)col * p.ldb];
-    if (!AK && rows == 4) {
-      const float4 x = *reinterpret_cast<const float4*>(p.a + row + (int64_t)q * p.lda);
-      sum[0] += x.x * y;
-      sum[1] += x.y * y;
-      sum[2] += x.z * y;
-      sum[3] += x.w * y;
-    } else {
-      for (int t = 0; t < rows; ++t)
-        sum[t] += (AK ? p.a[q + (int64_t)(row + t) * p.lda] : p.a[row + t + (int64_t)q * p.lda]) * y;
-    }
-  }
-  float* cp = p.c + (int64_t)col * p.ldc + row;
-  const bool extra = p.bias_row != nullptr || p.bias_col != nullptr || p.relu != 0;
-  const float bias_c = p.bias_col != nullptr ? p.bias_col[col] : 0.f;
-  const auto finish = [&](float v, int r) {
-    if (p.bias_row != nullptr) v += p.bias_row[r];
-    v += bias_c;
-    return (p.relu != 0 && v < 0.f) ? 0.f : v;
-  };
-  if (rows == 4) {
-    float r[4] = {p.alpha * sum[0], p.alpha * sum[1], p.alpha * sum[2], p.alpha * sum[3]};
-    if (p.beta != 0.f) {
-      const float4 old = *reinterpret_cast<const float4*>(cp);
-      r[0] = p.alpha * sum[0] + p.beta * old.x;
-      r[1] = p.alpha * sum[1] + p.beta * old.y;
-      r[2] = p.alpha * sum[2] + p.beta * old.z;
-      r[3] = p.alpha * sum[3] + p.beta * old.w;
-    }
-    if (extra) {
+  float x[kMaxK][4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) r[t] = finish(r[t], row + t);
+  for (int q = 0; q < kMaxK; ++q) {
+    if (q < p.k) {
+      if (!AK && rows == 4) {
+        const float4 v = *reinterpret_cast<const float4*>(p.a + row + (int64_t)q * p.lda);
+        x[q][0] = v.x;
+        x[q][1] = v.y;
+        x[q][2] = v.z;
+        x[q][3] = v.w;
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          x[q][t] = t < rows ? (AK ? p.a[q + (int64_t)(row + t) * p.lda] : p.a[row + t + (int64_t)q * p.lda])
+                             : 0.f;
+      }
     }
-    *reinterpret_cast<float4*>(cp) = make_float4(r[0], r[1], r[2], r[3]);
-    return;
   }
-  for (int t = 0; t < rows; ++t) {
-    const float val = p.alpha * sum[t];
-    const float out = p.beta != 0.f ? val + p.beta * cp[t] : val;
-    cp[t] = extra ? finish(out, row + t) : out;
+  const bool extra = p.bias_row != nullptr || p.bias_col != nullptr || p.relu != 0;
+  float brow[4] = {0.f, 0.f, 0.f, 0.f};
+  if (p.bias_row != nullptr)
+    for (int t = 0; t < rows; ++t) brow[t] = p.bias_row[row + t];
+  const int cols = min(kThinCols, p.n - col0);
+  for (int j = 0; j < cols; ++j) {
+    const int col = col0 + j;
+    float sum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < kMaxK; ++q) {
+      if (q < p.k) {
+        const float y = BN ? p.b[col + (int64_t)q * p.ldb] : p.b[q + (int64_t)col * p.ldb];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) sum[t] += x[q][t] * y;
+      }
+    }
+    float* cp = p.c + (int64_t)col * p.ldc + row;
+    const float bias_c = p.bias_col != nullptr ? p.bias_col[col] : 0.f;
+    const auto finish = [&](float v, int t) {
+      if (p.bias_row != nullptr) v += brow[t];
+      v += bias_c;
+      return (p.relu != 0 && v < 0.f) ? 0.f : v;
+    };
+    if (rows == 4) {
+      float r[4] = {p.alpha * sum[0], p.alpha * sum[1], p.alpha * sum[2], p.alpha * sum[3]};
+      if (p.beta != 0.f) {
+        const float4 old = *reinterpret_cast<const float4*>(cp);
+        r[0] = p.alpha * sum[0] + p.beta * old.x;
+        r[1] = p.alpha * sum[1] + p.beta * old.y;
+        r[2] = p.alpha * sum[2] + p.beta * old.z;
+        r[3] = p.alpha * sum[3] + p.beta * old.w;
+      }
+      if (extra) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) r[t] = finish(r[t], t);
+      }
+      *reinterpret_cast<float4*>(cp) = make_float4(r[0], r[1], r[2], r[3]);
+    } else {
+      for (int t = 0; t < rows; ++t) {
+        const float val = p.alpha * sum[t];
+        const float out = p.beta != 0.f ? val + p.beta * cp[t] : val;
+        cp[t] = extra ? finish(out, t) : out;
+      }
+    }
   }
 }
 
@@ -976,8 +1037,9 @@ hipError_t launch_splitk_reduce(const Params& p, hipStream_t stream, hipEvent_t 
 // recorded by the dispatch.
 hipError_t launch_thin_k(const Params& p, bool a_kcontig, bool b_ncontig, hipStream_t stream,
                          hipEvent_t start, hipEvent_t stop) {
-  const int64_t quads = (((int64_t)p.m + 3) / 4) * p.n;
-  const dim3 grid(static_cast<unsigned>((quads + kThreads - 1) / kThreads)), block(kThreads);
+  const int64_t row_blocks = ((int64_t)p.m + 4 * kThreads - 1) / (4 * kThreads);
+  const int64_t col_groups = ((int64_t)p.n + kThinCols - 1) / kThinCols;
+  const dim3 grid(static_cast<unsigned>(row_blocks * col_groups)), block(kThreads);
   if (!a_kcontig && !b_ncontig)
     hipExtLaunchKernelGGL((thin_k_kernel<false, false>), grid, block, 0, stream, start, stop, 0, p);
   else if (!a_kcontig && b_ncontig)
@@ -990,11 +1052,11 @@ hipError_t launch_thin_k(const Params& p, bool a_kcontig, bool b_ncontig, hipStr
 }
 
 // Launches a 256 x 256 kernel for `p` (tiles_m / tiles_n already in 256s):
-// for launches of interior tiles only, sgemm_ring_kernel (N/T, K a multiple
-// of 4) or sgemm_ring8_kernel (the other forms, K a multiple of 8), their
-// two-panel instance when p.a2 is set (the caller has checked that launch's
-// contract); else sgemm_wide_kernel. start / stop (optional) are recorded by
-// the dispatch itself.
+// sgemm_ring_kernel (N/T, K a multiple of 4) or sgemm_ring8_kernel (the other
+// forms, K a multiple of 8) -- for launches of interior tiles their interior
+// instances, or the two-panel ones when p.a2 is set (the caller has checked
+// that launch's contract), else their edge instances; sgemm_wide_kernel for
+// other K. start / stop (optional) are recorded by the dispatch itself.
 hipError_t launch_wide(const Params& p, bool a_kcontig, bool b_ncontig, hipStream_t stream,
                        hipEvent_t start, hipEvent_t stop) {
   const dim3 block(kThreads);
@@ -1004,13 +1066,13 @@ hipError_t launch_wide(const Params& p, bool a_kcontig, bool b_ncontig, hipStrea
     // start event rides on the first dispatch, the stop event on the second.
     const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n * p.splits));
     if (!a_kcontig && b_ncontig)
-      hipExtLaunchKernelGGL((sgemm_ring_kernel<false, true>), grid, block, 0, stream, start, nullptr, 0, p);
+      hipExtLaunchKernelGGL((sgemm_ring_kernel<false, true, false>), grid, block, 0, stream, start, nullptr, 0, p);
     else if (!a_kcontig && !b_ncontig)
-      hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, false, true>), grid, block, 0, stream, start, nullptr, 0, p);
+      hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, false, true, false>), grid, block, 0, stream, start, nullptr, 0, p);
     else if (a_kcontig && !b_ncontig)
-      hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, false, true>), grid, block, 0, stream, start, nullptr, 0, p);
+      hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, false, true, false>), grid, block, 0, stream, start, nullptr, 0, p);
     else
-      hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, false, true>), grid, block, 0, stream, start, nullptr, 0, p);
+      hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, false, true, false>), grid, block, 0, stream, start, nullptr, 0, p);
     if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     return launch_splitk_reduce(p, stream, stop);
   }
@@ -1018,20 +1080,30 @@ hipError_t launch_wide(const Params& p, bool a_kcontig, bool b_ncontig, hipStrea
   const bool interior = p.m % kTile == 0 && p.n % kTile == 0;
   if (interior && !a_kcontig && b_ncontig && p.k % 4 == 0) {
     if (p.a2 != nullptr)
-      hipExtLaunchKernelGGL((sgemm_ring_kernel<true, false>), grid, block, 0, stream, start, stop, 0, p);
+      hipExtLaunchKernelGGL((sgemm_ring_kernel<true, false, false>), grid, block, 0, stream, start, stop, 0, p);
     else
-      hipExtLaunchKernelGGL((sgemm_ring_kernel<false, false>), grid, block, 0, stream, start, stop, 0, p);
+      hipExtLaunchKernelGGL((sgemm_ring_kernel<false, false, false>), grid, block, 0, stream, start, stop, 0, p);
   } else if (interior && p.k % kSlotK == 0) {
     const bool two = p.a2 != nullptr;
     if (!a_kcontig && !b_ncontig)
-      two ? hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, true, false>), grid, block, 0, stream, start, stop, 0, p)
-          : hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, false, false>), grid, block, 0, stream, start, stop, 0, p);
+      two ? hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, true, false, false>), grid, block, 0, stream, start, stop, 0, p)
+          : hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, false, false, false>), grid, block, 0, stream, start, stop, 0, p);
     else if (a_kcontig && !b_ncontig)
-      two ? hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, true, false>), grid, block, 0, stream, start, stop, 0, p)
-          : hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, false, false>), grid, block, 0, stream, start, stop, 0, p);
+      two ? hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, true, false, false>), grid, block, 0, stream, start, stop, 0, p)
+          : hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, false, false, false>), grid, block, 0, stream, start, stop, 0, p);
     else
-      two ? hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, true, false>), grid, block, 0, stream, start, stop, 0, p)
-          : hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, false, false>), grid, block, 0, stream, start, stop, 0, p);
+      two ? hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, true, false, false>), grid, block, 0, stream, start, stop, 0, p)
+          : hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, false, false, false>), grid, block, 0, stream, start, stop, 0, p);
+  } else if (!a_kcontig && b_ncontig && p.k % 4 == 0) {
+    // Edge tiles (one panel: two-panel launches are interior).
+    hipExtLaunchKernelGGL((sgemm_ring_kernel<false, false, true>), grid, block, 0, stream, start, stop, 0, p);
+  } else if (p.k % kSlotK == 0) {
+    if (!a_kcontig && !b_ncontig)
+      hipExtLaunchKernelGGL((sgemm_ring8_kernel<false, true, false, false, true>), grid, block, 0, stream, start, stop, 0, p);
+    else if (a_kcontig && !b_ncontig)
+      hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, true, false, false, true>), grid, block, 0, stream, start, stop, 0, p);
+    else
+      hipExtLaunchKernelGGL((sgemm_ring8_kernel<true, false, false, false, true>), grid, block, 0, stream, start, stop, 0, p);
   } else if (!a_kcontig && !b_ncontig)
     hipExtLaunchKernelGGL((sgemm_wide_kernel<false, false>), grid, block, 0, stream, start, stop, 0, p);
   else if (!a_kcontig && b_ncontig)
