@@ -23,6 +23,12 @@ would show in C.
 * Thin-K launches (K = 1, 3 and 7; 1001 x 515: a partial row block and a
   partial group of columns), all four forms, alpha, beta, a per-column bias
   and ReLU: within the bound.
+* The other kernels under the same NaN padding, whose predicated loads take
+  out-of-range rows, columns and k as zeros in both operands (0 x NaN would
+  be NaN): the general 256 x 256 kernel on 4001 x 3999 x 501 (edge tiles and
+  a K tail; no K remainder below 512) and 4096^2 x 1001 (interior tiles, K
+  tail), and the 256 x 128 kernel's split on config 2 (3001 x 2047 x 4099),
+  all four forms: within the bound, no NaN.
 
 Tolerance: |C - C_ref| <= 4*K*2^-24*(|alpha||A||B| + |beta C0| + |bias|)_ij."""
 import ctypes
@@ -163,3 +169,12 @@ def test_thin_k_within_bound(lib, hip, oracle_mod, form, k):
     outs, ref, absab = run_gemm(lib, hip, oracle_mod, m, n, k, form, 921 + k, -1.5, 0.25,
                                 abi.BIAS_PER_COLUMN, True)
     check(oracle_mod, outs, k, ref, absab, f"thin {m}x{n}x{k} {form} bias col + ReLU")
+
+
+@pytest.mark.parametrize("m,n,k", [(4001, 3999, 501), (4096, 4096, 1001), (3001, 2047, 4099)],
+                         ids=["wide-edge", "wide-ktail", "narrow-split"])
+@pytest.mark.parametrize("form", sorted(FORMS))
+def test_other_kernels_ignore_nan_padding(lib, hip, oracle_mod, form, m, n, k):
+    outs, ref, absab = run_gemm(lib, hip, oracle_mod, m, n, k, form, 931, 1.5, 0.5,
+                                abi.BIAS_PER_COLUMN, False, repeat=1)
+    check(oracle_mod, outs, k, ref, absab, f"{m}x{n}x{k} {form} under NaN padding")
