@@ -103,7 +103,9 @@ typedef struct xvram_amd_device_info_v1 {
 /* One GEMM on device memory, column-major (see sgemm_device above). Every
    pointer is device memory of the stream's GPU, 16-byte aligned; leading
    dimensions are in floats, multiples of 4, at least the stored rows; each
-   operand buffer holds ld x (stored columns) floats. m, n, k in 1..2^31-1. */
+   operand buffer holds ld x (stored columns) floats. The padding rows (stored
+   rows .. ld - 1) may be read but hold any values, NaN included: none reaches
+   C. m, n, k in 1..2^31-1. */
 typedef struct xvram_amd_sgemm_v1 {
   uint32_t struct_size;
   uint32_t flags;
